@@ -1,0 +1,177 @@
+"""Benchmark of the fused LM-head logprob path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3] [--no-cpu-baseline]
+
+A step is one pass of the path over one packed micro-batch, inputs resident in HBM:
+  compaction of the scored rows -> fused forward (MFMA GEMM + softmax epilogue, merge, target gather)
+  -> GRPO weight g per flat token -> fused backward (recompute dz, grad_hidden and grad_W GEMMs, row
+  scatter, grad_W to bf16).
+Default workload cfg3: N = 32,768 packed tree tokens (an 8,192-token root shared by 12 branches of 2,048,
+root masked: 24,576 scored rows), d = 2560, V = 151,936, bf16, T = 1.0 (octopus_amd.workloads).
+Prints one JSON line: packed tokens/s, the MFMA roofline of the forward head kernel measured with HIP
+events, and the reference algorithm timed on the host CPU beside it.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s (AMD public spec)
+PEAK_F32 = 157.3e12
+PEAK_HBM = 8.0e12
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(cfg, scored_rows: int) -> dict:
+    """The reference algorithm on the host (oracle.baseline: CHUNK-row checkpointed chunks, bf16 GEMMs, fp32
+    softmax), timed on whole 2048-row chunks and scaled to the step's scored rows (chunks are independent)."""
+    from oracle import baseline
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    n_chunks = 1
+    r = baseline.time_chunks(cfg.d, cfg.V, n_chunks, cfg.temperature, repeats=1)
+    if r["seconds"] < 8.0:
+        r = baseline.time_chunks(cfg.d, cfg.V, n_chunks, cfg.temperature, repeats=3)
+    step_s = r["seconds"] * scored_rows / r["rows"]
+    return {"value": cfg.N / step_s, "unit": "tokens/s", "cores": r["threads"], "kind": "port",
+            "sample": f"{n_chunks} x 2048-row chunk fwd+bwd (bf16, d={cfg.d}, V={cfg.V}) timed "
+                      f"{r['seconds']:.2f} s (median), scaled x{scored_rows / r['rows']:.2f} to the step's "
+                      f"{scored_rows} scored rows; extrapolated; host: {_cpu_model()}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="cfg3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the LM-head path runs on a single MI355X here (no multi-GPU run)",
+              file=sys.stderr)
+        return 2
+
+    from octopus_amd import _lib, head_op
+    from octopus_amd.workloads import CONFIGS, make_batch
+
+    cfg = CONFIGS[args.workload]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _lib.load()
+    b = make_batch(cfg, dev)
+    h, W, y = b.hidden, b.weight, b.labels
+    inv_T = 1.0 / cfg.temperature
+    mask_f = b.scored.float()
+    need_w = cfg.backward == "full"
+
+    # untimed set-up: the rollout's ("old") logprobs = this policy's + N(0, 0.01)
+    idx, count = head_op.compact_rows(b.scored)
+    out, _ = head_op.head_fwd(h, W, b.w_scale, y, idx, count, inv_T, 1.0, 1.0, False, True, True)
+    old = (out[:, 0] + b.old_noise).contiguous()
+    scored_rows = int(count.item())
+    torch.cuda.synchronize()
+
+    def forward():
+        idx, count = head_op.compact_rows(b.scored)
+        out, lse = head_op.head_fwd(h, W, b.w_scale, y, idx, count, inv_T, 1.0, 1.0, False, True, True)
+        return idx, count, out, lse
+
+    def loss_grad(out):
+        return head_op.grpo_loss(out[:, 0], old, None, b.adv, mask_f, 0.2, 0.28, 5.0)
+
+    def backward(idx, count, lse, g_flat):
+        g = torch.empty(idx.numel(), dtype=torch.float32, device=dev)
+        _lib.call("octo_gather_f32", head_op._p(g_flat), 1, head_op._p(idx), head_op._p(count), idx.numel(),
+                  head_op._p(g), head_op._stream(g))
+        return head_op.head_bwd(h, W, b.w_scale, y, idx, count, lse, g, inv_T, 1.0, 1.0, False, True, True,
+                                need_w)
+
+    def step():
+        idx, count, out, lse = forward()
+        loss, g_flat = loss_grad(out)
+        return backward(idx, count, lse, g_flat)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+
+    # per-phase HIP-event timing on the launch stream (torch's current stream carries every launch)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    fwd_ms, bwd_ms, reps = [], [], 3
+    for _ in range(reps):
+        ev[0].record()
+        idx, count, out, lse = forward()
+        ev[1].record()
+        loss, g_flat = loss_grad(out)
+        ev[2].record()
+        backward(idx, count, lse, g_flat)
+        ev[3].record()
+        torch.cuda.synchronize()
+        fwd_ms.append(ev[0].elapsed_time(ev[1]))
+        bwd_ms.append(ev[2].elapsed_time(ev[3]))
+    fwd_ms = sorted(fwd_ms)[reps // 2]
+    bwd_ms = sorted(bwd_ms)[reps // 2]
+
+    n, d, V = scored_rows, cfg.d, cfg.V
+    alg_flop = {"full": 6, "hidden": 4, "none": 2}[cfg.backward] * n * d * V
+    exe_flop = {"full": 8, "hidden": 6, "none": 2}[cfg.backward] * n * d * V
+    peak = PEAK_BF16 if cfg.dtype != torch.float32 else PEAK_F32
+    step_s = ms / 1e3
+    fwd_flop = 2 * n * d * V
+    fwd_achieved = fwd_flop / (fwd_ms / 1e3)
+    result = {
+        "metric": "packed tokens/sec fwd+bwd logprob @ d=2560,V=151936 bf16; % MFMA peak",
+        "value": cfg.N / step_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.dtype == torch.bfloat16 else str(cfg.dtype).replace("torch.", ""),
+        "data": "synthetic (seeded: hidden N(0,1) RMS-normalised, W N(0,0.02), Zipf(1.1) targets)",
+        "config": {"workload": f"{cfg.name}: packed tree micro-batch, fused fwd+bwd GRPO logprob head",
+                   "N_packed": cfg.N, "scored_rows": n, "d": d, "V": V, "temperature": cfg.temperature,
+                   "backward": cfg.backward, "parallelism": "single GPU"},
+        "mfma_frac_algorithmic": alg_flop / step_s / peak,
+        "mfma_frac_executed": exe_flop / step_s / peak,
+        "phase_ms": {"forward": fwd_ms, "backward": bwd_ms},
+        "roofline": {"kernel": "gemm_stats_kernel (fused forward head: MFMA GEMM + softmax epilogue; the event "
+                               "bracket also holds its merge kernel and the compaction)",
+                     "bound": "mfma", "achieved": fwd_achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                     "frac": fwd_achieved / peak, "traffic": None,
+                     "per_launch": f"2*n*d*V = {fwd_flop:.4g} FLOP (n={n} scored rows)"},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(cfg, n)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,154 @@
+/*
+ * octo_head.h — C ABI of libocto_head.so, the gfx950 (MI355X) LM-head logprob path.
+ *
+ * The path: for packed, prefix-deduplicated hidden rows h_r (d wide), labels y_r and the vocabulary
+ * weight W [V, d], compute per row
+ *     z = post(h_r . W^T),  s = z / T,  lse = log sum_j exp(s_j),
+ *     logprob = s_y - lse,  entropy = lse - sum_j p_j s_j     (p = exp(s - lse), entropy detached)
+ * without ever writing the [rows, V] logits, and the backward of a loss L(logprob):
+ *     dL/dz_rj = g_r (1[j = y_r] - p_rj) / T * post'(z_rj),   g_r = dL/dlogprob_r
+ *     grad_h = dz . W,   grad_W = dz^T . h.
+ *
+ * Every entry point
+ *   - returns an int status (OCTO_OK or a negative OCTO_E* code) and never throws;
+ *     octo_last_error() gives a message for the last failing call on the calling thread;
+ *   - takes plain device pointers, element strides and sizes, and an explicit hipStream_t
+ *     (passed as void* so that the header needs no HIP include); all work is queued on that stream;
+ *   - allocates nothing: scratch memory comes from a caller-provided workspace whose size the
+ *     matching *_workspace_bytes query returns;
+ *   - does no device-to-host synchronisation: row counts produced on the device (octo_compact_rows)
+ *     are read by the kernels themselves.
+ *
+ * Reference interfaces replaced (shatianming5/octopus):
+ *   octopus/rl/lm_head.py:102-105  _head_chunk      -> octo_head_fwd (GEMM + fused epilogue)
+ *   octopus/rl/lm_head.py:108-112  _head_columns    -> octo_columns_fwd / octo_columns_bwd
+ *   octopus/rl/lm_head.py:115-121  _chunked_rows    -> octo_head_fwd + octo_head_bwd (no chunk loop,
+ *                                                     no checkpoint: the backward recomputes by design)
+ *   octopus/rl/lm_head.py:124-130  _scored_rows     -> octo_compact_rows + OCTO_ROWS_VIA_IDX /
+ *                                                     OCTO_OUT_SCATTER modes of octo_head_fwd
+ *   octopus/rl/prefix_tree.py:416-421 tree_head_output -> octo_pairs_expand / octo_pairs_grad
+ *   AReaL grpo_loss_fn (cited by docs/rl-plan-episodes.md:496-497, constants grpo.yaml:103-118)
+ *                                                  -> octo_grpo_grad
+ */
+#ifndef OCTO_HEAD_H
+#define OCTO_HEAD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------------------- */
+#define OCTO_OK            0
+#define OCTO_EINVAL       -1 /* bad shape, stride, pointer or dtype combination (ValueError)      */
+#define OCTO_EWORKSPACE   -2 /* workspace smaller than the query returned (ValueError)             */
+#define OCTO_EUNSUPPORTED -3 /* dtype or option the kernels do not implement (NotImplementedError) */
+#define OCTO_EHIP         -4 /* HIP runtime error while queueing work (RuntimeError)               */
+
+/* ---- element types ------------------------------------------------------------------------ */
+#define OCTO_BF16   0
+#define OCTO_F16    1
+#define OCTO_F32    2
+#define OCTO_FP8E4M3 3 /* OCP e4m3 (torch.float8_e4m3fn); weights only, with one fp32 scale per row */
+
+/* ---- flags -------------------------------------------------------------------------------- */
+#define OCTO_ROWS_VIA_IDX     1  /* labels[] are per hidden row: row r uses labels[idx[r]]            */
+#define OCTO_OUT_SCATTER      2  /* out2 row for compact row r is idx[r] (else r)                     */
+#define OCTO_GRADW_ACCUMULATE 4  /* grad_w += contribution (else grad_w = contribution)               */
+#define OCTO_WS_BACKWARD      8  /* octo_head_workspace_bytes: size for octo_head_bwd                 */
+#define OCTO_WS_NO_GRADW     16  /* octo_head_workspace_bytes: backward without grad_w                */
+
+const char *octo_version(void);
+const char *octo_last_error(void);
+
+/* Workspace bytes for octo_head_fwd (flags without OCTO_WS_BACKWARD) or octo_head_bwd
+ * (OCTO_WS_BACKWARD [| OCTO_WS_NO_GRADW]) at n_max rows, width d, vocabulary V. */
+int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes);
+
+/* Masked-row compaction (lm_head.py:128 `scored.nonzero()[:, 0]`): idx[0..count) = the positions
+ * r < n with mask[r] != 0, ascending; *count written on the device. idx must hold n entries;
+ * entries at and after *count are left unspecified. */
+int octo_compact_rows(const uint8_t *mask, int64_t n, int64_t *idx, int32_t *count, void *stream);
+
+/* Forward: logprob, entropy and lse of each compact row r < *count (or n_max when count is NULL).
+ *   hidden row of r  : h + (idx ? idx[r] : r) * ldh          (h_dtype BF16, F16 or F32);
+ *                      h holds h_rows rows and every idx[r] must be below h_rows
+ *   weight           : w [V, ldw] (w_dtype = h_dtype, or FP8E4M3 with w_scale[V] and BF16 h)
+ *   label of r       : labels[(flags & OCTO_ROWS_VIA_IDX) ? idx[r] : r], int64 in [0, V)
+ *   post-head logits : z' = use_tanh ? post * tanh(pre * z) : post * pre * z;  s = z' * inv_T
+ *   outputs          : logp[r], ent[r], lse[r] (any may be NULL) and, if out2 != NULL,
+ *                      out2[row * ld_out2 + {0,1}] = {logp, entropy} with row = idx[r] under
+ *                      OCTO_OUT_SCATTER, else r. Rows of out2 not written are left untouched.
+ * Requires d % 8 == 0 (bf16/f16/fp8) or d % 4 == 0 (f32), inv_T > 0, pre * post > 0 when !use_tanh. */
+int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
+                  const void *w, int64_t ldw, int w_dtype, const float *w_scale,
+                  const int64_t *labels, const int64_t *idx, const int32_t *count,
+                  int64_t n_max, int d, int V, int flags,
+                  float inv_T, float pre, float post, int use_tanh,
+                  float *logp, float *ent, float *lse, float *out2, int64_t ld_out2,
+                  void *ws, size_t ws_bytes, void *stream);
+
+/* Backward of octo_head_fwd's logprob column (the entropy column carries no gradient):
+ *   g[r]   : dL/dlogprob of compact row r (fp32, compact order)
+ *   lse[r] : from octo_head_fwd on the same inputs
+ *   grad_h : NULL or [n_max, ld_gh] of gh_dtype (BF16, F16 or F32), compact order; rows at and
+ *            after *count are left unspecified
+ *   grad_w : NULL or [V, d] fp32; = or += (OCTO_GRADW_ACCUMULATE). Not available for FP8E4M3 weights.
+ * The logits are recomputed tile by tile; dz is staged in the workspace in passes of rows. */
+int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
+                  const void *w, int64_t ldw, int w_dtype, const float *w_scale,
+                  const int64_t *labels, const int64_t *idx, const int32_t *count,
+                  int64_t n_max, int d, int V, int flags,
+                  float inv_T, float pre, float post, int use_tanh,
+                  const float *lse, const float *g,
+                  void *grad_h, int64_t ld_gh, int gh_dtype, float *grad_w,
+                  void *ws, size_t ws_bytes, void *stream);
+
+/* _head_columns on materialised logits [n, ld] (dtype BF16, F16 or F32):
+ * out2[r] = {log_softmax(s)[y_r], entropy}, s = logits * inv_T; lse[r] saved (may be NULL). */
+int octo_columns_fwd(const void *logits, int64_t ld, int dtype, const int64_t *labels,
+                     int64_t n, int V, float inv_T, float *out2, float *lse, void *stream);
+/* dlogits[r, j] = g[r] * (1[j = y_r] - p_rj) * inv_T, written in dtype at stride ld_d. */
+int octo_columns_bwd(const void *logits, int64_t ld, int dtype, const int64_t *labels,
+                     int64_t n, int V, float inv_T, const float *lse, const float *g,
+                     void *dlogits, int64_t ld_d, void *stream);
+
+/* Pair expansion (prefix_tree.py:419-421): out[t, :C] = pairs[flat_pair[t], :C] when
+ * 0 <= flat_pair[t] < P, else 0. */
+int octo_pairs_expand(const float *pairs, int64_t P, int C, const int64_t *flat_pair, int64_t T,
+                      float *out, void *stream);
+/* Its backward: grad_pairs[p, :C] = sum of grad_flat[t, :C] over t with flat_pair[t] == p
+ * (grad_pairs is overwritten). */
+int octo_pairs_grad(const float *grad_flat, int64_t T, int C, const int64_t *flat_pair, int64_t P,
+                    float *grad_pairs, void *stream);
+
+/* dst[idx[r], :d] (+)= src[r, :d] for r < *count, with idx ascending (repeats allowed: the rows of
+ * one run are summed in fp32 first). dst rows not named by idx are untouched; accumulate != 0 adds
+ * to dst. src/dst dtypes BF16, F16 or F32. */
+int octo_rows_scatter(const void *src, int64_t ld_src, int src_dtype, const int64_t *idx,
+                      const int32_t *count, int64_t n_max, int d,
+                      void *dst, int64_t ld_dst, int dst_dtype, int accumulate, void *stream);
+
+/* out[r] = src[idx[r] * ld_src] (fp32) for r < *count, 0 for count <= r < n_max. */
+int octo_gather_f32(const float *src, int64_t ld_src, const int64_t *idx, const int32_t *count,
+                    int64_t n_max, float *out, void *stream);
+
+/* GRPO/PPO policy-gradient weight per token (AReaL grpo_loss_fn semantics):
+ *   ratio r = exp(logp - prox)          (prox == NULL: prox = logp, i.e. reuse_train_logp)
+ *   behaviour weight w = exp(prox - old) when old != NULL (decoupled loss), else 1;
+ *                    w = 0 where reject_upper > 0 and w > reject_upper
+ *   L = sum_t mask_t * w_t * max(-A_t r_t, -A_t clip(r_t, 1 - eps_lo, 1 + eps_hi)) / Z,
+ *   Z = max(1, count of mask_t != 0)
+ *   g[t] = dL/dlogp[t] (ties of the max split evenly, as torch.maximum's backward)
+ * loss (NULL or one float) receives L. ws needs octo_grpo_workspace_bytes() bytes. */
+int octo_grpo_workspace_bytes(size_t *bytes);
+int octo_grpo_grad(const float *logp, const float *prox, const float *old, const float *adv,
+                   const float *mask, int64_t n, float eps_lo, float eps_hi, float reject_upper,
+                   float *g, float *loss, void *ws, size_t ws_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OCTO_HEAD_H */

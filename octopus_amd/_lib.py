@@ -1,0 +1,97 @@
+"""ctypes binding of libocto_head.so (the C ABI declared in include/octo_head.h).
+
+Every entry point returns an int status; `call` turns a non-zero status into the Python exception the
+reference raises for the same condition (ValueError for bad arguments, NotImplementedError for an
+unsupported dtype or option, RuntimeError for a HIP failure). The library is required: there is no
+fallback, and importing a GPU entry point without it raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libocto_head.so")
+
+# status codes and enums (include/octo_head.h)
+OK, EINVAL, EWORKSPACE, EUNSUPPORTED, EHIP = 0, -1, -2, -3, -4
+BF16, F16, F32, FP8E4M3 = 0, 1, 2, 3
+ROWS_VIA_IDX, OUT_SCATTER, GRADW_ACCUMULATE, WS_BACKWARD, WS_NO_GRADW = 1, 2, 4, 8, 16
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> argument types (restype is int unless listed in _RESTYPES)
+SIGNATURES = {
+    "octo_version": [],
+    "octo_last_error": [],
+    "octo_head_workspace_bytes": [_i64, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)],
+    "octo_compact_rows": [_p, _i64, _p, _p, _p],
+    "octo_head_fwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                      _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, _p, _sz, _p],
+    "octo_head_bwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                      _f32, _f32, _f32, _i32, _p, _p, _p, _i64, _i32, _p, _p, _sz, _p],
+    "octo_columns_fwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p],
+    "octo_columns_bwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p, _i64, _p],
+    "octo_pairs_expand": [_p, _i64, _i32, _p, _i64, _p, _p],
+    "octo_pairs_grad": [_p, _i64, _i32, _p, _i64, _p, _p],
+    "octo_rows_scatter": [_p, _i64, _i32, _p, _p, _i64, _i32, _p, _i64, _i32, _i32, _p],
+    "octo_gather_f32": [_p, _i64, _p, _p, _i64, _p, _p],
+    "octo_grpo_workspace_bytes": [ctypes.POINTER(_sz)],
+    "octo_grpo_grad": [_p, _p, _p, _p, _p, _i64, _f32, _f32, _f32, _p, _p, _p, _sz, _p],
+}
+_RESTYPES = {"octo_version": ctypes.c_char_p, "octo_last_error": ctypes.c_char_p}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """The loaded library with every signature bound. Raises RuntimeError when it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise RuntimeError(f"{path} is missing: build it with `python -m octopus_amd.build` "
+                                   "(the LM head has no non-HIP GPU path)")
+            lib = ctypes.CDLL(path)
+            for name, args in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.argtypes = args
+                fn.restype = _RESTYPES.get(name, ctypes.c_int)
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().octo_last_error().decode(errors="replace")
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point; raise on a non-zero status."""
+    rc = getattr(load(), name)(*args)
+    if rc == OK:
+        return
+    msg = f"{name}: {last_error()}"
+    if rc in (EINVAL, EWORKSPACE):
+        raise ValueError(msg)
+    if rc == EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(f"{msg} (status {rc})")
+
+
+def workspace_bytes(n_max: int, d: int, V: int, w_dtype: int, flags: int) -> int:
+    out = _sz(0)
+    call("octo_head_workspace_bytes", n_max, d, V, w_dtype, flags, ctypes.byref(out))
+    return out.value
+
+
+def grpo_workspace_bytes() -> int:
+    out = _sz(0)
+    call("octo_grpo_workspace_bytes", ctypes.byref(out))
+    return out.value

@@ -1,0 +1,357 @@
+// C-ABI entry points of the fused head (octo_head_fwd / octo_head_bwd), the workspace query and the
+// status plumbing. Argument checks happen here, on the host, before anything is queued.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "gemm_nt.h"
+#include "octo_internal.h"
+
+static thread_local char g_err[512] = "";
+
+void octo_set_error(const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+}
+
+int octo_fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+using namespace octo;
+
+namespace {
+
+constexpr int64_t kPassRows = 32768;  // backward rows per pass (bounds the dz staging buffers)
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+int elem_bytes(int dt) { return dt == OCTO_F32 ? 4 : (dt == OCTO_FP8E4M3 ? 1 : 2); }
+// MFMA operand type for a weight dtype: fp8 weights are widened to bf16 in LDS.
+int staged_dtype(int w_dtype) { return w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_dtype; }
+
+struct FwdLayout {
+  int64_t mtiles;
+  size_t part, total;
+};
+FwdLayout fwd_layout(int64_t n_max, int V) {
+  FwdLayout L;
+  L.mtiles = cdiv(V, TM);
+  L.part = 0;
+  L.total = align_up((size_t)n_max * L.mtiles * sizeof(f32x4));
+  return L;
+}
+
+struct BwdLayout {
+  int64_t P, V_pad, passes;
+  int esz;
+  size_t wt, ht, dza, dzb, total;
+};
+BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw) {
+  BwdLayout L;
+  L.esz = elem_bytes(staged_dtype(w_dtype));
+  L.V_pad = round_up(V, TM);
+  L.P = n_max == 0 ? 0 : (round_up(n_max, TN) < kPassRows ? round_up(n_max, TN) : kPassRows);
+  L.passes = L.P == 0 ? 0 : cdiv(n_max, L.P);
+  size_t off = 0;
+  L.wt = off;
+  off += align_up((size_t)d * L.V_pad * L.esz);
+  L.ht = off;
+  if (need_gw) off += align_up((size_t)d * L.P * L.esz);
+  L.dza = off;
+  if (need_gh) off += align_up((size_t)L.P * L.V_pad * L.esz);
+  L.dzb = off;
+  if (need_gw) off += align_up((size_t)L.V_pad * L.P * L.esz);
+  L.total = off;
+  return L;
+}
+
+struct Common {
+  int hesz, wesz, dt;
+  bool fp8;
+  float c, pre, gmul;
+  uint32_t h_extent;
+};
+
+int check_common(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
+                 const float *w_scale, const int64_t *labels, const int64_t *idx, int64_t n_max, int d, int V,
+                 int flags, float inv_T, float pre, float post, int use_tanh, Common &cm) {
+  OCTO_CHECK_ARG(n_max >= 0 && d > 0 && V > 0, "head: bad sizes n_max=%lld d=%d V=%d", (long long)n_max, d, V);
+  OCTO_CHECK_ARG(h && w && labels, "head: null h, w or labels");
+  const bool fp8 = w_dtype == OCTO_FP8E4M3;
+  if (fp8) {
+    if (h_dtype != OCTO_BF16) return octo_fail(OCTO_EUNSUPPORTED, "head: fp8 weights need bf16 hidden rows");
+    OCTO_CHECK_ARG(w_scale != nullptr, "head: fp8 weights need per-row scales");
+  } else {
+    if (!(h_dtype == OCTO_BF16 || h_dtype == OCTO_F16 || h_dtype == OCTO_F32))
+      return octo_fail(OCTO_EUNSUPPORTED, "head: hidden dtype %d", h_dtype);
+    if (w_dtype != h_dtype)
+      return octo_fail(OCTO_EUNSUPPORTED, "head: weight dtype %d differs from hidden dtype %d", w_dtype, h_dtype);
+  }
+  cm.hesz = elem_bytes(h_dtype);
+  cm.wesz = elem_bytes(w_dtype);
+  cm.dt = staged_dtype(w_dtype);
+  cm.fp8 = fp8;
+  const int kq = (h_dtype == OCTO_F32) ? 4 : 8;
+  OCTO_CHECK_ARG(d % kq == 0, "head: d=%d must be a multiple of %d", d, kq);
+  OCTO_CHECK_ARG(ldh >= d && ldw >= d, "head: row strides below d");
+  OCTO_CHECK_ARG((ldh * cm.hesz) % 16 == 0 && ((uintptr_t)h) % 16 == 0, "head: hidden rows must be 16-byte aligned");
+  OCTO_CHECK_ARG((ldw * cm.wesz) % (fp8 ? 8 : 16) == 0 && ((uintptr_t)w) % 16 == 0,
+                 "head: weight rows must be 16-byte aligned");
+  OCTO_CHECK_ARG(!fp8 || ((uintptr_t)w_scale) % 16 == 0, "head: w_scale must be 16-byte aligned");
+  OCTO_CHECK_ARG(256 * ldh * cm.hesz < (int64_t)0x7fffffff && 256 * ldw * cm.wesz < (int64_t)0x7fffffff,
+                 "head: row stride too large");
+  if (idx) {
+    OCTO_CHECK_ARG(h_rows > 0, "head: h_rows must be positive with idx");
+    const int64_t ext = h_rows * ldh * cm.hesz;
+    if (ext >= (int64_t)0x7fffffff) return octo_fail(OCTO_EUNSUPPORTED, "head: gathered hidden exceeds 2 GiB");
+    cm.h_extent = (uint32_t)ext;
+  } else {
+    OCTO_CHECK_ARG(h_rows >= n_max, "head: h_rows %lld < n_max %lld", (long long)h_rows, (long long)n_max);
+    cm.h_extent = 0;
+    OCTO_CHECK_ARG(!(flags & (OCTO_ROWS_VIA_IDX | OCTO_OUT_SCATTER)), "head: idx-based flags without idx");
+  }
+  OCTO_CHECK_ARG(inv_T > 0.f, "head: temperature must be positive");
+  if (use_tanh) {
+    OCTO_CHECK_ARG(post > 0.f && pre != 0.f, "head: softcap needs post > 0 and pre != 0");
+    cm.c = post * inv_T * OCTO_LOG2E;
+  } else {
+    OCTO_CHECK_ARG(pre * post > 0.f, "head: logit scale must be positive");
+    cm.c = pre * post * inv_T * OCTO_LOG2E;
+  }
+  cm.pre = pre;
+  cm.gmul = inv_T * pre * post;
+  return OCTO_OK;
+}
+
+Operand weight_operand(const void *w, int64_t ldw, const Common &cm, int V) {
+  Operand A;
+  A.base = (const char *)w;
+  A.ld = ldw * cm.wesz;
+  A.map = nullptr;
+  A.rows = V;
+  A.count = nullptr;
+  A.count_off = 0;
+  A.extent = 0;
+  return A;
+}
+
+// Hidden rows [r0, r0 + rows) of the compact order.
+Operand hidden_operand(const void *h, int64_t ldh, const int64_t *idx, const int32_t *count, int64_t r0,
+                       int64_t rows, const Common &cm) {
+  Operand B;
+  B.ld = ldh * cm.hesz;
+  if (idx) {
+    B.base = (const char *)h;
+    B.map = idx + r0;
+    B.extent = cm.h_extent;
+  } else {
+    B.base = (const char *)h + r0 * B.ld;
+    B.map = nullptr;
+    B.extent = 0;
+  }
+  B.rows = rows;
+  B.count = count;
+  B.count_off = r0;
+  return B;
+}
+
+Operand plain_operand(const void *base, int64_t ld_bytes, int64_t rows, const int32_t *count, int64_t count_off) {
+  Operand X;
+  X.base = (const char *)base;
+  X.ld = ld_bytes;
+  X.map = nullptr;
+  X.rows = rows;
+  X.count = count;
+  X.count_off = count_off;
+  X.extent = 0;
+  return X;
+}
+
+GemmShape shape(int64_t M, int64_t N, int64_t K, int group_m, int count_on, const int32_t *count, int64_t count_off) {
+  GemmShape s;
+  s.M = M;
+  s.N = N;
+  s.K = K;
+  s.mtiles = (int)cdiv(M, TM);
+  s.ntiles = (int)cdiv(N, TN);
+  s.group_m = group_m;
+  s.count_on = count_on;
+  s.count = count;
+  s.count_off = count_off;
+  return s;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *octo_version(void) { return "octo_head 0.1 (gfx950)"; }
+const char *octo_last_error(void) { return g_err; }
+
+int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes) {
+  OCTO_CHECK_ARG(bytes != nullptr, "workspace_bytes: null pointer");
+  OCTO_CHECK_ARG(n_max >= 0 && d > 0 && V > 0, "workspace_bytes: bad sizes");
+  OCTO_CHECK_ARG(w_dtype >= OCTO_BF16 && w_dtype <= OCTO_FP8E4M3, "workspace_bytes: dtype %d", w_dtype);
+  if (flags & OCTO_WS_BACKWARD) {
+    *bytes = bwd_layout(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW)).total;
+  } else {
+    *bytes = fwd_layout(n_max, V).total;
+  }
+  return OCTO_OK;
+}
+
+int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
+                  const float *w_scale, const int64_t *labels, const int64_t *idx, const int32_t *count,
+                  int64_t n_max, int d, int V, int flags, float inv_T, float pre, float post, int use_tanh,
+                  float *logp, float *ent, float *lse, float *out2, int64_t ld_out2, void *ws, size_t ws_bytes,
+                  void *stream) {
+  Common cm;
+  int rc = check_common(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, n_max, d, V, flags, inv_T,
+                        pre, post, use_tanh, cm);
+  if (rc) return rc;
+  OCTO_CHECK_ARG(!out2 || ld_out2 >= 2, "head_fwd: ld_out2 < 2");
+  if (n_max == 0) return OCTO_OK;
+  const FwdLayout L = fwd_layout(n_max, V);
+  if (!ws || ws_bytes < L.total)
+    return octo_fail(OCTO_EWORKSPACE, "head_fwd: workspace %zu < %zu bytes", ws_bytes, L.total);
+  hipStream_t st = (hipStream_t)stream;
+
+  const Operand A = weight_operand(w, ldw, cm, V);
+  const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
+  const GemmShape s = shape(V, n_max, d, 4, 2, count, 0);
+  StatsArgs e;
+  e.part = (f32x4 *)((char *)ws + L.part);
+  e.mtiles = L.mtiles;
+  e.V = V;
+  e.wscale = w_scale;
+  e.c = cm.c;
+  e.pre = cm.pre;
+  rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, A, B, s, e, st);
+  if (rc) return rc;
+
+  MergeArgs m;
+  m.part = e.part;
+  m.mtiles = L.mtiles;
+  m.h = h;
+  m.ldh = ldh;
+  m.h_dtype = h_dtype;
+  m.w = w;
+  m.ldw = ldw;
+  m.w_dtype = w_dtype;
+  m.wscale = w_scale;
+  m.labels = labels;
+  m.idx = idx;
+  m.count = count;
+  m.n_max = n_max;
+  m.d = d;
+  m.V = V;
+  m.flags = flags;
+  m.inv_T = inv_T;
+  m.pre = pre;
+  m.post = post;
+  m.use_tanh = use_tanh;
+  m.logp = logp;
+  m.ent = ent;
+  m.lse = lse;
+  m.out2 = out2;
+  m.ld_out2 = ld_out2;
+  return launch_merge(m, st);
+}
+
+int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
+                  const float *w_scale, const int64_t *labels, const int64_t *idx, const int32_t *count,
+                  int64_t n_max, int d, int V, int flags, float inv_T, float pre, float post, int use_tanh,
+                  const float *lse, const float *g, void *grad_h, int64_t ld_gh, int gh_dtype, float *grad_w,
+                  void *ws, size_t ws_bytes, void *stream) {
+  Common cm;
+  int rc = check_common(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, n_max, d, V, flags, inv_T,
+                        pre, post, use_tanh, cm);
+  if (rc) return rc;
+  OCTO_CHECK_ARG(lse && g, "head_bwd: null lse or g");
+  if (grad_h) {
+    OCTO_CHECK_ARG(gh_dtype == OCTO_BF16 || gh_dtype == OCTO_F16 || gh_dtype == OCTO_F32, "head_bwd: grad_h dtype");
+    OCTO_CHECK_ARG(ld_gh >= d, "head_bwd: ld_gh < d");
+  }
+  if (grad_w && cm.fp8) return octo_fail(OCTO_EUNSUPPORTED, "head_bwd: grad_w of fp8 weights");
+  const bool need_gh = grad_h != nullptr, need_gw = grad_w != nullptr;
+  if (n_max == 0 || (!need_gh && !need_gw)) return OCTO_OK;
+  const BwdLayout L = bwd_layout(n_max, d, V, w_dtype, need_gh, need_gw);
+  if (!ws || ws_bytes < L.total)
+    return octo_fail(OCTO_EWORKSPACE, "head_bwd: workspace %zu < %zu bytes", ws_bytes, L.total);
+  hipStream_t st = (hipStream_t)stream;
+  char *wsb = (char *)ws;
+  void *wt = wsb + L.wt, *ht = wsb + L.ht, *dza = wsb + L.dza, *dzb = wsb + L.dzb;
+  const int esz = L.esz;
+
+  // W^T [d, V_pad] in the staged type (fp8 weights: their exact bf16 values; the row scale is in dz)
+  if (need_gh) {
+    rc = launch_transpose(w, ldw, w_dtype, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt, L.V_pad, cm.dt, st);
+    if (rc) return rc;
+  }
+  const Operand Aw = weight_operand(w, ldw, cm, V);
+
+  for (int64_t p = 0; p < L.passes; ++p) {
+    const int64_t r0 = p * L.P;
+    const int64_t rows = (n_max - r0) < L.P ? (n_max - r0) : L.P;
+
+    // dz of this pass, recomputed tile by tile
+    const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm);
+    const GemmShape s1 = shape(V, rows, d, 4, 2, count, r0);
+    DzArgs e;
+    e.dzA = need_gh ? dza : nullptr;
+    e.ldA = L.V_pad;
+    e.dzB = need_gw ? dzb : nullptr;
+    e.ldB = L.P;
+    e.lse = lse;
+    e.g = g;
+    e.labels = labels;
+    e.label_idx = (flags & OCTO_ROWS_VIA_IDX) ? idx : nullptr;
+    e.row_off = r0;
+    e.V = V;
+    e.wscale = w_scale;
+    e.c = cm.c;
+    e.pre = cm.pre;
+    e.gmul = cm.gmul;
+    rc = launch_gemm_dz(cm.dt, cm.fp8, use_tanh != 0, Aw, Bh, s1, e, st);
+    if (rc) return rc;
+
+    if (need_gh) {  // grad_h[rows] = dz . W   (K = V_pad)
+      const Operand A2 = plain_operand(dza, L.V_pad * esz, rows, count, r0);
+      const Operand B2 = plain_operand(wt, L.V_pad * esz, d, nullptr, 0);
+      const GemmShape s2 = shape(rows, d, L.V_pad, 4, 1, count, r0);
+      StoreArgs o;
+      o.C = (char *)grad_h + r0 * ld_gh * elem_bytes(gh_dtype);
+      o.ldc = ld_gh;
+      o.dtype = gh_dtype;
+      o.accumulate = 0;
+      rc = launch_gemm_store(cm.dt, A2, B2, s2, o, st);
+      if (rc) return rc;
+    }
+    if (need_gw) {  // grad_W += dz^T . h   (K = this pass's rows)
+      const int64_t rows_pad = round_up(rows, TN);
+      rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, nullptr,
+                            idx ? idx + r0 : nullptr, count, r0, rows, rows_pad, d, ht, L.P, cm.dt, st);
+      if (rc) return rc;
+      const Operand A3 = plain_operand(dzb, L.P * esz, L.V_pad, nullptr, 0);
+      const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
+      const GemmShape s3 = shape(V, d, rows, 4, 3, count, r0);
+      StoreArgs o;
+      o.C = grad_w;
+      o.ldc = d;
+      o.dtype = OCTO_F32;
+      o.accumulate = (p > 0 || (flags & OCTO_GRADW_ACCUMULATE)) ? 1 : 0;
+      rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st);
+      if (rc) return rc;
+    }
+  }
+  return OCTO_OK;
+}
+
+}  // extern "C"

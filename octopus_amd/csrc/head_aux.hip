@@ -1,0 +1,408 @@
+// Memory-bound kernels of the LM-head path and their C-ABI entry points:
+//   merge          per-row merge of the vocab-tile softmax partials + target logit -> logp, entropy, lse
+//   transpose      K-contiguous copies (W^T, gathered h^T) feeding the backward GEMMs
+//   compact_rows   masked-row compaction, ascending (torch.nonzero order), count left on the device
+//   columns fwd/bwd  _head_columns over materialised logits
+//   pairs expand/grad, rows scatter, gather   the index plumbing of tree_head_output / _scored_rows
+//   grpo           the per-token policy-gradient weight g = dL/dlogp of the GRPO objective
+#include "octo_internal.h"
+
+namespace octo {
+
+// ---- merge: vocab-tile partials -> per-row outputs ----------------------------------------------
+// One wave per compact row: lanes merge the row's partials (m, S, U) strided by 64, then a wave
+// butterfly; the target logit h_r . W_y is a wave dot product in fp32.
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
+  if (r >= cnt) return;
+  const int64_t hrow = a.idx ? a.idx[r] : r;
+  const int64_t y = a.labels[(a.flags & OCTO_ROWS_VIA_IDX) ? hrow : r];
+
+  Stat3 st{-INFINITY, 0.f, 0.f};
+  const f32x4 *pr = a.part + r * a.mtiles;
+  for (int64_t mt = lane; mt < a.mtiles; mt += 64) {
+    const f32x4 p = pr[mt];
+    st = stat_merge(st, Stat3{p[0], p[1], p[2]});
+  }
+  st = wave_stat_merge(st);
+
+  float dot = 0.f;
+  const bool y_ok = y >= 0 && y < a.V;
+  if (y_ok) {
+    for (int k = lane; k < a.d; k += 64) {
+      const float hv = load_as_f32(a.h, a.h_dtype, hrow * a.ldh + k);
+      float wv;
+      if (a.w_dtype == OCTO_FP8E4M3) wv = e4m3_to_f32(((const uint8_t *)a.w)[y * a.ldw + k]);
+      else wv = load_as_f32(a.w, a.w_dtype, y * a.ldw + k);
+      dot = __builtin_fmaf(hv, wv, dot);
+    }
+  }
+  dot = wave_sum(dot);
+  if (lane != 0) return;
+  if (a.w_dtype == OCTO_FP8E4M3 && y_ok) dot *= a.wscale[y];
+  const float zt = a.use_tanh ? a.post * tanhf(a.pre * dot) : a.post * a.pre * dot;
+  const float sy = zt * a.inv_T;
+  const float l2S = flog2(st.S);
+  const float lse = (st.m + l2S) * OCTO_LN2;
+  const float ent = (l2S - st.U / st.S) * OCTO_LN2;
+  const float lp = y_ok ? sy - lse : __builtin_nanf("");
+  if (a.logp) a.logp[r] = lp;
+  if (a.ent) a.ent[r] = ent;
+  if (a.lse) a.lse[r] = lse;
+  if (a.out2) {
+    const int64_t orow = (a.flags & OCTO_OUT_SCATTER) ? hrow : r;
+    a.out2[orow * a.ld_out2] = lp;
+    a.out2[orow * a.ld_out2 + 1] = ent;
+  }
+}
+
+int launch_merge(const MergeArgs &a, hipStream_t st) {
+  if (a.n_max == 0) return OCTO_OK;
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)cdiv(a.n_max, 4)), dim3(256), 0, st, a);
+  OCTO_CHECK_LAUNCH("merge");
+  return OCTO_OK;
+}
+
+// ---- transpose -----------------------------------------------------------------------------------
+// dst[c, r] = src[row(r), c]: 64 x 64 tiles through LDS (fp32 words, padded against bank conflicts).
+__global__ __launch_bounds__(256) void transpose_kernel(const void *src, int64_t ld_src, int src_dtype,
+                                                        const int64_t *map, const int32_t *count,
+                                                        int64_t count_off, int64_t rows, int64_t rows_pad,
+                                                        int64_t cols, void *dst, int64_t ld_dst, int dst_dtype) {
+  __shared__ float tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  const int64_t valid = dev_count(count, count_off, rows);
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    float x = 0.f;
+    if (r < valid && c < cols) {
+      const int64_t pr = map ? map[r] : r;
+      if (src_dtype == OCTO_FP8E4M3) x = e4m3_to_f32(((const uint8_t *)src)[pr * ld_src + c]);
+      else x = load_as_f32(src, src_dtype, pr * ld_src + c);
+    }
+    tile[i][tx] = x;
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t c = c0 + i, r = r0 + tx;
+    if (c < cols && r < rows_pad) store_from_f32(dst, dst_dtype, c * ld_dst + r, tile[tx][i]);
+  }
+}
+
+int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *,
+                     const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
+                     int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st) {
+  if (rows_pad == 0 || cols == 0) return OCTO_OK;
+  dim3 grid((unsigned)cdiv(rows_pad, 64), (unsigned)cdiv(cols, 64));
+  hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, st, src, ld_src, src_dtype, map, count, count_off, rows,
+                     rows_pad, cols, dst, ld_dst, dst_dtype);
+  OCTO_CHECK_LAUNCH("transpose");
+  return OCTO_OK;
+}
+
+// ---- compaction ----------------------------------------------------------------------------------
+// One workgroup of 16 waves sweeps the mask 1024 entries at a time: a ballot per wave, the lane's
+// rank from the bits below it, the waves' totals scanned through LDS.
+__global__ __launch_bounds__(1024) void compact_kernel(const uint8_t *mask, int64_t n, int64_t *idx, int32_t *count) {
+  __shared__ int wsum[16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int64_t base = 0;
+  for (int64_t s0 = 0; s0 < n; s0 += 1024) {
+    const int64_t i = s0 + threadIdx.x;
+    const bool f = i < n && mask[i] != 0;
+    const uint64_t bal = __ballot(f);
+    const int rank = __popcll(bal & ((1ull << lane) - 1ull));
+    if (lane == 0) wsum[w] = __popcll(bal);
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int c = wsum[k];
+      off += (k < w) ? c : 0;
+      tot += c;
+    }
+    if (f) idx[base + off + rank] = i;
+    base += tot;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *count = (int32_t)base;
+}
+
+// ---- _head_columns over materialised logits ------------------------------------------------------
+__global__ __launch_bounds__(256) void columns_fwd_kernel(const void *logits, int64_t ld, int dtype,
+                                                          const int64_t *labels, int V, float inv_T,
+                                                          float *out2, float *lse_out) {
+  const int64_t r = blockIdx.x;
+  __shared__ float red[3][4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const float c = inv_T * OCTO_LOG2E;
+  float mx = -INFINITY;
+  for (int j = threadIdx.x; j < V; j += 256) mx = fmaxf(mx, load_as_f32(logits, dtype, r * ld + j));
+  mx = wave_max(mx);
+  if (lane == 0) red[0][w] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  const float m2 = mx * c;
+  float S = 0.f, U = 0.f;
+  for (int j = threadIdx.x; j < V; j += 256) {
+    const float t = __builtin_fmaf(load_as_f32(logits, dtype, r * ld + j), c, -m2);
+    const float e = fexp2(t);
+    S += e;
+    U = __builtin_fmaf(e, t, U);
+  }
+  S = wave_sum(S);
+  U = wave_sum(U);
+  if (lane == 0) {
+    red[1][w] = S;
+    red[2][w] = U;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    S = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    U = red[2][0] + red[2][1] + red[2][2] + red[2][3];
+    const float l2S = flog2(S);
+    const float lse = (m2 + l2S) * OCTO_LN2;
+    const int64_t y = labels[r];
+    const float sy = (y >= 0 && y < V) ? load_as_f32(logits, dtype, r * ld + y) * inv_T : __builtin_nanf("");
+    out2[2 * r] = sy - lse;
+    out2[2 * r + 1] = (l2S - U / S) * OCTO_LN2;
+    if (lse_out) lse_out[r] = lse;
+  }
+}
+
+__global__ __launch_bounds__(256) void columns_bwd_kernel(const void *logits, int64_t ld, int dtype,
+                                                          const int64_t *labels, int V, float inv_T,
+                                                          const float *lse, const float *g, void *dl,
+                                                          int64_t ld_d) {
+  const int64_t r = blockIdx.y;
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= V) return;
+  const float p = fexp2((load_as_f32(logits, dtype, r * ld + j) * inv_T - lse[r]) * OCTO_LOG2E);
+  const float onehot = (labels[r] == j) ? 1.f : 0.f;
+  store_from_f32(dl, dtype, r * ld_d + j, g[r] * inv_T * (onehot - p));
+}
+
+// ---- pairs / rows plumbing -----------------------------------------------------------------------
+__global__ void pairs_expand_kernel(const float *pairs, int64_t P, int C, const int64_t *fp, int64_t T, float *out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * C) return;
+  const int64_t t = i / C, c = i - t * C;
+  const int64_t p = fp[t];
+  out[i] = (p >= 0 && p < P) ? pairs[p * C + c] : 0.f;
+}
+
+__global__ void fill_zero_kernel(float *x, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = 0.f;
+}
+
+__global__ void pairs_grad_kernel(const float *gf, int64_t T, int C, const int64_t *fp, int64_t P, float *gp) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= T * C) return;
+  const int64_t t = i / C, c = i - t * C;
+  const int64_t p = fp[t];
+  if (p >= 0 && p < P) atomicAdd(gp + p * C + c, gf[i]);
+}
+
+// One workgroup per compact row r that starts a run of equal idx; it sums the run in fp32.
+__global__ __launch_bounds__(256) void rows_scatter_kernel(const void *src, int64_t ld_src, int src_dtype,
+                                                           const int64_t *idx, const int32_t *count, int64_t n_max,
+                                                           int d, void *dst, int64_t ld_dst, int dst_dtype,
+                                                           int accumulate) {
+  const int64_t r = blockIdx.x;
+  const int64_t cnt = count ? min((int64_t)(*count), n_max) : n_max;
+  if (r >= cnt) return;
+  const int64_t row = idx[r];
+  if (r > 0 && idx[r - 1] == row) return;
+  int64_t e = r + 1;
+  while (e < cnt && idx[e] == row) ++e;
+  for (int k = threadIdx.x; k < d; k += 256) {
+    float s = accumulate ? load_as_f32(dst, dst_dtype, row * ld_dst + k) : 0.f;
+    for (int64_t q = r; q < e; ++q) s += load_as_f32(src, src_dtype, q * ld_src + k);
+    store_from_f32(dst, dst_dtype, row * ld_dst + k, s);
+  }
+}
+
+__global__ void gather_f32_kernel(const float *src, int64_t ld, const int64_t *idx, const int32_t *count,
+                                  int64_t n_max, float *out) {
+  const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= n_max) return;
+  const int64_t cnt = count ? min((int64_t)(*count), n_max) : n_max;
+  out[r] = (r < cnt) ? src[idx[r] * ld] : 0.f;
+}
+
+// ---- GRPO ----------------------------------------------------------------------------------------
+// ws[0] = Z (masked-token count, at least 1); *loss zeroed. One workgroup.
+__global__ __launch_bounds__(1024) void grpo_count_kernel(const float *mask, int64_t n, float *ws, float *loss) {
+  __shared__ float part[16];
+  float c = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) c += (mask[i] != 0.f) ? 1.f : 0.f;
+  c = wave_sum(c);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float z = 0.f;
+    for (int k = 0; k < 16; ++k) z += part[k];
+    ws[0] = fmaxf(z, 1.f);
+    if (loss) *loss = 0.f;
+  }
+}
+
+__global__ __launch_bounds__(256) void grpo_grad_kernel(const float *logp, const float *prox, const float *old,
+                                                        const float *adv, const float *mask, int64_t n,
+                                                        float eps_lo, float eps_hi, float reject_upper,
+                                                        const float *ws, float *g, float *loss) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  float lt = 0.f;
+  if (t < n) {
+    float gt = 0.f;
+    if (mask[t] != 0.f) {
+      const float inv_z = 1.f / ws[0];
+      const float lp = logp[t];
+      const float px = prox ? prox[t] : lp;
+      const float r = expf(lp - px);
+      float w = 1.f;
+      if (old) {
+        w = expf(px - old[t]);
+        if (reject_upper > 0.f && w > reject_upper) w = 0.f;
+      }
+      const float A = adv[t];
+      const float lo = 1.f - eps_lo, hi = 1.f + eps_hi;
+      const float cl = fminf(fmaxf(r, lo), hi);
+      const float a = -A * r, b = -A * cl;
+      const bool inside = (r >= lo) && (r <= hi);
+      float ga, gb;
+      if (a > b) { ga = 1.f; gb = 0.f; }
+      else if (a < b) { ga = 0.f; gb = 1.f; }
+      else { ga = 0.5f; gb = 0.5f; }
+      const float dmax_dr = ga * (-A) + gb * (-A) * (inside ? 1.f : 0.f);
+      gt = w * dmax_dr * r * inv_z;
+      lt = w * fmaxf(a, b) * inv_z;
+    }
+    g[t] = gt;
+  }
+  if (loss) {
+    lt = wave_sum(lt);
+    if ((threadIdx.x & 63) == 0 && lt != 0.f) atomicAdd(loss, lt);
+  }
+}
+
+}  // namespace octo
+
+using namespace octo;
+
+// ---- C ABI: small entry points -------------------------------------------------------------------
+extern "C" {
+
+int octo_compact_rows(const uint8_t *mask, int64_t n, int64_t *idx, int32_t *count, void *stream) {
+  OCTO_CHECK_ARG(n >= 0, "compact_rows: n < 0");
+  OCTO_CHECK_ARG(count != nullptr && (n == 0 || (mask && idx)), "compact_rows: null pointer");
+  hipLaunchKernelGGL(compact_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, mask, n, idx, count);
+  OCTO_CHECK_LAUNCH("compact_rows");
+  return OCTO_OK;
+}
+
+int octo_columns_fwd(const void *logits, int64_t ld, int dtype, const int64_t *labels, int64_t n, int V,
+                     float inv_T, float *out2, float *lse, void *stream) {
+  OCTO_CHECK_ARG(n >= 0 && V > 0 && ld >= V, "columns_fwd: bad shape n=%lld V=%d ld=%lld", (long long)n, V, (long long)ld);
+  OCTO_CHECK_ARG(dtype == OCTO_BF16 || dtype == OCTO_F16 || dtype == OCTO_F32, "columns_fwd: dtype %d", dtype);
+  OCTO_CHECK_ARG(inv_T > 0.f, "columns_fwd: temperature must be positive");
+  if (n == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(logits && labels && out2, "columns_fwd: null pointer");
+  hipLaunchKernelGGL(columns_fwd_kernel, dim3((unsigned)n), dim3(256), 0, (hipStream_t)stream, logits, ld, dtype,
+                     labels, V, inv_T, out2, lse);
+  OCTO_CHECK_LAUNCH("columns_fwd");
+  return OCTO_OK;
+}
+
+int octo_columns_bwd(const void *logits, int64_t ld, int dtype, const int64_t *labels, int64_t n, int V,
+                     float inv_T, const float *lse, const float *g, void *dlogits, int64_t ld_d, void *stream) {
+  OCTO_CHECK_ARG(n >= 0 && V > 0 && ld >= V && ld_d >= V, "columns_bwd: bad shape");
+  OCTO_CHECK_ARG(dtype == OCTO_BF16 || dtype == OCTO_F16 || dtype == OCTO_F32, "columns_bwd: dtype %d", dtype);
+  if (n == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(logits && labels && lse && g && dlogits, "columns_bwd: null pointer");
+  OCTO_CHECK_ARG(n <= 65535, "columns_bwd: more than 65535 rows per call");
+  dim3 grid((unsigned)cdiv(V, 256), (unsigned)n);
+  hipLaunchKernelGGL(columns_bwd_kernel, grid, dim3(256), 0, (hipStream_t)stream, logits, ld, dtype, labels, V, inv_T,
+                     lse, g, dlogits, ld_d);
+  OCTO_CHECK_LAUNCH("columns_bwd");
+  return OCTO_OK;
+}
+
+int octo_pairs_expand(const float *pairs, int64_t P, int C, const int64_t *flat_pair, int64_t T, float *out,
+                      void *stream) {
+  OCTO_CHECK_ARG(P >= 0 && C > 0 && T >= 0, "pairs_expand: bad shape");
+  if (T == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(flat_pair && out && (P == 0 || pairs), "pairs_expand: null pointer");
+  hipLaunchKernelGGL(pairs_expand_kernel, dim3((unsigned)cdiv(T * C, 256)), dim3(256), 0, (hipStream_t)stream, pairs, P,
+                     C, flat_pair, T, out);
+  OCTO_CHECK_LAUNCH("pairs_expand");
+  return OCTO_OK;
+}
+
+int octo_pairs_grad(const float *grad_flat, int64_t T, int C, const int64_t *flat_pair, int64_t P,
+                    float *grad_pairs, void *stream) {
+  OCTO_CHECK_ARG(P >= 0 && C > 0 && T >= 0, "pairs_grad: bad shape");
+  if (P > 0) {
+    OCTO_CHECK_ARG(grad_pairs != nullptr, "pairs_grad: null pointer");
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)cdiv(P * C, 256)), dim3(256), 0, (hipStream_t)stream,
+                       grad_pairs, P * C);
+  }
+  if (T > 0 && P > 0) {
+    OCTO_CHECK_ARG(grad_flat && flat_pair, "pairs_grad: null pointer");
+    hipLaunchKernelGGL(pairs_grad_kernel, dim3((unsigned)cdiv(T * C, 256)), dim3(256), 0, (hipStream_t)stream,
+                       grad_flat, T, C, flat_pair, P, grad_pairs);
+  }
+  OCTO_CHECK_LAUNCH("pairs_grad");
+  return OCTO_OK;
+}
+
+int octo_rows_scatter(const void *src, int64_t ld_src, int src_dtype, const int64_t *idx, const int32_t *count,
+                      int64_t n_max, int d, void *dst, int64_t ld_dst, int dst_dtype, int accumulate, void *stream) {
+  OCTO_CHECK_ARG(n_max >= 0 && d >= 0, "rows_scatter: bad shape");
+  OCTO_CHECK_ARG(src_dtype == OCTO_BF16 || src_dtype == OCTO_F16 || src_dtype == OCTO_F32, "rows_scatter: src dtype");
+  OCTO_CHECK_ARG(dst_dtype == OCTO_BF16 || dst_dtype == OCTO_F16 || dst_dtype == OCTO_F32, "rows_scatter: dst dtype");
+  if (n_max == 0 || d == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(src && idx && dst, "rows_scatter: null pointer");
+  OCTO_CHECK_ARG(n_max <= 0x7fffffff, "rows_scatter: too many rows");
+  hipLaunchKernelGGL(rows_scatter_kernel, dim3((unsigned)n_max), dim3(256), 0, (hipStream_t)stream, src, ld_src,
+                     src_dtype, idx, count, n_max, d, dst, ld_dst, dst_dtype, accumulate);
+  OCTO_CHECK_LAUNCH("rows_scatter");
+  return OCTO_OK;
+}
+
+int octo_gather_f32(const float *src, int64_t ld_src, const int64_t *idx, const int32_t *count, int64_t n_max,
+                    float *out, void *stream) {
+  OCTO_CHECK_ARG(n_max >= 0, "gather_f32: bad shape");
+  if (n_max == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(src && idx && out, "gather_f32: null pointer");
+  hipLaunchKernelGGL(gather_f32_kernel, dim3((unsigned)cdiv(n_max, 256)), dim3(256), 0, (hipStream_t)stream, src,
+                     ld_src, idx, count, n_max, out);
+  OCTO_CHECK_LAUNCH("gather_f32");
+  return OCTO_OK;
+}
+
+int octo_grpo_workspace_bytes(size_t *bytes) {
+  OCTO_CHECK_ARG(bytes != nullptr, "grpo_workspace_bytes: null pointer");
+  *bytes = 256;
+  return OCTO_OK;
+}
+
+int octo_grpo_grad(const float *logp, const float *prox, const float *old, const float *adv, const float *mask,
+                   int64_t n, float eps_lo, float eps_hi, float reject_upper, float *g, float *loss, void *ws,
+                   size_t ws_bytes, void *stream) {
+  OCTO_CHECK_ARG(n >= 0, "grpo_grad: n < 0");
+  if (ws_bytes < 256 || ws == nullptr) return octo_fail(OCTO_EWORKSPACE, "grpo_grad: workspace needs 256 bytes");
+  OCTO_CHECK_ARG(n == 0 || (logp && adv && mask && g), "grpo_grad: null pointer");
+  hipLaunchKernelGGL(grpo_count_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, mask, n, (float *)ws, loss);
+  if (n > 0)
+    hipLaunchKernelGGL(grpo_grad_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream, logp, prox,
+                       old, adv, mask, n, eps_lo, eps_hi, reject_upper, (const float *)ws, g, loss);
+  OCTO_CHECK_LAUNCH("grpo_grad");
+  return OCTO_OK;
+}
+
+}  // extern "C"

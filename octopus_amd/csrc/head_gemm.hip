@@ -1,0 +1,323 @@
+// GEMM kernels of the LM-head path, each the MFMA mainloop of gemm_nt.h with a fused epilogue:
+//
+//   gemm_stats : S^T = W . H^T tile -> per (row, vocab tile) online softmax statistics (m, S, U)
+//                (forward; octopus/rl/lm_head.py:102-112 without the [rows, V] logits)
+//   gemm_dz    : the same tile recomputed -> dz = g (onehot - p) / T * post'(z), written as bf16 in
+//                the row-major [tokens, V] layout and/or the vocab-major [V, tokens] layout
+//                (backward recompute, lm_head.py:118-121 under checkpoint)
+//   gemm_store : plain C = A . B^T with fp32/bf16/f16 output, optionally accumulated
+//                (grad_h = dz . W, grad_W = dz^T . h)
+//
+// Orientation: the first operand (MFMA "A", tile rows) of gemm_stats / gemm_dz is the vocabulary,
+// the second (tile columns) the tokens. In the 32x32 MFMA output layout a lane holds one column
+// and 16 rows, so each lane holds 64 vocabulary entries of each of its 4 tokens and the softmax
+// reductions over the vocabulary are almost entirely in registers: one lane-pair exchange (rows
+// split across lane halves) and one LDS exchange between the two waves that share the tokens.
+#include "gemm_nt.h"
+#include "octo_internal.h"
+
+namespace octo {
+
+// ---- epilogue: online softmax statistics ----------------------------------------------------
+
+// acc *= per-vocab-row scale (fp8 weights), then the softcap tanh if any; then stats per token.
+template <bool A_FP8, bool TANH>
+__device__ __forceinline__ void pre_transform(f32x16 (&acc)[4][4], int64_t m0, int wm, int lane,
+                                              const float *wscale, int64_t V, float pre) {
+  if constexpr (A_FP8) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float sc[16];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        int64_t row = m0 + acc_row(wm, i, 4 * g4, lane);
+        if (row + 3 < V) {
+          f32x4 q = *(const f32x4 *)(wscale + row);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) sc[4 * g4 + u] = q[u];
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) sc[4 * g4 + u] = (row + u < V) ? wscale[row + u] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] *= sc[v];
+    }
+  }
+  if constexpr (TANH) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = ftanh(pre * acc[i][j][v]);
+  }
+}
+
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+
+template <bool MASK>
+__device__ __forceinline__ void stats_cols(f32x16 (&acc)[4][4], int64_t m0, int wm, int wn, int lane,
+                                           int64_t V, float c, lds_f32x4 *red) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const bool ok = !MASK || (m0 + acc_row(wm, i, v, lane) < V);
+        if (ok) mx = fmaxf(mx, acc[i][j][v]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m2 = mx * c;
+    float S = 0.f, U = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float t = __builtin_fmaf(acc[i][j][v], c, -m2);
+        float e = fexp2(t);
+        if (MASK) {
+          const bool ok = m0 + acc_row(wm, i, v, lane) < V;
+          e = ok ? e : 0.f;
+        }
+        S += e;
+        U = __builtin_fmaf(e, t, U);
+      }
+    S += __shfl_xor(S, 32, 64);
+    U += __shfl_xor(U, 32, 64);
+    if (lane < 32) {
+      f32x4 o;
+      o[0] = m2; o[1] = S; o[2] = U; o[3] = 0.f;
+      red[wm * 256 + acc_col(wn, j, lane)] = o;
+    }
+  }
+}
+
+template <int DT, bool A_FP8, bool TANH>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_stats_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
+  lds_char *smem = (lds_char *)smem_;
+  int mt, nt;
+  if (!tile_of(s, mt, nt)) return;
+  const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
+  const int64_t nvalid = dev_count(s.count, s.count_off + n0, s.N - n0);
+  if (nvalid <= 0) return;
+
+  f32x16 acc[4][4];
+  mainloop<DT, A_FP8>(A, B, m0, n0, s.K, smem, acc);
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  pre_transform<A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+  lds_f32x4 *red = (lds_f32x4 *)smem;
+  if (m0 + TM > e.V) stats_cols<true>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  else stats_cols<false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < nvalid) {
+    const f32x4 a = red[t], b = red[256 + t];
+    Stat3 sa{a[0], a[1], a[2]}, sb{b[0], b[1], b[2]};
+    Stat3 r = stat_merge(sa, sb);
+    f32x4 o;
+    o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
+    e.part[(n0 + t) * e.mtiles + mt] = o;
+  }
+}
+
+// ---- epilogue: dz recompute ------------------------------------------------------------------
+
+template <int DT, bool A_FP8, bool TANH>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_dz_kernel(Operand A, Operand B, GemmShape s, DzArgs e) {
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
+  lds_char *smem = (lds_char *)smem_;
+  int mt, nt;
+  if (!tile_of(s, mt, nt)) return;
+  const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
+  const int64_t nvalid = dev_count(s.count, s.count_off + n0, s.N - n0);
+  if (nvalid <= 0) return;
+
+  f32x16 acc[4][4];
+  mainloop<DT, A_FP8>(A, B, m0, n0, s.K, smem, acc);
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  if constexpr (A_FP8) pre_transform<true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int col = acc_col(wn, j, lane);
+    const int64_t tk = n0 + col;          // token within this pass
+    const bool tok_ok = col < nvalid;
+    const int64_t r = e.row_off + tk;     // compact row
+    float lse2 = 0.f, gs = 0.f;
+    int64_t y = -1;
+    if (tok_ok) {
+      lse2 = e.lse[r] * OCTO_LOG2E;
+      gs = e.g[r] * e.gmul;
+      y = e.labels[e.label_idx ? e.label_idx[r] : r];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int64_t row0 = m0 + acc_row(wm, i, 4 * g4, lane);
+        float d[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int v = 4 * g4 + u;
+          const int64_t row = row0 + u;
+          float x = acc[i][j][v];
+          float dd;
+          if constexpr (TANH) {
+            const float th = ftanh(e.pre * x);
+            const float p = fexp2(__builtin_fmaf(th, e.c, -lse2));
+            dd = gs * ((row == y ? 1.f : 0.f) - p) * (1.f - th * th);
+          } else {
+            const float p = fexp2(__builtin_fmaf(x, e.c, -lse2));
+            dd = gs * ((row == y ? 1.f : 0.f) - p);
+          }
+          if constexpr (A_FP8) dd *= (row < e.V) ? e.wscale[row] : 0.f;
+          d[u] = (row < e.V && tok_ok) ? dd : 0.f;
+        }
+        typedef typename Elem<DT>::T DzT;
+        typedef DzT DzT4 __attribute__((ext_vector_type(4)));
+        if (e.dzA) {
+          DzT4 pk;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) pk[u] = (DzT)d[u];
+          *(DzT4 *)((DzT *)e.dzA + tk * e.ldA + row0) = pk;
+        }
+        if (e.dzB) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) ((DzT *)e.dzB)[(row0 + u) * e.ldB + tk] = (DzT)d[u];
+        }
+      }
+    }
+  }
+}
+
+// ---- epilogue: plain store -------------------------------------------------------------------
+
+template <typename OT, bool ACC, bool EDGE>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], OT *C, int64_t ldc, int64_t m0, int64_t n0,
+                                           int64_t mvalid, int64_t nvalid, int wm, int wn, int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int rr = acc_row(wm, i, v, lane);
+      if (EDGE && rr >= mvalid) continue;
+      OT *crow = C + (m0 + rr) * ldc + n0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cc = acc_col(wn, j, lane);
+        if (EDGE && cc >= nvalid) continue;
+        float x = acc[i][j][v];
+        if (ACC) x += (float)crow[cc];
+        crow[cc] = (OT)x;
+      }
+    }
+}
+
+template <typename OT>
+__device__ __forceinline__ void store_any(const f32x16 (&acc)[4][4], void *C, int64_t ldc, int64_t m0, int64_t n0,
+                                          int64_t mvalid, int64_t nvalid, int accumulate) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  const bool edge = mvalid < TM || nvalid < TN;
+  OT *c = (OT *)C;
+  if (accumulate) {
+    if (edge) store_tile<OT, true, true>(acc, c, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    else store_tile<OT, true, false>(acc, c, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+  } else {
+    if (edge) store_tile<OT, false, true>(acc, c, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    else store_tile<OT, false, false>(acc, c, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+  }
+}
+
+template <int DT, int OT>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
+  lds_char *smem = (lds_char *)smem_;
+  int mt, nt;
+  if (!tile_of(s, mt, nt)) return;
+  const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
+  int64_t mvalid = s.M - m0, nvalid = s.N - n0, K_eff = s.K;
+  if (s.count_on == 1) mvalid = dev_count(s.count, s.count_off + m0, mvalid);
+  if (s.count_on == 3) K_eff = round_up(dev_count(s.count, s.count_off, s.K), 64);
+  if (mvalid <= 0 || nvalid <= 0) return;
+
+  f32x16 acc[4][4];
+  mainloop<DT, false>(A, B, m0, n0, K_eff, smem, acc);
+  store_any<typename Elem<OT>::T>(acc, e.C, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
+}
+
+// ---- host launchers ----------------------------------------------------------------------------
+
+static inline dim3 grid_of(const GemmShape &s) { return dim3((unsigned)((int64_t)s.mtiles * s.ntiles)); }
+
+template <int DT, bool F8, bool TH>
+static int go_stats(const Operand &A, const Operand &B, const GemmShape &s, const StatsArgs &e, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_stats_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
+  OCTO_CHECK_LAUNCH("gemm_stats");
+  return OCTO_OK;
+}
+template <int DT, bool F8, bool TH>
+static int go_dz(const Operand &A, const Operand &B, const GemmShape &s, const DzArgs &e, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_dz_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
+  OCTO_CHECK_LAUNCH("gemm_dz");
+  return OCTO_OK;
+}
+
+int launch_gemm_stats(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
+                      const StatsArgs &e, hipStream_t st) {
+  if (a_fp8) {
+    if (dt != OCTO_BF16) return octo_fail(OCTO_EUNSUPPORTED, "fp8 weights need bf16 hidden rows");
+    return tanh ? go_stats<OCTO_BF16, true, true>(A, B, s, e, st) : go_stats<OCTO_BF16, true, false>(A, B, s, e, st);
+  }
+  switch (dt) {
+    case OCTO_BF16: return tanh ? go_stats<OCTO_BF16, false, true>(A, B, s, e, st) : go_stats<OCTO_BF16, false, false>(A, B, s, e, st);
+    case OCTO_F16: return tanh ? go_stats<OCTO_F16, false, true>(A, B, s, e, st) : go_stats<OCTO_F16, false, false>(A, B, s, e, st);
+    case OCTO_F32: return tanh ? go_stats<OCTO_F32, false, true>(A, B, s, e, st) : go_stats<OCTO_F32, false, false>(A, B, s, e, st);
+  }
+  return octo_fail(OCTO_EUNSUPPORTED, "gemm_stats: dtype %d", dt);
+}
+
+int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
+                   const DzArgs &e, hipStream_t st) {
+  if (a_fp8) {
+    if (dt != OCTO_BF16) return octo_fail(OCTO_EUNSUPPORTED, "fp8 weights need bf16 hidden rows");
+    return tanh ? go_dz<OCTO_BF16, true, true>(A, B, s, e, st) : go_dz<OCTO_BF16, true, false>(A, B, s, e, st);
+  }
+  switch (dt) {
+    case OCTO_BF16: return tanh ? go_dz<OCTO_BF16, false, true>(A, B, s, e, st) : go_dz<OCTO_BF16, false, false>(A, B, s, e, st);
+    case OCTO_F16: return tanh ? go_dz<OCTO_F16, false, true>(A, B, s, e, st) : go_dz<OCTO_F16, false, false>(A, B, s, e, st);
+    case OCTO_F32: return tanh ? go_dz<OCTO_F32, false, true>(A, B, s, e, st) : go_dz<OCTO_F32, false, false>(A, B, s, e, st);
+  }
+  return octo_fail(OCTO_EUNSUPPORTED, "gemm_dz: dtype %d", dt);
+}
+
+template <int DT>
+static int go_store(const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e, hipStream_t st) {
+  switch (e.dtype) {
+    case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
+  }
+  OCTO_CHECK_LAUNCH("gemm_store");
+  return OCTO_OK;
+}
+
+int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
+                      hipStream_t st) {
+  switch (dt) {
+    case OCTO_BF16: return go_store<OCTO_BF16>(A, B, s, e, st);
+    case OCTO_F16: return go_store<OCTO_F16>(A, B, s, e, st);
+    case OCTO_F32: return go_store<OCTO_F32>(A, B, s, e, st);
+  }
+  return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: dtype %d", dt);
+}
+
+}  // namespace octo

@@ -1,0 +1,82 @@
+// Internal interfaces between the C ABI (head_abi.hip) and the kernel translation units.
+#pragma once
+
+#include "octo_common.h"
+
+namespace octo {
+
+struct Operand;
+struct GemmShape;
+
+// gemm_stats epilogue arguments: part[row * mtiles + mt] = (m, S, U) of row over vocab tile mt.
+struct StatsArgs {
+  f32x4 *part;
+  int64_t mtiles;
+  int64_t V;
+  const float *wscale;  // per-vocab-row scale (fp8 weights) or NULL
+  float c;              // base-2 softmax scale of the (transformed) logit
+  float pre;            // tanh argument scale (softcap)
+};
+
+// gemm_dz epilogue arguments (tokens are pass-local; compact row = row_off + token).
+struct DzArgs {
+  void *dzA;  // [tokens, ldA] vocabulary contiguous, staged MFMA type, or NULL
+  int64_t ldA;
+  void *dzB;  // [V_pad, ldB] tokens contiguous, staged MFMA type, or NULL
+  int64_t ldB;
+  const float *lse;
+  const float *g;
+  const int64_t *labels;
+  const int64_t *label_idx;  // labels[label_idx[r]] when set
+  int64_t row_off;
+  int64_t V;
+  const float *wscale;
+  float c, pre, gmul;
+};
+
+struct StoreArgs {
+  void *C;
+  int64_t ldc;  // elements
+  int dtype;
+  int accumulate;
+};
+
+int launch_gemm_stats(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
+                      const StatsArgs &e, hipStream_t st);
+int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
+                   const DzArgs &e, hipStream_t st);
+int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
+                      hipStream_t st);
+
+// ---- small kernels (head_aux.hip) ---------------------------------------------------------------
+struct MergeArgs {
+  const f32x4 *part;
+  int64_t mtiles;
+  const void *h;
+  int64_t ldh;  // elements
+  int h_dtype;
+  const void *w;
+  int64_t ldw;  // elements
+  int w_dtype;
+  const float *wscale;
+  const int64_t *labels;
+  const int64_t *idx;
+  const int32_t *count;
+  int64_t n_max;
+  int d;
+  int64_t V;
+  int flags;
+  float inv_T, pre, post;
+  int use_tanh;
+  float *logp, *ent, *lse, *out2;
+  int64_t ld_out2;
+};
+int launch_merge(const MergeArgs &a, hipStream_t st);
+
+// dst[c * ld_dst + r] = src row r, element c, for r < rows_pad, c < cols; rows r >= valid read 0.
+// Source row r is row map[r] (or r) of src; dst holds the staged MFMA type (bf16/f16/f32).
+int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *src_scale,
+                     const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
+                     int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st);
+
+}  // namespace octo

@@ -1,0 +1,336 @@
+"""PyTorch custom ops over libocto_head.so: the fused LM-head logprob path on HIP tensors.
+
+    octohead::head_fwd / head_bwd      the fused head (GEMM + online softmax epilogue; recompute backward)
+    octohead::columns_fwd / columns_bwd  _head_columns over materialised logits
+    octohead::pairs_expand / pairs_grad  tree_head_output's pair -> flat expansion
+    octohead::grpo_loss                the GRPO objective's value and dL/dlogp per token
+
+Each op is registered for the "cuda" device type only (HIP tensors on ROCm): a CPU tensor has no kernel
+here and raises. All work is queued on the current stream; nothing synchronises with the host.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import NamedTuple, Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_DT = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32,
+       torch.float8_e4m3fn: _lib.FP8E4M3}
+
+
+class Post(NamedTuple):
+    """Post-head logit transform z' = post * tanh(pre * z) (tanh) or post * pre * z."""
+    pre: float = 1.0
+    post: float = 1.0
+    tanh: bool = False
+
+
+def _p(t: Optional[Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _dtype_code(t: Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise NotImplementedError(f"octohead: dtype {t.dtype} has no HIP kernel") from None
+
+
+def _rows2d(x: Tensor) -> Tensor:
+    if x.dim() != 2:
+        raise ValueError(f"octohead: expected [rows, d], got {tuple(x.shape)}")
+    if x.stride(1) != 1 or (x.stride(0) * x.element_size()) % 16 or x.data_ptr() % 16:
+        x = x.contiguous()
+    return x
+
+
+def _index(t: Optional[Tensor]) -> Optional[Tensor]:
+    if t is None:
+        return None
+    return t.to(torch.int64).contiguous()
+
+
+def _workspace(nbytes: int, like: Tensor) -> Tensor:
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=like.device)
+
+
+# ---- fused head ---------------------------------------------------------------------------------
+
+@torch.library.custom_op("octohead::head_fwd", mutates_args=(), device_types="cuda")
+def head_fwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Tensor, idx: Optional[Tensor],
+             count: Optional[Tensor], inv_T: float, pre: float, post: float, use_tanh: bool,
+             labels_via_idx: bool, scatter: bool) -> tuple[Tensor, Tensor]:
+    """(out, lse): out [n, 2] fp32 = (logprob, entropy) per compact row (n = len(idx) or rows), or
+    [rows, 2] with each compact row written at idx[r] and zeros elsewhere (scatter); lse [n] fp32."""
+    rows, weight = _rows2d(rows), _rows2d(weight)
+    labels, idx = _index(labels), _index(idx)
+    n_max = idx.numel() if idx is not None else rows.shape[0]
+    V, d = weight.shape
+    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | (_lib.OUT_SCATTER if scatter else 0)
+    out = torch.zeros(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32, device=rows.device)
+    lse = torch.zeros(n_max, dtype=torch.float32, device=rows.device)
+    if n_max == 0:
+        return out, lse
+    w_code = _dtype_code(weight)
+    ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, 0), rows)
+    _lib.call("octo_head_fwd", _p(rows), rows.shape[0], rows.stride(0), _dtype_code(rows),
+              _p(weight), weight.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
+              n_max, d, V, flags, inv_T, pre, post, int(use_tanh),
+              None, None, _p(lse), _p(out), 2, _p(ws), ws.numel(), _stream(rows))
+    return out, lse
+
+
+@head_fwd.register_fake
+def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, labels_via_idx, scatter):
+    n_max = idx.shape[0] if idx is not None else rows.shape[0]
+    out = rows.new_empty(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32)
+    return out, rows.new_empty(n_max, dtype=torch.float32)
+
+
+@torch.library.custom_op("octohead::head_bwd", mutates_args=(), device_types="cuda")
+def head_bwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Tensor, idx: Optional[Tensor],
+             count: Optional[Tensor], lse: Tensor, g: Tensor, inv_T: float, pre: float, post: float,
+             use_tanh: bool, labels_via_idx: bool, need_rows: bool, need_weight: bool) -> tuple[Tensor, Tensor]:
+    """(grad_rows [rows, d] in rows' dtype, grad_weight [V, d] in weight's dtype) for g = dL/dlogprob per
+    compact row; an output not asked for is an empty tensor."""
+    rows2, weight2 = _rows2d(rows), _rows2d(weight)
+    labels, idx = _index(labels), _index(idx)
+    n_max = idx.numel() if idx is not None else rows2.shape[0]
+    V, d = weight2.shape
+    grad_rows = torch.zeros_like(rows) if need_rows else rows.new_empty(0)
+    grad_w = weight.new_empty(0)
+    if n_max == 0 or not (need_rows or need_weight):
+        if need_weight:
+            grad_w = torch.zeros_like(weight)
+        return grad_rows, grad_w
+    w_code = _dtype_code(weight2)
+    flags = _lib.ROWS_VIA_IDX if labels_via_idx else 0
+    ws_flags = _lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW)
+    ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, ws_flags), rows2)
+    gh = None
+    if need_rows:
+        # compact-order rows; scattered (runs of equal idx summed) into grad_rows below
+        gh = grad_rows if idx is None else torch.empty(n_max, d, dtype=rows2.dtype, device=rows2.device)
+    gw32 = torch.empty(V, d, dtype=torch.float32, device=rows2.device) if need_weight else None
+    _lib.call("octo_head_bwd", _p(rows2), rows2.shape[0], rows2.stride(0), _dtype_code(rows2),
+              _p(weight2), weight2.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
+              n_max, d, V, flags, inv_T, pre, post, int(use_tanh), _p(lse.contiguous()),
+              _p(g.contiguous()), _p(gh), d, _dtype_code(rows2) if need_rows else _lib.F32, _p(gw32),
+              _p(ws), ws.numel(), _stream(rows2))
+    if need_rows and idx is not None:
+        _lib.call("octo_rows_scatter", _p(gh), d, _dtype_code(gh), _p(idx), _p(count), n_max, d,
+                  _p(grad_rows), grad_rows.stride(0), _dtype_code(grad_rows), 0, _stream(rows2))
+    if need_weight:
+        grad_w = gw32 if weight.dtype == torch.float32 else gw32.to(weight.dtype)
+    return grad_rows, grad_w
+
+
+@head_bwd.register_fake
+def _(rows, weight, w_scale, labels, idx, count, lse, g, inv_T, pre, post, use_tanh, labels_via_idx,
+      need_rows, need_weight):
+    return (torch.empty_like(rows) if need_rows else rows.new_empty(0),
+            torch.empty_like(weight) if need_weight else weight.new_empty(0))
+
+
+def _head_setup(ctx, inputs, output):
+    rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, labels_via_idx, scatter = inputs
+    ctx.save_for_backward(rows, weight, w_scale, labels, idx, count, output[1])
+    ctx.params = (inv_T, pre, post, use_tanh, labels_via_idx, scatter)
+
+
+def _head_backward(ctx, gout, _glse):
+    rows, weight, w_scale, labels, idx, count, lse = ctx.saved_tensors
+    inv_T, pre, post, use_tanh, labels_via_idx, scatter = ctx.params
+    need_rows, need_weight = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    if need_weight and weight.dtype == torch.float8_e4m3fn:
+        raise NotImplementedError("octohead: no gradient for fp8 weights")
+    gout = gout.float()
+    if scatter:  # g of compact row r is the output gradient at its hidden row idx[r]
+        col = gout[:, 0].contiguous()
+        g = torch.empty(idx.numel(), dtype=torch.float32, device=gout.device)
+        _lib.call("octo_gather_f32", _p(col), 1, _p(idx.to(torch.int64).contiguous()), _p(count), idx.numel(),
+                  _p(g), _stream(gout))
+    else:
+        g = gout[:, 0].contiguous()
+    grad_rows, grad_w = head_bwd(rows, weight, w_scale, labels, idx, count, lse, g, inv_T, pre, post, use_tanh,
+                                 labels_via_idx, need_rows, need_weight)
+    return (grad_rows if need_rows else None, grad_w if need_weight else None,
+            None, None, None, None, None, None, None, None, None, None)
+
+
+torch.library.register_autograd("octohead::head_fwd", _head_backward, setup_context=_head_setup)
+
+
+def fused_head(rows: Tensor, weight: Tensor, labels: Tensor, temperature: float, post: Post = Post(), *,
+               idx: Optional[Tensor] = None, count: Optional[Tensor] = None, labels_via_idx: bool = False,
+               scatter: bool = False, w_scale: Optional[Tensor] = None) -> Tensor:
+    """[n, 2] (logprob, entropy) of rows[idx] (or all rows) against weight, differentiable in rows and weight;
+    with scatter, a [rows, 2] tensor holding each compact row at idx[r] and 0 elsewhere."""
+    if temperature <= 0:
+        raise ValueError("temperature must be positive")
+    out, _ = head_fwd(rows, weight, w_scale, labels, idx, count, 1.0 / float(temperature), float(post.pre),
+                      float(post.post), bool(post.tanh), labels_via_idx, scatter)
+    return out
+
+
+# ---- _head_columns over materialised logits ------------------------------------------------------
+
+@torch.library.custom_op("octohead::columns_fwd", mutates_args=(), device_types="cuda")
+def columns_fwd(logits: Tensor, labels: Tensor, inv_T: float) -> tuple[Tensor, Tensor]:
+    logits = _rows2d(logits)
+    labels = _index(labels)
+    n, V = logits.shape
+    out = torch.empty(n, 2, dtype=torch.float32, device=logits.device)
+    lse = torch.empty(n, dtype=torch.float32, device=logits.device)
+    _lib.call("octo_columns_fwd", _p(logits), logits.stride(0), _dtype_code(logits), _p(labels), n, V, inv_T,
+              _p(out), _p(lse), _stream(logits))
+    return out, lse
+
+
+@columns_fwd.register_fake
+def _(logits, labels, inv_T):
+    return logits.new_empty(logits.shape[0], 2, dtype=torch.float32), logits.new_empty(logits.shape[0],
+                                                                                        dtype=torch.float32)
+
+
+@torch.library.custom_op("octohead::columns_bwd", mutates_args=(), device_types="cuda")
+def columns_bwd(logits: Tensor, labels: Tensor, inv_T: float, lse: Tensor, g: Tensor) -> Tensor:
+    logits = _rows2d(logits)
+    labels = _index(labels)
+    n, V = logits.shape
+    dl = torch.empty_like(logits)
+    for r0 in range(0, n, 65535):
+        r1 = min(n, r0 + 65535)
+        _lib.call("octo_columns_bwd", _p(logits[r0:r1]), logits.stride(0), _dtype_code(logits), _p(labels[r0:r1]),
+                  r1 - r0, V, inv_T, _p(lse[r0:r1].contiguous()), _p(g[r0:r1].contiguous()), _p(dl[r0:r1]),
+                  dl.stride(0), _stream(logits))
+    return dl
+
+
+@columns_bwd.register_fake
+def _(logits, labels, inv_T, lse, g):
+    return torch.empty_like(logits)
+
+
+def _columns_setup(ctx, inputs, output):
+    logits, labels, inv_T = inputs
+    ctx.save_for_backward(logits, labels, output[1])
+    ctx.inv_T = inv_T
+
+
+def _columns_backward(ctx, gout, _glse):
+    logits, labels, lse = ctx.saved_tensors
+    g = gout[:, 0].float().contiguous()  # the entropy column is detached
+    return columns_bwd(logits, labels, ctx.inv_T, lse, g), None, None
+
+
+torch.library.register_autograd("octohead::columns_fwd", _columns_backward, setup_context=_columns_setup)
+
+
+def head_columns(logits: Tensor, temperature: float, labels: Tensor) -> Tensor:
+    return columns_fwd(logits, labels, 1.0 / float(temperature))[0]
+
+
+# ---- pair expansion ------------------------------------------------------------------------------
+
+@torch.library.custom_op("octohead::pairs_expand", mutates_args=(), device_types="cuda")
+def pairs_expand(pairs: Tensor, flat_pair: Tensor) -> Tensor:
+    pairs = pairs.float().contiguous()
+    fp = _index(flat_pair)
+    P, C = pairs.shape
+    out = torch.empty(fp.numel(), C, dtype=torch.float32, device=pairs.device)
+    _lib.call("octo_pairs_expand", _p(pairs), P, C, _p(fp), fp.numel(), _p(out), _stream(pairs))
+    return out
+
+
+@pairs_expand.register_fake
+def _(pairs, flat_pair):
+    return pairs.new_empty(flat_pair.shape[0], pairs.shape[1], dtype=torch.float32)
+
+
+@torch.library.custom_op("octohead::pairs_grad", mutates_args=(), device_types="cuda")
+def pairs_grad(grad: Tensor, flat_pair: Tensor, P: int) -> Tensor:
+    grad = grad.float().contiguous()
+    fp = _index(flat_pair)
+    T, C = grad.shape
+    out = torch.empty(P, C, dtype=torch.float32, device=grad.device)
+    _lib.call("octo_pairs_grad", _p(grad), T, C, _p(fp), P, _p(out), _stream(grad))
+    return out
+
+
+@pairs_grad.register_fake
+def _(grad, flat_pair, P):
+    return grad.new_empty(P, grad.shape[1], dtype=torch.float32)
+
+
+def _pairs_setup(ctx, inputs, output):
+    pairs, flat_pair = inputs
+    ctx.save_for_backward(flat_pair)
+    ctx.P = pairs.shape[0]
+
+
+def _pairs_backward(ctx, gout):
+    (flat_pair,) = ctx.saved_tensors
+    return pairs_grad(gout, flat_pair, ctx.P), None
+
+
+torch.library.register_autograd("octohead::pairs_expand", _pairs_backward, setup_context=_pairs_setup)
+
+
+# ---- masked-row compaction -----------------------------------------------------------------------
+
+def compact_rows(mask: Tensor) -> tuple[Tensor, Tensor]:
+    """(idx [n] int64, count [1] int32): idx[:count] = positions of the true entries, ascending, as
+    mask.nonzero()[:, 0]; count stays on the device (no host synchronisation)."""
+    m = mask.reshape(-1)
+    if m.dtype != torch.bool and m.dtype != torch.uint8:
+        m = m != 0
+    m = m.contiguous().view(torch.uint8)
+    idx = torch.empty(m.numel(), dtype=torch.int64, device=m.device)
+    count = torch.empty(1, dtype=torch.int32, device=m.device)
+    _lib.call("octo_compact_rows", _p(m), m.numel(), _p(idx), _p(count), _stream(m))
+    return idx, count
+
+
+# ---- GRPO objective ------------------------------------------------------------------------------
+
+@torch.library.custom_op("octohead::grpo_loss", mutates_args=(), device_types="cuda")
+def grpo_loss(logp: Tensor, prox: Optional[Tensor], old: Optional[Tensor], adv: Tensor, mask: Tensor,
+              eps_lo: float, eps_hi: float, reject_upper: float) -> tuple[Tensor, Tensor]:
+    """(loss [] fp32, g [n] fp32 = dloss/dlogp)."""
+    f = lambda t: None if t is None else t.float().contiguous().reshape(-1)  # noqa: E731
+    logp_, prox_, old_, adv_, mask_ = f(logp), f(prox), f(old), f(adv), f(mask)
+    n = logp_.numel()
+    g = torch.empty(n, dtype=torch.float32, device=logp.device)
+    loss = torch.empty((), dtype=torch.float32, device=logp.device)
+    ws = _workspace(_lib.grpo_workspace_bytes(), logp_)
+    _lib.call("octo_grpo_grad", _p(logp_), _p(prox_), _p(old_), _p(adv_), _p(mask_), n, eps_lo, eps_hi,
+              reject_upper, _p(g), _p(loss), _p(ws), ws.numel(), _stream(logp_))
+    return loss, g.reshape(logp.shape)
+
+
+@grpo_loss.register_fake
+def _(logp, prox, old, adv, mask, eps_lo, eps_hi, reject_upper):
+    return logp.new_empty((), dtype=torch.float32), torch.empty_like(logp, dtype=torch.float32)
+
+
+def _grpo_setup(ctx, inputs, output):
+    ctx.save_for_backward(output[1])
+    ctx.dtype = inputs[0].dtype
+
+
+def _grpo_backward(ctx, gloss, _gg):
+    (g,) = ctx.saved_tensors
+    return (g * gloss).to(ctx.dtype), None, None, None, None, None, None, None
+
+
+torch.library.register_autograd("octohead::grpo_loss", _grpo_backward, setup_context=_grpo_setup)

@@ -1,0 +1,81 @@
+"""The C ABI without a GPU: the library loads, exports every function include/octo_head.h declares, the
+ctypes table binds exactly those, and argument checks return their status before anything is queued."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from octopus_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "octo_head.h")
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    return set(re.findall(r"^\s*(?:int|const char \*)\s*(octo_\w+)\s*\(", text, flags=re.M))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared()
+    assert len(declared) >= 14
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert declared == set(_lib.SIGNATURES), declared ^ set(_lib.SIGNATURES)
+    assert lib.octo_version().startswith(b"octo_head")
+
+
+def test_workspace_query():
+    V, d = 151936, 2560
+    fwd = _lib.workspace_bytes(32768, d, V, _lib.BF16, 0)
+    assert fwd >= 32768 * ((V + 255) // 256) * 16
+    bwd = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_BACKWARD)
+    no_gw = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_BACKWARD | _lib.WS_NO_GRADW)
+    Vp = (V + 255) // 256 * 256
+    assert bwd >= d * Vp * 2 + 2 * 32768 * Vp * 2 + d * 32768 * 2
+    assert no_gw < bwd
+    with pytest.raises(ValueError):
+        _lib.workspace_bytes(-1, d, V, _lib.BF16, 0)
+
+
+P = ctypes.c_void_p(256)  # never dereferenced: every call below fails its host-side checks first
+
+
+def _fwd(**kw):
+    a = dict(h=P, h_rows=10, ldh=64, h_dtype=_lib.BF16, w=P, ldw=64, w_dtype=_lib.BF16, w_scale=None, labels=P,
+             idx=None, count=None, n_max=10, d=64, V=100, flags=0, inv_T=1.0, pre=1.0, post=1.0, tanh=0,
+             ws=None, ws_bytes=0)
+    a.update(kw)
+    _lib.call("octo_head_fwd", a["h"], a["h_rows"], a["ldh"], a["h_dtype"], a["w"], a["ldw"], a["w_dtype"],
+              a["w_scale"], a["labels"], a["idx"], a["count"], a["n_max"], a["d"], a["V"], a["flags"], a["inv_T"],
+              a["pre"], a["post"], a["tanh"], None, None, None, None, 2, a["ws"], a["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("kw,exc", [
+    (dict(d=60, ldh=60, ldw=60), ValueError),                      # d not a multiple of 8
+    (dict(h_dtype=_lib.F16), NotImplementedError),                 # hidden / weight dtypes differ
+    (dict(w_dtype=_lib.FP8E4M3, h_dtype=_lib.F32), NotImplementedError),
+    (dict(w_dtype=_lib.FP8E4M3), ValueError),                      # fp8 without scales
+    (dict(inv_T=0.0), ValueError),
+    (dict(pre=-1.0), ValueError),
+    (dict(flags=_lib.OUT_SCATTER), ValueError),                    # scatter without idx
+    (dict(h_rows=5), ValueError),                                  # fewer hidden rows than n_max
+    (dict(), ValueError),                                          # no workspace
+    (dict(h_dtype=7, w_dtype=7), NotImplementedError),
+], ids=["d", "dtypes", "fp8-f32", "fp8-noscale", "T", "scale", "scatter", "rows", "workspace", "dtype"])
+def test_head_fwd_argument_checks(kw, exc):
+    with pytest.raises(exc):
+        _fwd(**kw)
+    assert _lib.last_error()
+
+
+def test_small_entry_point_checks():
+    with pytest.raises(ValueError):
+        _lib.call("octo_compact_rows", P, -1, P, P, None)
+    with pytest.raises(ValueError):
+        _lib.call("octo_columns_fwd", P, 10, _lib.BF16, P, 4, 100, 1.0, P, None, None)  # ld < V
+    with pytest.raises(ValueError):
+        _lib.call("octo_grpo_grad", P, None, None, P, P, 4, 0.2, 0.28, 5.0, P, None, None, 0, None)
+    assert _lib.grpo_workspace_bytes() >= 4

@@ -1,0 +1,196 @@
+"""Parity of the HIP path (through the C ABI, via octopus_amd.head_op) with the oracle.
+
+Small shapes: every output against the fp64 oracle on the same inputs (the bf16 inputs rounded first), at
+logprob / entropy 1e-5 abs (fp32) and 2e-3 abs (bf16/f16); gradients relative
+Frobenius error 1e-2 (bf16), 1e-4 (fp32); compaction and target gathers bit-exact.
+Full-size configurations: all rows on the GPU, the oracle on a seeded subsample of rows, and a chunked
+fp32 torch reference on the GPU for the gradients (which depend on every row)."""
+
+import numpy as np
+import pytest
+import torch
+
+from octopus_amd import head_op
+from octopus_amd.head_op import Post, fused_head
+from oracle import grpo as ogrpo
+from oracle import head as ohead
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _inputs(n, d, V, dtype, seed=0, T_rows=None):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(T_rows or n, d, generator=g)
+    h = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype)
+    W = (torch.randn(V, d, generator=g) * (0.02 if dtype != torch.float32 else 0.05)).to(dtype)
+    y = torch.randint(0, V, (T_rows or n,), generator=g)
+    return h, W, y
+
+
+def _tol(dtype):
+    return 1e-5 if dtype == torch.float32 else 2e-3
+
+
+def _rel(a, b):
+    return ((a.double() - b.double()).norm() / b.double().norm()).item()
+
+
+SHAPES = [(1, 64, 100), (300, 64, 1000), (513, 256, 5000), (256, 40, 777), (1000, 128, 2048), (70, 2560, 3000)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{n}x{d}x{V}" for n, d, V in SHAPES])
+def test_forward_matches_oracle(dtype, shape):
+    n, d, V = shape
+    h, W, y = _inputs(n, d, V, dtype)
+    for T, post in ((1.0, Post()), (0.7, Post(0.5, 2.0, True)), (1.3, Post(0.25, 1.0, False))):
+        out = fused_head(h.to(DEV), W.to(DEV), y.to(DEV), T, post).cpu()
+        lp, ent, _ = ohead.head_forward(h, W, y, T, post.pre, post.post, post.tanh)
+        tol = _tol(dtype)
+        assert (out[:, 0].double() - lp).abs().max() <= tol, (T, post)
+        assert (out[:, 1].double() - ent).abs().max() <= tol, (T, post)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(300, 64, 1000), (513, 256, 5000), (256, 40, 777)], ids=str)
+def test_backward_matches_oracle(dtype, shape):
+    n, d, V = shape
+    h, W, y = _inputs(n, d, V, dtype, seed=1)
+    g = torch.randn(n, generator=torch.Generator().manual_seed(9))
+    for T, post in ((1.0, Post()), (0.7, Post(0.5, 2.0, True))):
+        hd = h.to(DEV).requires_grad_(True)
+        Wd = W.to(DEV).requires_grad_(True)
+        out = fused_head(hd, Wd, y.to(DEV), T, post)
+        (out[:, 0] * g.to(DEV)).sum().backward()
+        gh, gw = ohead.head_backward(h, W, y, T, g, post.pre, post.post, post.tanh)
+        bar = 1e-4 if dtype == torch.float32 else 1e-2
+        assert _rel(hd.grad.cpu(), gh) <= bar and _rel(Wd.grad.cpu(), gw) <= bar, (T, post)
+
+
+def test_compaction_is_bit_exact_nonzero():
+    rng = np.random.default_rng(0)
+    for n in (1, 63, 64, 65, 1023, 1024, 1025, 32768, 131072 + 7):
+        m = torch.from_numpy(rng.random(n) < rng.random()).to(DEV)
+        idx, count = head_op.compact_rows(m)
+        ref = torch.nonzero(m)[:, 0]
+        assert int(count.item()) == ref.numel()
+        assert torch.equal(idx[:ref.numel()], ref)
+
+
+def test_scored_rows_equal_the_unscored_rows_bitwise():
+    n, d, V = 777, 128, 3000
+    h, W, y = _inputs(n, d, V, torch.bfloat16, seed=2)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    scored = torch.rand(n, generator=torch.Generator().manual_seed(3)) < 0.45
+    idx, count = head_op.compact_rows(scored.to(DEV))
+    full = fused_head(hd, Wd, yd, 0.7)
+    part = fused_head(hd, Wd, yd, 0.7, idx=idx, count=count, labels_via_idx=True, scatter=True)
+    s = scored.to(DEV)
+    assert torch.equal(part[s], full[s]) and (part[~s] == 0).all()
+    # gradients of a loss over the scored rows equal the unscored head's
+    w = torch.randn(n, generator=torch.Generator().manual_seed(4)).to(DEV) * s
+    grads = []
+    for kw in (dict(), dict(idx=idx, count=count, labels_via_idx=True, scatter=True)):
+        a = hd.clone().requires_grad_(True)
+        b = Wd.clone().requires_grad_(True)
+        (fused_head(a, b, yd, 0.7, **kw)[:, 0] * w).sum().backward()
+        grads.append((a.grad, b.grad))
+    assert torch.equal(grads[0][0], grads[1][0])
+    assert _rel(grads[1][1].float(), grads[0][1].float()) < 1e-6
+
+
+def test_pair_gather_and_expansion_match_the_reference_composition():
+    """tree_head_output with the fused pair gather equals index_select + head + expansion (reference
+    prefix_tree.py:419-421), values and gradients."""
+    from octopus_amd.rl.prefix_tree import TreeMeta, build_tree, tree_head_output
+    rng = np.random.default_rng(5)
+    prefix = rng.integers(0, 500, 300)
+    seqs = [np.concatenate([prefix, rng.integers(0, 500, k)]) for k in (40, 90, 7, 64)]
+    flat = np.concatenate(seqs)
+    cu = [0, *np.cumsum([len(s) for s in seqs]).tolist()]
+    scored = rng.random(len(flat)) < 0.6
+    meta = TreeMeta(build_tree(flat, cu, scored=scored), DEV)
+    d, V = 64, 500
+    h, W, _ = _inputs(meta.n_tokens, d, V, torch.float32, seed=6)
+    hd = h.to(DEV)[None].requires_grad_(True)
+    Wd = W.to(DEV).requires_grad_(True)
+
+    def chunk(rows, labels):
+        return fused_head(rows, Wd, labels, 0.9)
+
+    chunk.octopus_fused_rows = lambda h2, pos, y: fused_head(h2, Wd, y, 0.9, idx=pos)
+    out = tree_head_output(chunk, hd, meta)
+    gw = torch.randn(out.shape, generator=torch.Generator().manual_seed(7)).to(DEV)
+    (out * gw).sum().backward()
+    g_fused = (hd.grad.clone(), Wd.grad.clone())
+    hd.grad, Wd.grad = None, None
+    pairs = fused_head(hd[0].index_select(0, meta.pair_pos), Wd, meta.pair_label, 0.9)
+    ref = torch.cat([pairs, pairs.new_zeros(1, 2)]).index_select(0, meta.flat_pair)[None]
+    (ref * gw).sum().backward()
+    assert torch.equal(out, ref)
+    assert _rel(g_fused[0], hd.grad) < 1e-6 and _rel(g_fused[1], Wd.grad) < 1e-6
+    # the pairs themselves against the oracle
+    lp, ent, _ = ohead.head_forward(h[meta.pair_pos.cpu()], W, meta.pair_label.cpu(), 0.9)
+    assert (pairs[:, 0].detach().cpu().double() - lp).abs().max() < 1e-5
+
+
+def test_bound_head_on_a_model_matches_its_own_logits():
+    """Reference tests/test_lm_head.py:11-34 on the GPU, through the fused HIP head (fp32, atol 1e-5)."""
+    from transformers import AutoModelForCausalLM, Gemma2Config, LlamaConfig
+    from octopus_amd.rl.lm_head import bind_head
+    small = dict(vocab_size=96, hidden_size=32, intermediate_size=64, num_hidden_layers=2, num_attention_heads=2,
+                 num_key_value_heads=1, head_dim=16)
+    for config in (LlamaConfig(**small), Gemma2Config(**small, final_logit_softcapping=2.0)):
+        torch.manual_seed(0)
+        model = AutoModelForCausalLM.from_config(config, attn_implementation="eager").eval().to(DEV)
+        ids = torch.randint(0, 96, (1, 12), device=DEV)
+        labels = torch.roll(ids, -1, -1).reshape(-1)
+        with torch.no_grad():
+            own = model(input_ids=ids).logits[0].float()
+        for T in (1.0, 0.7):
+            head = bind_head(model, T)
+            head.octopus_labels, head.octopus_tree = labels, None
+            with torch.no_grad():
+                out = model(input_ids=ids).logits[0]
+            logp = torch.log_softmax(own / T, -1)
+            assert torch.allclose(out[:, 0], logp.gather(-1, labels[:, None])[:, 0], atol=1e-5)
+            assert torch.allclose(out[:, 1], -(logp.exp() * logp).sum(-1), atol=1e-5)
+
+
+def test_head_columns_hip_matches_eager():
+    """Reference tests/test_seq_tiles.py:145-165 for _head_columns: the HIP kernel against its eager twin."""
+    from octopus_amd.rl import lm_head
+    torch.manual_seed(0)
+    logits = torch.randn(64, 1000, device=DEV, dtype=torch.bfloat16)
+    labels = torch.randint(0, 1000, (64,), device=DEV)
+    outs, grads = [], []
+    for f in (lm_head._head_columns, lm_head._head_columns._torchdynamo_orig_callable):
+        x = logits.detach().clone().float().requires_grad_() if f is not lm_head._head_columns else \
+            logits.detach().clone().requires_grad_()
+        out = f(x, 1.0, labels)
+        out[:, 0].float().pow(2).sum().backward()
+        outs.append(out.float())
+        grads.append(x.grad.float())
+    assert (outs[0] - outs[1]).abs().max() <= 2e-3
+    assert (grads[0] - grads[1]).norm() <= 2e-2 * grads[1].norm() + 1e-6
+
+
+def test_grpo_matches_oracle():
+    rng = np.random.default_rng(8)
+    n = 5000
+    logp = np.log(rng.uniform(0.01, 1.0, n))
+    prox = logp + rng.normal(0, 0.2, n)
+    old = prox + rng.normal(0, 1.0, n)
+    adv = rng.normal(0, 1, n)
+    mask = (rng.random(n) < 0.7).astype(np.float32)
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=DEV)  # noqa: E731
+    for kw in (dict(prox=prox, old=old), dict(old=old), dict(prox=prox)):
+        loss, g = head_op.grpo_loss(t(logp), None if "prox" not in kw else t(kw["prox"]),
+                                    None if "old" not in kw else t(kw["old"]), t(adv), t(mask), 0.2, 0.28, 5.0)
+        # the oracle on the same fp32-rounded inputs
+        f = lambda a: np.asarray(a, dtype=np.float32).astype(np.float64)  # noqa: E731
+        ref_loss, ref_g = ogrpo.grpo(f(logp), f(adv), mask, prox=None if "prox" not in kw else f(kw["prox"]),
+                                     old=None if "old" not in kw else f(kw["old"]))
+        assert abs(loss.item() - ref_loss) < 1e-4 * max(1.0, abs(ref_loss))
+        assert np.abs(g.cpu().numpy() - ref_g).max() < 1e-6
