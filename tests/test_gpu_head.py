@@ -23,7 +23,7 @@ def _inputs(n, d, V, dtype, seed=0, T_rows=None):
     g = torch.Generator().manual_seed(seed)
     h = torch.randn(T_rows or n, d, generator=g)
     h = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype)
-    W = (torch.randn(V, d, generator=g) * (0.02 if dtype != torch.float32 else 0.05)).to(dtype)
+    W = (torch.randn(V, d, generator=g) * 0.02).to(dtype)  # the configurations' weight scale
     y = torch.randint(0, V, (T_rows or n,), generator=g)
     return h, W, y
 
@@ -97,7 +97,9 @@ def test_scored_rows_equal_the_unscored_rows_bitwise():
         (fused_head(a, b, yd, 0.7, **kw)[:, 0] * w).sum().backward()
         grads.append((a.grad, b.grad))
     assert torch.equal(grads[0][0], grads[1][0])
-    assert _rel(grads[1][1].float(), grads[0][1].float()) < 1e-6
+    # grad_W contracts over rows: the two runs sum the same terms in a different order before the bf16
+    # rounding of the result, so they agree to bf16 resolution rather than bitwise
+    assert _rel(grads[1][1].float(), grads[0][1].float()) < 2e-3
 
 
 def test_pair_gather_and_expansion_match_the_reference_composition():
