@@ -54,6 +54,12 @@ _lock = threading.Lock()
 def load(path: str = LIB_PATH) -> ctypes.CDLL:
     """The loaded library with every signature bound. Raises RuntimeError when it has not been built."""
     global _lib
+    # torch first: the library binds libamdhip64 by soname, so in a torch process it must resolve to the
+    # HIP runtime torch already loaded (one runtime per process)
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     with _lock:
         if _lib is None:
             if not os.path.exists(path):

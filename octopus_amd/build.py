@@ -1,8 +1,9 @@
 """Build libocto_head.so (the gfx950 HIP kernels and their C ABI) in-tree with hipcc.
 
-    python -m octopus_amd.build [--verbose]
+    python -m octopus_amd.build [--verbose] [--resources]
 
-The library lands next to this file, so it travels with the source tree; nothing is installed.
+Each translation unit compiles to its own object in parallel, then one link. The library lands next to this
+file, so it travels with the source tree; nothing is installed.
 """
 
 from __future__ import annotations
@@ -11,7 +12,9 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 import time
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -21,7 +24,7 @@ ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 generation (the host pass warns it does not know the
 # feature; that warning is harmless). -munsafe-fp-atomics: hardware fp32 atomic add.
-FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-munsafe-fp-atomics", "-Wno-unused-result"]
 
@@ -33,21 +36,34 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm under /opt/rocm)")
 
 
-def build(verbose: bool = False, extra: list[str] | None = None) -> str:
-    """Compile every source into LIB (always recompiles) and return its path."""
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *FLAGS, *(extra or []), "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]]
-    t0 = time.time()
+def _run(cmd: list[str]) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
-    out = "\n".join(line for line in (res.stdout + res.stderr).splitlines()
-                    if "packed-fp32-ops" not in line)
+    out = "\n".join(line for line in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in line)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{out}")
-    os.replace(tmp, LIB)
+    return out
+
+
+def build(verbose: bool = False, extra: list[str] | None = None, out: str = LIB) -> str:
+    """Compile every source and link `out` (always recompiles). Returns its path."""
+    t0 = time.time()
+    cc = hipcc()
+    with tempfile.TemporaryDirectory(prefix="octo_build_") as tmp:
+        objs = [os.path.join(tmp, s.replace(".hip", ".o")) for s in SOURCES]
+        cmds = [[cc, *FLAGS, *(extra or []), "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+        with ThreadPoolExecutor(len(cmds)) as pool:
+            logs = list(pool.map(_run, cmds))
+        linked = os.path.join(tmp, "lib.so")
+        logs.append(_run([cc, *FLAGS, "-shared", *objs, "-o", linked]))
+        shutil.copyfile(linked, out + ".tmp")
+        os.chmod(out + ".tmp", 0o755)
+        os.replace(out + ".tmp", out)
     if verbose:
-        print(out)
-        print(f"built {LIB} in {time.time() - t0:.1f} s")
-    return LIB
+        text = "\n".join(x for x in logs if x.strip())
+        if text:
+            print(text)
+        print(f"built {out} in {time.time() - t0:.1f} s")
+    return out
 
 
 if __name__ == "__main__":

@@ -54,20 +54,26 @@ struct GemmShape {
   int64_t count_off;
 };
 
-// Block -> (mt, nt). Returns false for blocks past the tile count.
+// Block -> (mt, nt). Blocks run on XCD b % 8. M-tiles are dealt to the XCDs round-robin (XCD x owns
+// mt = x, x + 8, ...), so a device-side count that idles a suffix of M-tiles idles them evenly on every
+// XCD; each XCD walks its own M-tiles in groups of group_m across all N-tiles, so the ~32 workgroups
+// resident on an XCD share a few A and B K-slices in its L2. The grid is 8 * (tiles of the largest
+// XCD); blocks past their XCD's tiles return false.
+__host__ __device__ inline int64_t tile_grid(int mtiles, int ntiles) {
+  return 8 * ((int64_t)((mtiles + 7) / 8) * ntiles);
+}
 __device__ __forceinline__ bool tile_of(const GemmShape &s, int &mt, int &nt) {
-  const int64_t total = (int64_t)s.mtiles * s.ntiles;
   const int64_t b = blockIdx.x;
-  if (b >= total) return false;
-  const int64_t x = b & 7, k = b >> 3;
-  const int64_t q = total >> 3, r = total & 7;
-  const int64_t t = x * q + (x < r ? x : r) + k;
+  const int x = (int)(b & 7);
+  const int64_t k = b >> 3;
+  const int64_t mx = (s.mtiles - x + 7) / 8;  // M-tiles owned by XCD x
+  if (k >= mx * s.ntiles) return false;
   const int64_t span = (int64_t)s.group_m * s.ntiles;
-  const int64_t gid = t / span;
+  const int64_t gid = k / span;
   const int64_t first = gid * s.group_m;
-  const int64_t gsize = (s.mtiles - first) < s.group_m ? (s.mtiles - first) : s.group_m;
-  const int64_t local = t - gid * span;
-  mt = (int)(first + local % gsize);
+  const int64_t gsize = (mx - first) < s.group_m ? (mx - first) : s.group_m;
+  const int64_t local = k - gid * span;
+  mt = (int)(x + 8 * (first + local % gsize));
   nt = (int)(local / gsize);
   return true;
 }
@@ -232,6 +238,166 @@ __device__ __forceinline__ void mainloop(const Operand &A, const Operand &B, int
     }
     __syncthreads();
   }
+}
+
+// ---- direct-to-LDS mainloop -----------------------------------------------------------------------
+//
+// K advances 64 bytes per stage (32 bf16 / 16 fp32). The A and B slices of a stage (256 rows x 64 B each,
+// 32 KB together) are written straight into LDS by buffer_load_dwordx4 ... lds: each wave instruction
+// moves 1 KB, lane i's 16 bytes landing at the instruction's LDS base + 16 i, so the LDS layout is chosen
+// by which global chunk each lane fetches. Four stages form a ring (128 KB); the DMA for stage k + 4 is
+// issued in iteration k, three stages ahead of its use, so global latency is covered by ~3 stages of MFMA
+// work. One bare s_barrier per stage (no memory fence: the waits are explicit) separates "stage k + 1
+// landed in every wave" and "every wave has read stage k" from the DMA that overwrites stage k's buffer.
+//
+// LDS row layout (64-byte rows, 4 chunks of 16 bytes): chunk c of row r sits at physical chunk
+// c ^ f(r), f(r) = ((r >> 1) ^ (r >> 3)) & 3, which keeps the fragment reads of 8 consecutive lanes
+// (rows r..r+7, same c) on distinct 16-byte bank groups of a 128-byte bank window and those of 16
+// consecutive lanes distinct within a 256-byte window.
+constexpr int DKB = 64;                    // K bytes per stage
+constexpr int DSTAGE = 2 * 256 * DKB;      // A + B bytes per stage (32 KB)
+constexpr int DNSTAGE = 4;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at bits 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int WAIT_LGKM0 = 15 | (3 << 14) | (7 << 4);
+
+#ifndef OCTO_SWZ
+#define OCTO_SWZ 2
+#endif
+__device__ __forceinline__ int swz64(int r) {
+  if (OCTO_SWZ == 1) return (r >> 1) & 3;
+  if (OCTO_SWZ == 2) return (r >> 2) & 3;
+  if (OCTO_SWZ == 3) return 0;
+  return ((r >> 1) ^ (r >> 3)) & 3;
+}
+
+// Per-thread DMA sources of one operand: instruction q (0..3) of wave w fills LDS rows
+// (4 q + w) * 16 .. +16; lane i takes row + (i >> 2) and physical chunk i & 3.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_rows(const Operand &op, int64_t row0, uint32_t (&off)[4],
+                                                           uint32_t (&coff)[4]) {
+  const int w = threadIdx.x >> 6, i = threadIdx.x & 63;
+  const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
+  uint32_t rowoff[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (4 * q + w) * 16 + (i >> 2);
+    coff[q] = (uint32_t)(((i & 3) ^ swz64(r)) << 4);
+    if (r < valid) rowoff[q] = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
+    else rowoff[q] = 0x80000000u;
+    off[q] = rowoff[q] + coff[q];
+  }
+  if (op.map) return make_rsrc(uniform_ptr(op.base), op.extent);
+  return make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
+}
+
+__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[4],
+                                          const uint32_t (&coff)[4], uint32_t kb, uint32_t kbytes,
+                                          lds_char *dst) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t o = (kb + coff[q] < kbytes) ? off[q] + kb : 0x80000000u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(dst + (4 * q + w) * 1024),
+                                             16, o, 0, 0, 0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void mfma_block(const i32x4 (&af)[4], const i32x4 (&bf)[4], f32x16 (&acc)[4][4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) Mfma<DT>::run(af[i], bf[j], acc[i][j]);
+}
+
+__device__ __forceinline__ void read_frags(const lds_char *s, int aoff, int boff, i32x4 (&af)[4], i32x4 (&bf)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) af[i] = *(const lds_i32x4 *)(s + aoff + i * 32 * DKB);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) bf[j] = *(const lds_i32x4 *)(s + boff + j * 32 * DKB);
+}
+
+// smem: DNSTAGE * DSTAGE bytes; stage s at s * DSTAGE, A rows first then B rows.
+template <int DT>
+__device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B, int64_t m0, int64_t n0, int64_t K_eff,
+                                             lds_char *smem, f32x16 (&acc)[4][4]) {
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  constexpr int ebytes = (DT == OCTO_F32) ? 4 : 2;
+  const uint32_t kbytes = (uint32_t)(K_eff * ebytes);
+  const int nk = (int)((kbytes + DKB - 1) / DKB);
+  if (nk == 0) return;
+
+  uint32_t offa[4], offb[4], ca[4], cb[4];
+  const __amdgpu_buffer_rsrc_t rsa = dma_rows(A, m0, offa, ca);
+  const __amdgpu_buffer_rsrc_t rsb = dma_rows(B, n0, offb, cb);
+
+  const int f = swz64(lane);
+  int aoff[2], boff[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int pc = ((2 * ks + (lane >> 5)) ^ f) << 4;
+    aoff[ks] = (wm * 128 + (lane & 31)) * DKB + pc;
+    boff[ks] = 256 * DKB + (wn * 128 + (lane & 31)) * DKB + pc;
+  }
+
+#pragma unroll
+  for (int s = 0; s < DNSTAGE; ++s) {
+    dma_stage(rsa, offa, ca, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE);
+    dma_stage(rsb, offb, cb, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE + 256 * DKB);
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 * (DNSTAGE - 1)));
+  __builtin_amdgcn_s_barrier();
+
+  // scheduling groups (__builtin_amdgcn_sched_group_barrier masks): MFMA 0x8, VMEM read 0x20, DS read 0x100
+  constexpr int NMF = (DT == OCTO_F32) ? 64 : 16;  // MFMA instructions per 16-byte-fragment block
+  i32x4 a0[4], b0[4], a1[4], b1[4];
+  read_frags(smem, aoff[0], boff[0], a0, b0);
+  for (int k = 0; k < nk; ++k) {
+    const lds_char *cur = smem + (k & (DNSTAGE - 1)) * DSTAGE;
+    // half 1: fragments of sub-step 1 read under the MFMAs of sub-step 0
+    read_frags(cur, aoff[1], boff[1], a1, b1);
+    mfma_block<DT>(a0, b0, acc);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF / 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NMF / 2, 0);
+    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);                       // this wave's reads of stage k are done
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 * (DNSTAGE - 2)));    // stage k + 1 landed (this wave's part)
+    __builtin_amdgcn_s_barrier();                                 // ... in every wave; stage k is free
+    // half 2: refill stage k's buffer four stages ahead and read sub-step 0 of stage k + 1 under the
+    // MFMAs of sub-step 1
+    lds_char *refill = smem + (k & (DNSTAGE - 1)) * DSTAGE;
+    const uint32_t kb = (uint32_t)(k + DNSTAGE) * DKB;
+    dma_stage(rsa, offa, ca, kb, kbytes, refill);
+    dma_stage(rsb, offb, cb, kb, kbytes, refill + 256 * DKB);
+    const lds_char *nxt = smem + ((k + 1) & (DNSTAGE - 1)) * DSTAGE;
+    read_frags(nxt, aoff[0], boff[0], a0, b0);
+    mfma_block<DT>(a1, b1, acc);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF / 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NMF / 16, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
+  __builtin_amdgcn_s_barrier();
 }
 
 // Row (M) and column (N) of accumulator element v of block (i, j), relative to the tile origin.

@@ -13,6 +13,8 @@
 // and 16 rows, so each lane holds 64 vocabulary entries of each of its 4 tokens and the softmax
 // reductions over the vocabulary are almost entirely in registers: one lane-pair exchange (rows
 // split across lane halves) and one LDS exchange between the two waves that share the tokens.
+#include <type_traits>
+
 #include "gemm_nt.h"
 #include "octo_internal.h"
 
@@ -98,7 +100,7 @@ __device__ __forceinline__ void stats_cols(f32x16 (&acc)[4][4], int64_t m0, int 
 }
 
 template <int DT, bool A_FP8, bool TANH>
-__global__ __launch_bounds__(NTHREADS, 1) void gemm_stats_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
+__global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stats_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
@@ -108,7 +110,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_stats_kernel(Operand A, Oper
   if (nvalid <= 0) return;
 
   f32x16 acc[4][4];
-  mainloop<DT, A_FP8>(A, B, m0, n0, s.K, smem, acc);
+  if constexpr (A_FP8) mainloop<DT, true>(A, B, m0, n0, s.K, smem, acc);
+  else mainloop_dma<DT>(A, B, m0, n0, s.K, smem, acc);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
   pre_transform<A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
@@ -128,9 +131,203 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_stats_kernel(Operand A, Oper
 }
 
 // ---- epilogue: dz recompute ------------------------------------------------------------------
+//
+// dz of the 256 (vocab) x 256 (token) tile is computed in place in the accumulators, packed to 16-bit
+// and written out through LDS (the 128 KB stage ring, free after the mainloop) in two passes, so that
+// both global layouts are written as whole 512-byte row segments with 16-byte stores:
+//   dzA [token][vocab]: each lane holds 4 consecutive vocab rows of one token -> one 8-byte LDS write;
+//   dzB [vocab][token]: a 4 x 4 transpose inside each lane quad (DPP quad_perm) gives each lane 4
+//                       consecutive tokens of one vocab row -> one 8-byte LDS write.
+// LDS rows are 512 bytes; the 8-byte slot index is XOR-swizzled so the 32 lanes of a half-wave hit
+// distinct banks, and the read-back of 16 bytes stays a contiguous (possibly half-swapped) slot pair.
+
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, bf16x2 *) {
+  bf16x2 p;
+  p[0] = (__bf16)lo;
+  p[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, p);
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, f16x2_t *) {
+  f16x2_t p;
+  p[0] = (_Float16)lo;
+  p[1] = (_Float16)hi;
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// quad lane exchanges (DPP quad_perm): swap with lane ^ 1, lane ^ 2
+__device__ __forceinline__ uint32_t quad_swap1(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint32_t quad_swap2(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, true);
+}
+
+// Stream a 256 x 512-byte LDS tile (rows stored with slot swizzle `s(row)` on 8-byte slots) to global
+// rows dst + row * ld_bytes, 16 bytes per thread per row-eighth.
+template <typename SWZ>
+__device__ __forceinline__ void lds_tile_to_global(const lds_char *tile, char *dst, int64_t ld_bytes, SWZ swz) {
+  const int t = threadIdx.x;
+  const int c16 = t & 31;
+#pragma unroll 4
+  for (int p = 0; p < 32; ++p) {
+    const int row = p * 8 + (t >> 5);
+    const int s = swz(row);
+    // logical slots 2c, 2c+1 sit at physical (2c ^ s, (2c+1) ^ s): one aligned 16-byte pair, its halves
+    // swapped when s is odd
+    i32x4 v = *(const lds_i32x4 *)(tile + row * 512 + ((2 * c16) ^ (s & ~1)) * 8);
+    if (s & 1) v = __builtin_shufflevector(v, v, 2, 3, 0, 1);
+    *(i32x4 *)(dst + row * ld_bytes + c16 * 16) = v;
+  }
+}
+
+// dz = g (onehot - p) / T * post'(z) of every tile element, in place (fp32), zero outside V and the
+// pass's valid tokens. The one-hot test compares the label, relative to this lane's first vocab row,
+// with each register's compile-time row offset.
+template <bool A_FP8, bool TANH>
+__device__ __forceinline__ void dz_in_place(f32x16 (&acc)[4][4], const DzArgs &e, int64_t m0, int64_t n0,
+                                            int64_t nvalid, int wm, int wn, int lane) {
+  const int64_t lane_row0 = m0 + wm * 128 + 4 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int col = acc_col(wn, j, lane);
+    const bool tok_ok = col < nvalid;
+    const int64_t r = e.row_off + n0 + col;  // compact row
+    float lse2 = 0.f, gs = 0.f;
+    int yrel = -1;
+    if (tok_ok) {
+      lse2 = e.lse[r] * OCTO_LOG2E;
+      gs = e.g[r] * e.gmul;
+      const int64_t y = e.labels[e.label_idx ? e.label_idx[r] : r] - lane_row0;
+      yrel = (y >= 0 && y < 256) ? (int)y : -1;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int roff = i * 32 + 8 * (v >> 2) + (v & 3);
+        const float hit = (yrel == roff) ? gs : 0.f;
+        const float x = acc[i][j][v];
+        if constexpr (TANH) {
+          const float th = ftanh(e.pre * x);
+          const float p = fexp2(__builtin_fmaf(th, e.c, -lse2));
+          acc[i][j][v] = __builtin_fmaf(-gs, p, hit) * (1.f - th * th);
+        } else {
+          const float p = fexp2(__builtin_fmaf(x, e.c, -lse2));
+          acc[i][j][v] = __builtin_fmaf(-gs, p, hit);
+        }
+      }
+  }
+  if constexpr (A_FP8) {  // d/d(raw e4m3 product) = dz * row scale
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = lane_row0 + i * 32 + 8 * (v >> 2) + (v & 3);
+        const float sc = row < e.V ? e.wscale[row] : 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j][v] *= sc;
+      }
+  }
+  if (m0 + TM > e.V || nvalid < TN) {  // edge tile: zero rows past V and tokens past the pass's count
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool tok_ok = acc_col(wn, j, lane) < nvalid;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const bool ok = tok_ok && (lane_row0 + i * 32 + 8 * (v >> 2) + (v & 3) < e.V);
+          acc[i][j][v] = ok ? acc[i][j][v] : 0.f;
+        }
+    }
+  }
+}
+
+// fp32 dz (fp32 inputs): direct 16-byte stores to dzA, 4-byte stores to dzB.
+__device__ __forceinline__ void dz_store_direct(const f32x16 (&acc)[4][4], const DzArgs &e, int64_t m0, int64_t n0,
+                                                int wm, int wn, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t tk = n0 + acc_col(wn, j, lane);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int64_t row0 = m0 + acc_row(wm, i, 4 * g4, lane);
+        if (e.dzA) {
+          f32x4 pk;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) pk[u] = acc[i][j][4 * g4 + u];
+          *(f32x4 *)((float *)e.dzA + tk * e.ldA + row0) = pk;
+        }
+        if (e.dzB) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) ((float *)e.dzB)[(row0 + u) * e.ldB + tk] = acc[i][j][4 * g4 + u];
+        }
+      }
+  }
+}
+
+// 16-bit dz through LDS (see the layout notes above).
+template <typename P2>
+__device__ __forceinline__ void dz_store_staged(const f32x16 (&acc)[4][4], const DzArgs &e, int64_t m0, int64_t n0,
+                                                int wm, int wn, int lane, lds_char *tile) {
+  if (e.dzA) {  // [token][vocab]
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tt = acc_col(wn, j, lane);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int slot = (acc_row(wm, i, 4 * g4, lane) >> 2) ^ (tt & 31);
+          i32x2 pk;
+          pk[0] = (int)pack2(acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], (P2 *)nullptr);
+          pk[1] = (int)pack2(acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3], (P2 *)nullptr);
+          *(lds_i32x2 *)(tile + tt * 512 + slot * 8) = pk;
+        }
+    }
+    __syncthreads();
+    lds_tile_to_global(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return row & 31; });
+    __syncthreads();
+  }
+  if (e.dzB) {  // [vocab][token]: 4 x 4 transpose inside each lane quad first
+    const int b = lane & 3;
+    const int rowsel = (b == 1) ? 2 : ((b == 2) ? 1 : b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int slot0 = (acc_col(wn, j, lane) & ~3) >> 2;  // 4-token slot of this quad
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const uint32_t w01 = pack2(acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], (P2 *)nullptr);
+          const uint32_t w23 = pack2(acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3], (P2 *)nullptr);
+          const uint32_t recv = quad_swap1((b & 1) ? w01 : w23);
+          // even lanes: rows r0, r0+1 of tokens (n, n+1); odd lanes: rows r0+2, r0+3 of tokens (n-1, n)
+          const uint32_t x = (b & 1) ? __builtin_amdgcn_perm(w23, recv, 0x05040100u)
+                                     : __builtin_amdgcn_perm(recv, w01, 0x05040100u);
+          const uint32_t y = (b & 1) ? __builtin_amdgcn_perm(w23, recv, 0x07060302u)
+                                     : __builtin_amdgcn_perm(recv, w01, 0x07060302u);
+          const uint32_t recv2 = quad_swap2((b & 2) ? x : y);
+          i32x2 pk;
+          pk[0] = (int)((b & 2) ? recv2 : x);
+          pk[1] = (int)((b & 2) ? y : recv2);
+          const int vr = acc_row(wm, i, 4 * g4, lane) + rowsel;
+          const int slot = slot0 ^ ((vr & 3) << 3);
+          *(lds_i32x2 *)(tile + vr * 512 + slot * 8) = pk;
+        }
+    }
+    __syncthreads();
+    lds_tile_to_global(tile, (char *)e.dzB + (m0 * e.ldB + n0) * 2, e.ldB * 2, [](int row) { return (row & 3) << 3; });
+  }
+}
 
 template <int DT, bool A_FP8, bool TANH>
-__global__ __launch_bounds__(NTHREADS, 1) void gemm_dz_kernel(Operand A, Operand B, GemmShape s, DzArgs e) {
+__global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_dz_kernel(Operand A, Operand B, GemmShape s, DzArgs e) {
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
@@ -140,61 +337,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_dz_kernel(Operand A, Operand
   if (nvalid <= 0) return;
 
   f32x16 acc[4][4];
-  mainloop<DT, A_FP8>(A, B, m0, n0, s.K, smem, acc);
+  if constexpr (A_FP8) mainloop<DT, true>(A, B, m0, n0, s.K, smem, acc);
+  else mainloop_dma<DT>(A, B, m0, n0, s.K, smem, acc);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
   if constexpr (A_FP8) pre_transform<true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int col = acc_col(wn, j, lane);
-    const int64_t tk = n0 + col;          // token within this pass
-    const bool tok_ok = col < nvalid;
-    const int64_t r = e.row_off + tk;     // compact row
-    float lse2 = 0.f, gs = 0.f;
-    int64_t y = -1;
-    if (tok_ok) {
-      lse2 = e.lse[r] * OCTO_LOG2E;
-      gs = e.g[r] * e.gmul;
-      y = e.labels[e.label_idx ? e.label_idx[r] : r];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int64_t row0 = m0 + acc_row(wm, i, 4 * g4, lane);
-        float d[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int v = 4 * g4 + u;
-          const int64_t row = row0 + u;
-          float x = acc[i][j][v];
-          float dd;
-          if constexpr (TANH) {
-            const float th = ftanh(e.pre * x);
-            const float p = fexp2(__builtin_fmaf(th, e.c, -lse2));
-            dd = gs * ((row == y ? 1.f : 0.f) - p) * (1.f - th * th);
-          } else {
-            const float p = fexp2(__builtin_fmaf(x, e.c, -lse2));
-            dd = gs * ((row == y ? 1.f : 0.f) - p);
-          }
-          if constexpr (A_FP8) dd *= (row < e.V) ? e.wscale[row] : 0.f;
-          d[u] = (row < e.V && tok_ok) ? dd : 0.f;
-        }
-        typedef typename Elem<DT>::T DzT;
-        typedef DzT DzT4 __attribute__((ext_vector_type(4)));
-        if (e.dzA) {
-          DzT4 pk;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) pk[u] = (DzT)d[u];
-          *(DzT4 *)((DzT *)e.dzA + tk * e.ldA + row0) = pk;
-        }
-        if (e.dzB) {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) ((DzT *)e.dzB)[(row0 + u) * e.ldB + tk] = (DzT)d[u];
-        }
-      }
-    }
+  dz_in_place<A_FP8, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
+  if constexpr (DT == OCTO_F32) {
+    dz_store_direct(acc, e, m0, n0, wm, wn, lane);
+  } else {
+    typedef typename std::conditional<DT == OCTO_BF16, bf16x2, f16x2_t>::type P2;
+    dz_store_staged<P2>(acc, e, m0, n0, wm, wn, lane, smem);
   }
 }
 
@@ -237,7 +390,7 @@ __device__ __forceinline__ void store_any(const f32x16 (&acc)[4][4], void *C, in
 }
 
 template <int DT, int OT>
-__global__ __launch_bounds__(NTHREADS, 1) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
+__global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
@@ -249,13 +402,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_store_kernel(Operand A, Oper
   if (mvalid <= 0 || nvalid <= 0) return;
 
   f32x16 acc[4][4];
-  mainloop<DT, false>(A, B, m0, n0, K_eff, smem, acc);
+  mainloop_dma<DT>(A, B, m0, n0, K_eff, smem, acc);
   store_any<typename Elem<OT>::T>(acc, e.C, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
 }
 
 // ---- host launchers ----------------------------------------------------------------------------
 
-static inline dim3 grid_of(const GemmShape &s) { return dim3((unsigned)((int64_t)s.mtiles * s.ntiles)); }
+static inline dim3 grid_of(const GemmShape &s) { return dim3((unsigned)tile_grid(s.mtiles, s.ntiles)); }
 
 template <int DT, bool F8, bool TH>
 static int go_stats(const Operand &A, const Operand &B, const GemmShape &s, const StatsArgs &e, hipStream_t st) {
