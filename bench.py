@@ -55,6 +55,35 @@ def cpu_baseline(cfg, scored_rows: int) -> dict:
                       f"{scored_rows} scored rows; extrapolated; host: {_cpu_model()}"}
 
 
+def library_gemms(workload: str, reps: int = 5) -> dict:
+    """torch.matmul (hipBLASLt) on the step's four contractions at the workload's scored-row count, bf16 in,
+    no epilogue: logits (twice: forward and recompute), dz . W and dz^T . h. Context for the fused kernels'
+    MFMA rates; these are not the path."""
+    from octopus_amd.workloads import CONFIGS
+    cfg = CONFIGS[workload]
+    dev = torch.device("cuda", 0)
+    n = sum(s for s, scored, _ in cfg.segments if scored)
+    g = torch.Generator(device=dev).manual_seed(0)
+    h = torch.randn(n, cfg.d, device=dev, dtype=torch.bfloat16, generator=g)
+    W = torch.randn(cfg.V, cfg.d, device=dev, dtype=torch.bfloat16, generator=g)
+    dz = torch.randn(n, cfg.V, device=dev, dtype=torch.bfloat16, generator=g)
+    flop = 2 * n * cfg.d * cfg.V
+    out = {"workload": workload, "rows": n, "flop_each": flop}
+    for name, f in (("logits W.h^T", lambda: W @ h.T), ("grad_h dz.W", lambda: dz @ W),
+                    ("grad_W dz^T.h", lambda: dz.T @ h)):
+        f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[name] = {"ms": ms, "tflops": flop / ms / 1e9}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -62,11 +91,28 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="cfg3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--hipblaslt", action="store_true",
+                    help="only time torch.matmul (hipBLASLt) on the four plain GEMMs of the workload's step, "
+                         "without any epilogue, for context; then exit")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB three times (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters against known bytes), then exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the LM-head path runs on a single MI355X here (no multi-GPU run)",
               file=sys.stderr)
         return 2
+    if args.copy_probe:
+        src = torch.ones(args.copy_probe << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4}), flush=True)
+        return 0
+    if args.hipblaslt:
+        print(json.dumps(library_gemms(args.workload)), flush=True)
+        return 0
 
     from octopus_amd import _lib, head_op
     from octopus_amd.workloads import CONFIGS, make_batch

@@ -4,10 +4,15 @@
 //
 // One workgroup = 256 threads = 4 wave64s computes a 256 x 256 tile of C; the waves sit 2 x 2 and
 // each owns a 128 x 128 sub-tile as 4 x 4 accumulators of v_mfma_f32_32x32x16_{bf16,f16}
-// (v_mfma_f32_32x32x2_f32 for fp32). K advances 128 bytes per step (64 bf16 / 32 fp32); the
-// A and B K-slices are staged through LDS, double buffered (2 x 64 KB), with the 16-byte chunks of
-// each 128-byte LDS row XOR-swizzled by (row & 7) so that the fragment reads of 8 consecutive lanes
-// (8 consecutive rows, same logical chunk) land on 8 distinct bank groups.
+// (v_mfma_f32_32x32x2_f32 for fp32), i.e. all 256 accumulation registers of a wave.
+//
+// Two mainloops feed the MFMAs from LDS:
+//   mainloop_dma  (every bf16 / f16 / f32 contraction): the A and B K-slices go straight from global memory
+//                 into a ring of LDS stages by buffer_load_dwordx4 ... lds (no register hop), with the
+//                 instruction order fixed in the source: fragment reads a sub-step ahead of their MFMAs and
+//                 the DMA issues spread one per two MFMAs;
+//   mainloop      (fp8 weights): register-staged, so that e4m3 bytes can be widened to bf16 on the way
+//                 into LDS; K advances 128 bytes per step, double buffered (2 x 64 KB).
 //
 // Global loads are raw buffer loads: rows past the operand's end and K chunks past K read as zero
 // (voffset >= 2^31 is out of range), so partial tiles need no branches in the loop. Operand rows can
@@ -15,9 +20,8 @@
 // into the GEMM.
 //
 // Workgroup -> tile: blocks are dealt to the 8 XCDs round-robin, so block b runs on XCD b % 8; each
-// XCD gets a contiguous range of the tile order, and the tile order walks groups of `group_m`
-// M-tiles across all N-tiles, so the ~32 workgroups resident on one XCD share a few A and B
-// K-slices in that XCD's L2.
+// XCD walks its own M-tiles in groups of `group_m` across all N-tiles, so the ~32 workgroups resident
+// on one XCD share a few A and B K-slices in that XCD's L2.
 #pragma once
 
 #include "octo_common.h"
@@ -29,7 +33,6 @@ constexpr int TN = 256;          // tile cols (N)
 constexpr int KB = 128;          // K bytes per step
 constexpr int NTHREADS = 256;
 constexpr int TILE_BYTES = 256 * KB;  // one operand K-slice in LDS: 32 KB
-constexpr int SMEM_BYTES = 4 * TILE_BYTES;
 
 typedef __attribute__((address_space(3))) char lds_char;
 typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
@@ -242,61 +245,73 @@ __device__ __forceinline__ void mainloop(const Operand &A, const Operand &B, int
 
 // ---- direct-to-LDS mainloop -----------------------------------------------------------------------
 //
-// K advances 64 bytes per stage (32 bf16 / 16 fp32). The A and B slices of a stage (256 rows x 64 B each,
-// 32 KB together) are written straight into LDS by buffer_load_dwordx4 ... lds: each wave instruction
-// moves 1 KB, lane i's 16 bytes landing at the instruction's LDS base + 16 i, so the LDS layout is chosen
-// by which global chunk each lane fetches. Four stages form a ring (128 KB); the DMA for stage k + 4 is
-// issued in iteration k, three stages ahead of its use, so global latency is covered by ~3 stages of MFMA
-// work. One bare s_barrier per stage (no memory fence: the waits are explicit) separates "stage k + 1
-// landed in every wave" and "every wave has read stage k" from the DMA that overwrites stage k's buffer.
+// K advances DKB bytes per stage (64: 32 bf16 / 16 fp32; 128: 64 bf16 / 32 fp32). The A and B slices of a
+// stage (256 rows x DKB bytes each) are written straight into LDS by buffer_load_dwordx4 ... lds: each
+// wave instruction moves 1 KB, lane i's 16 bytes landing at the instruction's LDS base + 16 i, so the LDS
+// layout is chosen by which global chunk each lane fetches (64 / (DKB / 16) whole rows per instruction).
+// DNSTAGE stages form a ring; the DMA for stage k + DNSTAGE is issued in iteration k, DNSTAGE - 1 stages
+// ahead of its use. One bare s_barrier per stage (no memory fence: the waits are explicit) separates
+// "stage k + 1 landed in every wave" and "every wave has read stage k" from the DMA that overwrites stage
+// k's buffer.
 //
-// LDS row layout (64-byte rows, 4 chunks of 16 bytes): chunk c of row r sits at physical chunk
-// c ^ f(r), f(r) = ((r >> 1) ^ (r >> 3)) & 3, which keeps the fragment reads of 8 consecutive lanes
-// (rows r..r+7, same c) on distinct 16-byte bank groups of a 128-byte bank window and those of 16
-// consecutive lanes distinct within a 256-byte window.
-constexpr int DKB = 64;                    // K bytes per stage
-constexpr int DSTAGE = 2 * 256 * DKB;      // A + B bytes per stage (32 KB)
-constexpr int DNSTAGE = 4;
+// LDS rows are DKB bytes of 16-byte chunks; chunk c of row r sits at physical chunk c ^ swz(r), which keeps
+// the fragment reads of consecutive lanes (consecutive rows, same logical chunk) on distinct bank groups.
+#ifndef OCTO_DKB
+#define OCTO_DKB 64
+#endif
+constexpr int DKB = OCTO_DKB;              // K bytes per stage
+constexpr int DSTAGE = 2 * 256 * DKB;      // A + B bytes per stage
+#ifndef OCTO_NSTAGE
+#define OCTO_NSTAGE (DKB == 64 ? 4 : 2)
+#endif
+constexpr int DNSTAGE = OCTO_NSTAGE;       // ring depth
+constexpr int DLPR = DKB / 16;             // lanes per row in one DMA instruction
+constexpr int DRPI = 64 / DLPR;            // rows per DMA instruction
+constexpr int DIPW = 256 / DRPI / 4;       // DMA instructions per wave per operand and stage
+constexpr int DNSUB = DKB / 32;            // 16-byte-fragment sub-steps per stage
+// LDS of one GEMM workgroup: the register-staged mainloop's 2 x (A + B) 32 KB slices or the DMA ring.
+constexpr int SMEM_BYTES = (4 * TILE_BYTES > DNSTAGE * DSTAGE) ? 4 * TILE_BYTES : DNSTAGE * DSTAGE;
+static_assert(DKB == 64 || DKB == 128, "stage width");
+static_assert(SMEM_BYTES <= 160 * 1024, "LDS budget");
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at bits 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int WAIT_LGKM0 = 15 | (3 << 14) | (7 << 4);
+static_assert(2 * DIPW * DNSTAGE <= 63, "vmcnt range");
 
-#ifndef OCTO_SWZ
-#define OCTO_SWZ 2
-#endif
-__device__ __forceinline__ int swz64(int r) {
-  if (OCTO_SWZ == 1) return (r >> 1) & 3;
-  if (OCTO_SWZ == 2) return (r >> 2) & 3;
-  if (OCTO_SWZ == 3) return 0;
-  return ((r >> 1) ^ (r >> 3)) & 3;
+// 64-byte rows: chunk c of row r at c ^ ((r >> 2) & 3), so the 8 lanes of a 128-byte LDS access (rows r0..r0+7
+// of one logical chunk: two rows per physical chunk index) cover all four chunk positions twice in two
+// different 64-byte halves of the bank space; 128-byte rows: c ^ (r & 7).
+__device__ __forceinline__ int swz_row(int r) {
+  if (DKB == 128) return r & 7;
+  return (r >> 2) & 3;
 }
 
-// Per-thread DMA sources of one operand: instruction q (0..3) of wave w fills LDS rows
-// (4 q + w) * 16 .. +16; lane i takes row + (i >> 2) and physical chunk i & 3.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_rows(const Operand &op, int64_t row0, uint32_t (&off)[4],
-                                                           uint32_t (&coff)[4]) {
+// Per-thread DMA sources of one operand: instruction q (0..DIPW-1) of wave w fills LDS rows
+// (4 q + w) * DRPI .. + DRPI; lane i takes row + i / DLPR and physical chunk i % DLPR.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_rows(const Operand &op, int64_t row0, uint32_t (&off)[DIPW],
+                                                           uint32_t (&coff)[DIPW]) {
   const int w = threadIdx.x >> 6, i = threadIdx.x & 63;
   const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
-  uint32_t rowoff[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int r = (4 * q + w) * 16 + (i >> 2);
-    coff[q] = (uint32_t)(((i & 3) ^ swz64(r)) << 4);
-    if (r < valid) rowoff[q] = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
-    else rowoff[q] = 0x80000000u;
-    off[q] = rowoff[q] + coff[q];
+  for (int q = 0; q < DIPW; ++q) {
+    const int r = (4 * q + w) * DRPI + i / DLPR;
+    coff[q] = (uint32_t)(((i % DLPR) ^ swz_row(r)) << 4);
+    uint32_t rowoff;
+    if (r < valid) rowoff = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
+    else rowoff = 0x80000000u;
+    off[q] = rowoff + coff[q];
   }
   if (op.map) return make_rsrc(uniform_ptr(op.base), op.extent);
   return make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
 }
 
-__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[4],
-                                          const uint32_t (&coff)[4], uint32_t kb, uint32_t kbytes,
+__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[DIPW],
+                                          const uint32_t (&coff)[DIPW], uint32_t kb, uint32_t kbytes,
                                           lds_char *dst) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < DIPW; ++q) {
     const uint32_t o = (kb + coff[q] < kbytes) ? off[q] + kb : 0x80000000u;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(dst + (4 * q + w) * 1024),
                                              16, o, 0, 0, 0);
@@ -318,10 +333,37 @@ __device__ __forceinline__ void read_frags(const lds_char *s, int aoff, int boff
   for (int j = 0; j < 4; ++j) bf[j] = *(const lds_i32x4 *)(s + boff + j * 32 * DKB);
 }
 
+// Fragment q (0..7) of a sub-step: A block q (q < 4) or B block q - 4.
+__device__ __forceinline__ void read_frag(const lds_char *s, int aoff, int boff, int q, i32x4 (&af)[4],
+                                          i32x4 (&bf)[4]) {
+  if (q < 4) af[q] = *(const lds_i32x4 *)(s + aoff + q * 32 * DKB);
+  else bf[q - 4] = *(const lds_i32x4 *)(s + boff + (q - 4) * 32 * DKB);
+}
+
+// One DMA instruction q (0..DIPW-1) of an operand slice (see dma_stage).
+__device__ __forceinline__ void dma_one(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t coff, uint32_t kb,
+                                        uint32_t kbytes, lds_char *dst, int q) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t o = (kb + coff < kbytes) ? off + kb : 0x80000000u;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(dst + (4 * q + w) * 1024),
+                                           16, o, 0, 0, 0);
+}
+
+// Instruction order is fixed in the source: a scheduling fence after every MFMA / load keeps the fragment
+// reads of the next sub-step early (so register allocation cannot fold them onto fragments still in use)
+// and spreads the DMA issues evenly between MFMAs.
+#define OCTO_FENCE() __builtin_amdgcn_sched_barrier(0)
+
 // smem: DNSTAGE * DSTAGE bytes; stage s at s * DSTAGE, A rows first then B rows.
+//
+// Stage j's A slice is issued right after the barrier that frees its slot (in iteration j - DNSTAGE), its
+// B slice under the first sub-step of the next iteration (into the slot stage j - DNSTAGE left), so the
+// 2 * DIPW DMA instructions of a stage are spread over two sub-steps. With a ring of 2 both slices go
+// after the barrier.
 template <int DT>
 __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B, int64_t m0, int64_t n0, int64_t K_eff,
                                              lds_char *smem, f32x16 (&acc)[4][4]) {
+  constexpr bool SPLIT = DNSTAGE >= 3;
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
@@ -337,64 +379,98 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
   const int nk = (int)((kbytes + DKB - 1) / DKB);
   if (nk == 0) return;
 
-  uint32_t offa[4], offb[4], ca[4], cb[4];
+  uint32_t offa[DIPW], offb[DIPW], ca[DIPW], cb[DIPW];
   const __amdgpu_buffer_rsrc_t rsa = dma_rows(A, m0, offa, ca);
   const __amdgpu_buffer_rsrc_t rsb = dma_rows(B, n0, offb, cb);
 
-  const int f = swz64(lane);
-  int aoff[2], boff[2];
+  const int f = swz_row(lane);
+  int aoff[DNSUB], boff[DNSUB];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int ks = 0; ks < DNSUB; ++ks) {
     const int pc = ((2 * ks + (lane >> 5)) ^ f) << 4;
     aoff[ks] = (wm * 128 + (lane & 31)) * DKB + pc;
     boff[ks] = 256 * DKB + (wn * 128 + (lane & 31)) * DKB + pc;
   }
 
+  if constexpr (SPLIT) {
 #pragma unroll
-  for (int s = 0; s < DNSTAGE; ++s) {
-    dma_stage(rsa, offa, ca, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE);
-    dma_stage(rsb, offb, cb, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE + 256 * DKB);
+    for (int s = 0; s < DNSTAGE - 1; ++s) {
+      dma_stage(rsa, offa, ca, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE);
+      dma_stage(rsb, offb, cb, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE + 256 * DKB);
+    }
+    dma_stage(rsa, offa, ca, (uint32_t)(DNSTAGE - 1) * DKB, kbytes, smem + (DNSTAGE - 1) * DSTAGE);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 2) + DIPW));
+  } else {
+#pragma unroll
+    for (int s = 0; s < DNSTAGE; ++s) {
+      dma_stage(rsa, offa, ca, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE);
+      dma_stage(rsb, offb, cb, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE + 256 * DKB);
+    }
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 1)));
   }
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 * (DNSTAGE - 1)));
   __builtin_amdgcn_s_barrier();
 
-  // scheduling groups (__builtin_amdgcn_sched_group_barrier masks): MFMA 0x8, VMEM read 0x20, DS read 0x100
-  constexpr int NMF = (DT == OCTO_F32) ? 64 : 16;  // MFMA instructions per 16-byte-fragment block
-  i32x4 a0[4], b0[4], a1[4], b1[4];
-  read_frags(smem, aoff[0], boff[0], a0, b0);
+  i32x4 fa[2][4], fb[2][4];
+  read_frags(smem, aoff[0], boff[0], fa[0], fb[0]);
+  int slot = 0;                 // k % DNSTAGE
+  int prev_slot = DNSTAGE - 1;  // (k - 1) % DNSTAGE
   for (int k = 0; k < nk; ++k) {
-    const lds_char *cur = smem + (k & (DNSTAGE - 1)) * DSTAGE;
-    // half 1: fragments of sub-step 1 read under the MFMAs of sub-step 0
-    read_frags(cur, aoff[1], boff[1], a1, b1);
-    mfma_block<DT>(a0, b0, acc);
+    const int next_slot = (slot + 1 == DNSTAGE) ? 0 : slot + 1;
+    const lds_char *cur = smem + slot * DSTAGE;
+    OCTO_FENCE();
+    // sub-steps 0 .. DNSUB - 2: read the next sub-step's fragments under the first 8 MFMAs
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NMF / 16, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    for (int sub = 0; sub + 1 < DNSUB; ++sub) {
+      const uint32_t kbB = (uint32_t)(k + DNSTAGE - 1) * DKB;
+      lds_char *dstB = smem + prev_slot * DSTAGE + 256 * DKB;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        Mfma<DT>::run(fa[sub & 1][q >> 2], fb[sub & 1][q & 3], acc[q >> 2][q & 3]);
+        OCTO_FENCE();
+        if (q < 8) {
+          read_frag(cur, aoff[sub + 1], boff[sub + 1], q, fa[(sub + 1) & 1], fb[(sub + 1) & 1]);
+          OCTO_FENCE();
+        } else if (SPLIT && sub == 0) {
+          // B slice of stage k + DNSTAGE - 1, DIPW instructions over MFMAs 8..15
+          constexpr int every = 8 / DIPW;
+          if ((q - 8) % every == every - 1) {
+            const int d = (q - 8) / every;
+            dma_one(rsb, offb[d], cb[d], kbB, kbytes, dstB, d);
+            OCTO_FENCE();
+          }
+        }
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, NMF / 2, 0);
-    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);                       // this wave's reads of stage k are done
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(8 * (DNSTAGE - 2)));    // stage k + 1 landed (this wave's part)
-    __builtin_amdgcn_s_barrier();                                 // ... in every wave; stage k is free
-    // half 2: refill stage k's buffer four stages ahead and read sub-step 0 of stage k + 1 under the
-    // MFMAs of sub-step 1
-    lds_char *refill = smem + (k & (DNSTAGE - 1)) * DSTAGE;
+    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);                                // this wave's reads of stage k are done
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 2)));     // stage k + 1 landed (this wave's part)
+    __builtin_amdgcn_s_barrier();                                          // ... in every wave; stage k is free
+    OCTO_FENCE();
+    // last sub-step: read the next stage's first fragments under the first 8 MFMAs, refill stage k's
+    // buffer (stage k + DNSTAGE) under the last 8
+    lds_char *refill = smem + slot * DSTAGE;
     const uint32_t kb = (uint32_t)(k + DNSTAGE) * DKB;
-    dma_stage(rsa, offa, ca, kb, kbytes, refill);
-    dma_stage(rsb, offb, cb, kb, kbytes, refill + 256 * DKB);
-    const lds_char *nxt = smem + ((k + 1) & (DNSTAGE - 1)) * DSTAGE;
-    read_frags(nxt, aoff[0], boff[0], a0, b0);
-    mfma_block<DT>(a1, b1, acc);
+    const lds_char *nxt = smem + next_slot * DSTAGE;
+    constexpr int LASTF = (DNSUB - 1) & 1;
+    constexpr int NV = SPLIT ? DIPW : 2 * DIPW;  // DMA instructions under the last sub-step
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NMF / 16, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
+    for (int q = 0; q < 16; ++q) {
+      Mfma<DT>::run(fa[LASTF][q >> 2], fb[LASTF][q & 3], acc[q >> 2][q & 3]);
+      OCTO_FENCE();
+      if (q < 8) {
+        read_frag(nxt, aoff[0], boff[0], q, fa[0], fb[0]);
+        OCTO_FENCE();
+      } else {
+        // NV DMA instructions over MFMAs 8..15: A slice first, then (ring of 2) the B slice
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NMF / 16, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        for (int d = (q - 8) * NV / 8; d < (q - 7) * NV / 8; ++d) {
+          if (d < DIPW) dma_one(rsa, offa[d], ca[d], kb, kbytes, refill, d);
+          else dma_one(rsb, offb[d - DIPW], cb[d - DIPW], kb, kbytes, refill + 256 * DKB, d - DIPW);
+          OCTO_FENCE();
+        }
+      }
     }
+    prev_slot = slot;
+    slot = next_slot;
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
   __builtin_amdgcn_s_barrier();

@@ -29,6 +29,10 @@ namespace {
 
 constexpr int64_t kPassRows = 32768;  // backward rows per pass (bounds the dz staging buffers)
 constexpr size_t kAlign = 256;
+#ifndef OCTO_GROUP_M
+#define OCTO_GROUP_M 4
+#endif
+constexpr int kGroupM = OCTO_GROUP_M;  // M-tiles per L2 group of the tile order (gemm_nt.h tile_of)
 
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
@@ -225,7 +229,7 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
 
   const Operand A = weight_operand(w, ldw, cm, V);
   const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
-  const GemmShape s = shape(V, n_max, d, 4, 2, count, 0);
+  const GemmShape s = shape(V, n_max, d, kGroupM, 2, count, 0);
   StatsArgs e;
   e.part = (f32x4 *)((char *)ws + L.part);
   e.mtiles = L.mtiles;
@@ -303,7 +307,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
 
     // dz of this pass, recomputed tile by tile
     const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm);
-    const GemmShape s1 = shape(V, rows, d, 4, 2, count, r0);
+    const GemmShape s1 = shape(V, rows, d, kGroupM, 2, count, r0);
     DzArgs e;
     e.dzA = need_gh ? dza : nullptr;
     e.ldA = L.V_pad;
@@ -325,7 +329,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     if (need_gh) {  // grad_h[rows] = dz . W   (K = V_pad)
       const Operand A2 = plain_operand(dza, L.V_pad * esz, rows, count, r0);
       const Operand B2 = plain_operand(wt, L.V_pad * esz, d, nullptr, 0);
-      const GemmShape s2 = shape(rows, d, L.V_pad, 4, 1, count, r0);
+      const GemmShape s2 = shape(rows, d, L.V_pad, kGroupM, 1, count, r0);
       StoreArgs o;
       o.C = (char *)grad_h + r0 * ld_gh * elem_bytes(gh_dtype);
       o.ldc = ld_gh;
@@ -341,7 +345,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       if (rc) return rc;
       const Operand A3 = plain_operand(dzb, L.P * esz, L.V_pad, nullptr, 0);
       const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
-      const GemmShape s3 = shape(V, d, rows, 4, 3, count, r0);
+      const GemmShape s3 = shape(V, d, rows, kGroupM, 3, count, r0);
       StoreArgs o;
       o.C = grad_w;
       o.ldc = d;
