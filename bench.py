@@ -8,8 +8,9 @@ A step is one pass of the path over one packed micro-batch, inputs resident in H
   scatter, grad_W to bf16).
 Default workload cfg3: N = 32,768 packed tree tokens (an 8,192-token root shared by 12 branches of 2,048,
 root masked: 24,576 scored rows), d = 2560, V = 151,936, bf16, T = 1.0 (octopus_amd.workloads).
-Prints one JSON line: packed tokens/s, the MFMA roofline of the forward head kernel measured with HIP
-events, and the reference algorithm timed on the host CPU beside it.
+Prints one JSON line: packed tokens/s; per GEMM kernel, its average launch time from HIP events recorded around
+each launch over the timed steps (the library's timing hook) and the MFMA roofline of the dominant one; and the
+reference algorithm timed on the host CPU beside it.
 """
 
 from __future__ import annotations
@@ -53,6 +54,23 @@ def cpu_baseline(cfg, scored_rows: int) -> dict:
             "sample": f"{n_chunks} x 2048-row chunk fwd+bwd (bf16, d={cfg.d}, V={cfg.V}) timed "
                       f"{r['seconds']:.2f} s (median), scaled x{scored_rows / r['rows']:.2f} to the step's "
                       f"{scored_rows} scored rows; extrapolated; host: {_cpu_model()}"}
+
+
+GEMM_KERNELS = ("gemm_stats", "gemm_dz", "gemm_store_grad_h", "gemm_store_grad_w")
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def recorded_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` at `workload` as recorded from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
+    in profiles/gemm_kernels_<workload>_counters.md (line `traffic <kernel>: <bytes>`), or None."""
+    path = os.path.join(PROFILES, f"gemm_kernels_{workload}_counters.md")
+    try:
+        for line in open(path):
+            if line.startswith(f"traffic {kernel}:"):
+                return float(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
 
 
 def library_gemms(workload: str, reps: int = 5) -> dict:
@@ -157,12 +175,21 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    # the timed region: each GEMM launch is bracketed by HIP events on its own stream (octo_timing_*)
+    _lib.call("octo_timing_enable", 1)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = elapsed / args.steps * 1e3
+    kernels = {}
+    for name in GEMM_KERNELS:
+        launches, total = _lib.timing_read(name)
+        if launches:
+            kernels[name] = {"launches_per_step": launches / args.steps, "avg_ms": total / launches,
+                             "ms_per_step": total / args.steps}
+    _lib.call("octo_timing_enable", 0)
 
     # per-phase HIP-event timing on the launch stream (torch's current stream carries every launch)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
@@ -186,8 +213,14 @@ def main() -> int:
     exe_flop = {"full": 8, "hidden": 6, "none": 2}[cfg.backward] * n * d * V
     peak = PEAK_BF16 if cfg.dtype != torch.float32 else PEAK_F32
     step_s = ms / 1e3
-    fwd_flop = 2 * n * d * V
-    fwd_achieved = fwd_flop / (fwd_ms / 1e3)
+    # every GEMM kernel of the path is one dense contraction of 2 * n * d * V FLOP per launch (the pass
+    # holds all n scored rows at this size): logits (gemm_stats), logits again -> dz (gemm_dz),
+    # dz . W (gemm_store_grad_h), dz^T . h (gemm_store_grad_w)
+    flop_launch = 2 * n * d * V
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+    dom_achieved = flop_launch / (kernels[dom]["avg_ms"] / 1e3)
+    for k in kernels.values():
+        k["tflops"] = flop_launch / (k["avg_ms"] / 1e3) / 1e12
     result = {
         "metric": "packed tokens/sec fwd+bwd logprob @ d=2560,V=151936 bf16; % MFMA peak",
         "value": cfg.N / step_s,
@@ -207,11 +240,12 @@ def main() -> int:
         "mfma_frac_algorithmic": alg_flop / step_s / peak,
         "mfma_frac_executed": exe_flop / step_s / peak,
         "phase_ms": {"forward": fwd_ms, "backward": bwd_ms},
-        "roofline": {"kernel": "gemm_stats_kernel (fused forward head: MFMA GEMM + softmax epilogue; the event "
-                               "bracket also holds its merge kernel and the compaction)",
-                     "bound": "mfma", "achieved": fwd_achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
-                     "frac": fwd_achieved / peak, "traffic": None,
-                     "per_launch": f"2*n*d*V = {fwd_flop:.4g} FLOP (n={n} scored rows)"},
+        "kernels": kernels,
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": dom_achieved / 1e12, "peak": peak / 1e12,
+                     "unit": "TFLOP/s", "frac": dom_achieved / peak,
+                     "traffic": recorded_traffic(dom, cfg.name),
+                     "per_launch": f"2*n*d*V = {flop_launch:.4g} FLOP (n={n} scored rows), HIP events around "
+                                   f"each launch over the timed steps"},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, n)

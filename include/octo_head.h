@@ -63,6 +63,14 @@ extern "C" {
 const char *octo_version(void);
 const char *octo_last_error(void);
 
+/* Kernel timing hook (no counterpart in the reference: a measurement aid for benchmarks). While enabled,
+ * every GEMM launch of octo_head_fwd / octo_head_bwd is bracketed by HIP events on its stream, under the
+ * names "gemm_stats", "gemm_dz", "gemm_store_grad_h" and "gemm_store_grad_w". octo_timing_read waits for
+ * the recorded launches of one name and returns their count and summed duration. octo_timing_enable
+ * (either value) discards what was recorded. Off by default; enabling it creates events (allocates). */
+int octo_timing_enable(int on);
+int octo_timing_read(const char *kernel, int *launches, double *total_ms);
+
 /* Workspace bytes for octo_head_fwd (flags without OCTO_WS_BACKWARD) or octo_head_bwd
  * (OCTO_WS_BACKWARD [| OCTO_WS_NO_GRADW]) at n_max rows, width d, vocabulary V. */
 int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes);

@@ -30,6 +30,8 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "octo_version": [],
     "octo_last_error": [],
+    "octo_timing_enable": [_i32],
+    "octo_timing_read": [ctypes.c_char_p, ctypes.POINTER(_i32), ctypes.POINTER(ctypes.c_double)],
     "octo_head_workspace_bytes": [_i64, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)],
     "octo_compact_rows": [_p, _i64, _p, _p, _p],
     "octo_head_fwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
@@ -95,6 +97,13 @@ def workspace_bytes(n_max: int, d: int, V: int, w_dtype: int, flags: int) -> int
     out = _sz(0)
     call("octo_head_workspace_bytes", n_max, d, V, w_dtype, flags, ctypes.byref(out))
     return out.value
+
+
+def timing_read(kernel: str) -> tuple[int, float]:
+    """(launches, summed ms) of one kernel name recorded by the timing hook (octo_timing_enable)."""
+    n, ms = _i32(0), ctypes.c_double(0.0)
+    call("octo_timing_read", kernel.encode(), ctypes.byref(n), ctypes.byref(ms))
+    return n.value, ms.value
 
 
 def grpo_workspace_bytes() -> int:

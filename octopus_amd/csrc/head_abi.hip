@@ -2,6 +2,10 @@
 // status plumbing. Argument checks happen here, on the host, before anything is queued.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
 
 #include "gemm_nt.h"
 #include "octo_internal.h"
@@ -26,6 +30,43 @@ int octo_fail(int code, const char *fmt, ...) {
 using namespace octo;
 
 namespace {
+
+// ---- kernel timing hook (octo_timing_enable / octo_timing_read) ----------------------------------
+// When enabled, each GEMM launch of octo_head_fwd / octo_head_bwd is bracketed by a pair of HIP events on
+// its stream; octo_timing_read waits for the recorded pairs of one kernel name and sums their durations.
+struct TimedPair {
+  const char *name;
+  hipEvent_t a, b;
+};
+std::mutex g_timing_mu;
+bool g_timing = false;
+std::vector<TimedPair> g_timed;
+
+struct TimedLaunch {
+  hipEvent_t a = nullptr, b = nullptr;
+  const char *name;
+  hipStream_t st;
+  TimedLaunch(const char *n, hipStream_t s) : name(n), st(s) {
+    if (!g_timing) return;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess || hipEventRecord(a, st) != hipSuccess) {
+      if (a) hipEventDestroy(a);
+      if (b) hipEventDestroy(b);
+      a = b = nullptr;
+    }
+  }
+  void done() {
+    if (!a) return;
+    if (hipEventRecord(b, st) == hipSuccess) {
+      std::lock_guard<std::mutex> lk(g_timing_mu);
+      g_timed.push_back({name, a, b});
+    } else {
+      hipEventDestroy(a);
+      hipEventDestroy(b);
+    }
+    a = b = nullptr;
+  }
+  ~TimedLaunch() { done(); }
+};
 
 constexpr int64_t kPassRows = 32768;  // backward rows per pass (bounds the dz staging buffers)
 constexpr size_t kAlign = 256;
@@ -199,6 +240,36 @@ extern "C" {
 const char *octo_version(void) { return "octo_head 0.1 (gfx950)"; }
 const char *octo_last_error(void) { return g_err; }
 
+int octo_timing_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  for (auto &t : g_timed) {
+    hipEventDestroy(t.a);
+    hipEventDestroy(t.b);
+  }
+  g_timed.clear();
+  g_timing = on != 0;
+  return OCTO_OK;
+}
+
+int octo_timing_read(const char *kernel, int *launches, double *total_ms) {
+  OCTO_CHECK_ARG(kernel && launches && total_ms, "timing_read: null argument");
+  std::lock_guard<std::mutex> lk(g_timing_mu);
+  int n = 0;
+  double ms = 0.0;
+  for (auto &t : g_timed) {
+    if (strcmp(t.name, kernel) != 0) continue;
+    float x = 0.f;
+    hipError_t e = hipEventSynchronize(t.b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&x, t.a, t.b);
+    if (e != hipSuccess) return octo_fail(OCTO_EHIP, "timing_read: %s", hipGetErrorString(e));
+    ++n;
+    ms += x;
+  }
+  *launches = n;
+  *total_ms = ms;
+  return OCTO_OK;
+}
+
 int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes) {
   OCTO_CHECK_ARG(bytes != nullptr, "workspace_bytes: null pointer");
   OCTO_CHECK_ARG(n_max >= 0 && d > 0 && V > 0, "workspace_bytes: bad sizes");
@@ -237,7 +308,10 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
   e.wscale = w_scale;
   e.c = cm.c;
   e.pre = cm.pre;
-  rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, A, B, s, e, st);
+  {
+    TimedLaunch t("gemm_stats", st);
+    rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, A, B, s, e, st);
+  }
   if (rc) return rc;
 
   MergeArgs m;
@@ -323,7 +397,10 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     e.c = cm.c;
     e.pre = cm.pre;
     e.gmul = cm.gmul;
-    rc = launch_gemm_dz(cm.dt, cm.fp8, use_tanh != 0, Aw, Bh, s1, e, st);
+    {
+      TimedLaunch t("gemm_dz", st);
+      rc = launch_gemm_dz(cm.dt, cm.fp8, use_tanh != 0, Aw, Bh, s1, e, st);
+    }
     if (rc) return rc;
 
     if (need_gh) {  // grad_h[rows] = dz . W   (K = V_pad)
@@ -335,7 +412,10 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       o.ldc = ld_gh;
       o.dtype = gh_dtype;
       o.accumulate = 0;
-      rc = launch_gemm_store(cm.dt, A2, B2, s2, o, st);
+      {
+        TimedLaunch t("gemm_store_grad_h", st);
+        rc = launch_gemm_store(cm.dt, A2, B2, s2, o, st);
+      }
       if (rc) return rc;
     }
     if (need_gw) {  // grad_W += dz^T . h   (K = this pass's rows)
@@ -351,7 +431,10 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       o.ldc = d;
       o.dtype = OCTO_F32;
       o.accumulate = (p > 0 || (flags & OCTO_GRADW_ACCUMULATE)) ? 1 : 0;
-      rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st);
+      {
+        TimedLaunch t("gemm_store_grad_w", st);
+        rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st);
+      }
       if (rc) return rc;
     }
   }

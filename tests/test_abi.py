@@ -79,3 +79,13 @@ def test_small_entry_point_checks():
     with pytest.raises(ValueError):
         _lib.call("octo_grpo_grad", P, None, None, P, P, 4, 0.2, 0.28, 5.0, P, None, None, 0, None)
     assert _lib.grpo_workspace_bytes() >= 4
+
+
+def test_timing_hook_without_launches():
+    """The timing hook records nothing until a GEMM is launched, and reading an unknown name is not an error."""
+    _lib.call("octo_timing_enable", 1)
+    assert _lib.timing_read("gemm_stats") == (0, 0.0)
+    assert _lib.timing_read("no_such_kernel") == (0, 0.0)
+    _lib.call("octo_timing_enable", 0)
+    with pytest.raises(ValueError):
+        _lib.call("octo_timing_read", None, None, None)

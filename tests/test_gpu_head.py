@@ -196,3 +196,59 @@ def test_grpo_matches_oracle():
                                      old=None if "old" not in kw else f(kw["old"]))
         assert abs(loss.item() - ref_loss) < 1e-4 * max(1.0, abs(ref_loss))
         assert np.abs(g.cpu().numpy() - ref_g).max() < 1e-6
+
+
+def test_timing_hook_brackets_each_gemm_launch():
+    """octo_timing_*: one gemm_stats launch per forward call, one each of the three backward GEMMs per backward
+    call, with positive durations."""
+    from octopus_amd import _lib
+    h, W, y = _inputs(513, 256, 5000, torch.bfloat16, seed=3)
+    hd, Wd = h.to(DEV).requires_grad_(True), W.to(DEV).requires_grad_(True)
+    _lib.call("octo_timing_enable", 1)
+    try:
+        out = fused_head(hd, Wd, y.to(DEV), 1.0)
+        out[:, 0].sum().backward()
+        torch.cuda.synchronize()
+        for name in ("gemm_stats", "gemm_dz", "gemm_store_grad_h", "gemm_store_grad_w"):
+            n, ms = _lib.timing_read(name)
+            assert n == 1 and ms > 0, name
+    finally:
+        _lib.call("octo_timing_enable", 0)
+
+
+def _golden(name):
+    import os
+    return np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_small_heads_match_the_golden_fixtures(dtype):
+    """The HIP path against the stored fp64 expectations (tests/golden/head_small.npz): forward columns and the
+    gradients of sum(g * logprob), plain, temperature and soft-capped."""
+    z = _golden("head_small.npz")
+    for nm in ("plain", "temp", "softcap"):
+        h, W, y, g = (torch.from_numpy(z[f"{nm}/{k}"]) for k in ("h", "W", "y", "g"))
+        T, pre, post, tanh = z[f"{nm}/params"].tolist()
+        hd = h.to(DEV, dtype).requires_grad_(True)
+        Wd = W.to(DEV, dtype).requires_grad_(True)
+        out = fused_head(hd, Wd, y.to(DEV), T, Post(pre, post, bool(tanh)))
+        (out[:, 0] * g.to(DEV)).sum().backward()
+        tol = _tol(dtype)
+        o = out.detach().cpu().double()
+        assert (o[:, 0] - torch.from_numpy(z[f"{nm}/logp"])).abs().max() <= tol, nm
+        assert (o[:, 1] - torch.from_numpy(z[f"{nm}/ent"])).abs().max() <= tol, nm
+        bar = 1e-4 if dtype == torch.float32 else 1e-2
+        assert _rel(hd.grad.cpu(), torch.from_numpy(z[f"{nm}/grad_h"])) <= bar, nm
+        assert _rel(Wd.grad.cpu(), torch.from_numpy(z[f"{nm}/grad_W"])) <= bar, nm
+
+
+def test_cfg1_matches_the_golden_fixture():
+    """The CPU-runnable configuration (N 512, d 1024, V 32,000, fp32), generated on the host as the fixture was,
+    against its stored fp64 logprob / entropy at 1e-5."""
+    from octopus_amd.workloads import CONFIGS, make_batch
+    z = _golden("cfg1_expected.npz")
+    b = make_batch(CONFIGS["cfg1"], "cpu")
+    assert np.array_equal(b.labels.numpy(), z["labels"])
+    out = fused_head(b.hidden.to(DEV), b.weight.to(DEV), b.labels.to(DEV), 1.0).cpu().double()
+    assert (out[:, 0] - torch.from_numpy(z["logp"])).abs().max() <= 1e-5
+    assert (out[:, 1] - torch.from_numpy(z["ent"])).abs().max() <= 1e-5

@@ -247,3 +247,21 @@ def test_grpo_matches_torch_autograd_and_finite_differences():
         b[t] -= eps
         num = (ogrpo.grpo(a, adv, mask, prox=prox, old=old)[0] - ogrpo.grpo(b, adv, mask, prox=prox, old=old)[0])
         assert abs(num / (2 * eps) - g[t]) < 1e-6
+
+
+def test_baseline_matches_the_oracle():
+    """oracle.baseline (the reference algorithm as run for the CPU baseline: CHUNK-row checkpointed chunks, autograd
+    backward) agrees with the fp64 closed forms in fp32 over more than one chunk."""
+    from oracle import baseline
+    g = torch.Generator().manual_seed(6)
+    n, d, V, T = 2048 + 300, 32, 257, 0.7
+    h = torch.randn(n, d, generator=g)
+    W = torch.randn(V, d, generator=g) * 0.3
+    y = torch.randint(0, V, (n,), generator=g)
+    gl = torch.randn(n, generator=g)
+    out, gh, gw = baseline.fwd_bwd(h, W, y, T, gl)
+    lp, ent, _ = ohead.head_forward(h, W, y, T)
+    oh, ow = ohead.head_backward(h, W, y, T, gl)
+    assert torch.allclose(out[:, 0].double(), lp, atol=1e-5) and torch.allclose(out[:, 1].double(), ent, atol=1e-5)
+    assert ((gh.double() - oh).norm() / oh.norm()).item() < 1e-5
+    assert ((gw.double() - ow).norm() / ow.norm()).item() < 1e-5
