@@ -103,15 +103,17 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
  *   lse[r] : from octo_head_fwd on the same inputs
  *   grad_h : NULL or [n_max, ld_gh] of gh_dtype (BF16, F16 or F32), compact order; rows at and
  *            after *count are left unspecified
- *   grad_w : NULL or [V, d] fp32; = or += (OCTO_GRADW_ACCUMULATE). Not available for FP8E4M3 weights.
- * The logits are recomputed tile by tile; dz is staged in the workspace in passes of rows. */
+ *   grad_w : NULL or [V, d] (row stride d) of gw_dtype (BF16, F16 or F32); = or += (OCTO_GRADW_ACCUMULATE),
+ *            summed in fp32 and rounded once to gw_dtype. Not available for FP8E4M3 weights.
+ * The logits are recomputed tile by tile; dz = g (onehot - p) / T is staged in the workspace (bf16 / f16 / f32)
+ * in passes of at most 32,768 rows. */
 int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                   const void *w, int64_t ldw, int w_dtype, const float *w_scale,
                   const int64_t *labels, const int64_t *idx, const int32_t *count,
                   int64_t n_max, int d, int V, int flags,
                   float inv_T, float pre, float post, int use_tanh,
                   const float *lse, const float *g,
-                  void *grad_h, int64_t ld_gh, int gh_dtype, float *grad_w,
+                  void *grad_h, int64_t ld_gh, int gh_dtype, void *grad_w, int gw_dtype,
                   void *ws, size_t ws_bytes, void *stream);
 
 /* _head_columns on materialised logits [n, ld] (dtype BF16, F16 or F32):

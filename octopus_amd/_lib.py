@@ -37,7 +37,7 @@ SIGNATURES = {
     "octo_head_fwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                       _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, _p, _sz, _p],
     "octo_head_bwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
-                      _f32, _f32, _f32, _i32, _p, _p, _p, _i64, _i32, _p, _p, _sz, _p],
+                      _f32, _f32, _f32, _i32, _p, _p, _p, _i64, _i32, _p, _i32, _p, _sz, _p],
     "octo_columns_fwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p],
     "octo_columns_bwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p, _i64, _p],
     "octo_pairs_expand": [_p, _i64, _i32, _p, _i64, _p, _p],

@@ -245,33 +245,38 @@ __device__ __forceinline__ void mainloop(const Operand &A, const Operand &B, int
 
 // ---- direct-to-LDS mainloop -----------------------------------------------------------------------
 //
-// K advances DKB bytes per stage (64: 32 bf16 / 16 fp32; 128: 64 bf16 / 32 fp32). The A and B slices of a
-// stage (256 rows x DKB bytes each) are written straight into LDS by buffer_load_dwordx4 ... lds: each
-// wave instruction moves 1 KB, lane i's 16 bytes landing at the instruction's LDS base + 16 i, so the LDS
-// layout is chosen by which global chunk each lane fetches (64 / (DKB / 16) whole rows per instruction).
-// DNSTAGE stages form a ring; the DMA for stage k + DNSTAGE is issued in iteration k, DNSTAGE - 1 stages
-// ahead of its use. One bare s_barrier per stage (no memory fence: the waits are explicit) separates
-// "stage k + 1 landed in every wave" and "every wave has read stage k" from the DMA that overwrites stage
-// k's buffer.
+// K advances 64 bytes of the staged type per stage (32 bf16 / f16, 16 fp32). Each operand's stage slice (16 KB)
+// is written straight into LDS by buffer_load_dwordx4 ... lds: a wave instruction moves 1 KB, lane i's 16 bytes
+// landing at the instruction's LDS base + 16 i, so the LDS layout is chosen by which global chunk each lane
+// fetches. DNSTAGE stages form a ring (A slice, then B slice, per stage). One bare s_barrier per stage (no
+// memory fence: the waits are explicit) separates "stage k + 1 landed in every wave" and "every wave has read
+// stage k" from the DMA that overwrites stage k's slot.
 //
-// LDS rows are DKB bytes of 16-byte chunks; chunk c of row r sits at physical chunk c ^ swz(r), which keeps
-// the fragment reads of consecutive lanes (consecutive rows, same logical chunk) on distinct bank groups.
-#ifndef OCTO_DKB
-#define OCTO_DKB 64
-#endif
-constexpr int DKB = OCTO_DKB;              // K bytes per stage
-constexpr int DSTAGE = 2 * 256 * DKB;      // A + B bytes per stage
+// An operand is streamed in one of two layouts:
+//   OpRows (K-contiguous rows, the NT case): a slice is 256 rows x 64 bytes. Chunk c of row r sits at
+//     physical chunk c ^ ((r >> 2) & 3), so a 16-lane pass of fragment reads (rows r0..r0+15 of one logical
+//     chunk) covers all 64 banks once. A fragment is one ds_read_b128: lane l holds row l & 31 of a 32-row
+//     block, K chunk 2 sub + (l >> 5).
+//   OpCols (MN-contiguous, 16-bit types): a slice is 32 K-rows x 512 bytes (256 columns). Chunk c of K-row r
+//     sits at physical chunk c ^ 4 (r & 3). A fragment is two ds_read_b64_tr_b16 (gfx950 transposing reads):
+//     within each 16-lane group, output lane i, element e comes from source lane 4 e + (i >> 2), element i & 3;
+//     so source lane s of group g reads K-row 16 sub + 8 (g >> 1) + (s >> 2) (+ 4 for the upper half) at
+//     columns 16 (g & 1) + 4 (s & 3) .. + 4 of the block, and lane l receives column l & 31 at the 8 K values
+//     16 sub + 8 (l >> 5) + 0..7, the MFMA operand layout. The 64 lanes of one read cover 8 K-rows x 64 bytes,
+//     which the XOR spreads over all 64 banks exactly twice.
+//     The buffer descriptor is rebuilt per stage at the stage's first K-row, so operands larger than 4 GB stay
+//     within 32-bit offsets; K-rows at or past `krows` read zero.
+constexpr int DKB = 64;                    // K bytes per stage
+constexpr int DSLICE = 256 * DKB;          // one operand's stage slice (16 KB)
+constexpr int DSTAGE = 2 * DSLICE;         // A + B bytes per stage
 #ifndef OCTO_NSTAGE
-#define OCTO_NSTAGE (DKB == 64 ? 4 : 2)
+#define OCTO_NSTAGE 4
 #endif
 constexpr int DNSTAGE = OCTO_NSTAGE;       // ring depth
-constexpr int DLPR = DKB / 16;             // lanes per row in one DMA instruction
-constexpr int DRPI = 64 / DLPR;            // rows per DMA instruction
-constexpr int DIPW = 256 / DRPI / 4;       // DMA instructions per wave per operand and stage
-constexpr int DNSUB = DKB / 32;            // 16-byte-fragment sub-steps per stage
+constexpr int DIPW = 4;                    // DMA instructions per wave per operand and stage
+constexpr int DNSUB = 2;                   // 16-byte-fragment sub-steps per stage
 // LDS of one GEMM workgroup: the register-staged mainloop's 2 x (A + B) 32 KB slices or the DMA ring.
 constexpr int SMEM_BYTES = (4 * TILE_BYTES > DNSTAGE * DSTAGE) ? 4 * TILE_BYTES : DNSTAGE * DSTAGE;
-static_assert(DKB == 64 || DKB == 128, "stage width");
 static_assert(SMEM_BYTES <= 160 * 1024, "LDS budget");
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at bits 15:14, expcnt 6:4, lgkmcnt 11:8)
@@ -279,92 +284,123 @@ constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) 
 constexpr int WAIT_LGKM0 = 15 | (3 << 14) | (7 << 4);
 static_assert(2 * DIPW * DNSTAGE <= 63, "vmcnt range");
 
-// 64-byte rows: chunk c of row r at c ^ ((r >> 2) & 3), so the 8 lanes of a 128-byte LDS access (rows r0..r0+7
-// of one logical chunk: two rows per physical chunk index) cover all four chunk positions twice in two
-// different 64-byte halves of the bank space; 128-byte rows: c ^ (r & 7).
-__device__ __forceinline__ int swz_row(int r) {
-  if (DKB == 128) return r & 7;
-  return (r >> 2) & 3;
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, lds_char *dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, voff, 0, 0, 0);
 }
 
-// Per-thread DMA sources of one operand: instruction q (0..DIPW-1) of wave w fills LDS rows
-// (4 q + w) * DRPI .. + DRPI; lane i takes row + i / DLPR and physical chunk i % DLPR.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_rows(const Operand &op, int64_t row0, uint32_t (&off)[DIPW],
-                                                           uint32_t (&coff)[DIPW]) {
-  const int w = threadIdx.x >> 6, i = threadIdx.x & 63;
-  const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
+// K-contiguous operand: instruction q of wave w fills slice rows (4 q + w) * 16 .. + 16; lane i takes row
+// + (i >> 2) and physical chunk i & 3.
+struct OpRows {
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t off[DIPW], coff[DIPW];
+  int fo[DNSUB];  // fragment byte offsets in the slice (block 0)
+
+  __device__ __forceinline__ void init(const Operand &op, int64_t row0, int wsub, uint32_t /*krows*/) {
+    const int w = threadIdx.x >> 6, i = threadIdx.x & 63, lane = i;
+    const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
 #pragma unroll
-  for (int q = 0; q < DIPW; ++q) {
-    const int r = (4 * q + w) * DRPI + i / DLPR;
-    coff[q] = (uint32_t)(((i % DLPR) ^ swz_row(r)) << 4);
-    uint32_t rowoff;
-    if (r < valid) rowoff = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
-    else rowoff = 0x80000000u;
-    off[q] = rowoff + coff[q];
+    for (int q = 0; q < DIPW; ++q) {
+      const int r = (4 * q + w) * 16 + (i >> 2);
+      coff[q] = (uint32_t)(((i & 3) ^ ((r >> 2) & 3)) << 4);
+      uint32_t rowoff;
+      if (r < valid) rowoff = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
+      else rowoff = 0x80000000u;
+      off[q] = rowoff + coff[q];
+    }
+    if (op.map) rs = make_rsrc(uniform_ptr(op.base), op.extent);
+    else rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
+#pragma unroll
+    for (int ks = 0; ks < DNSUB; ++ks)
+      fo[ks] = (wsub * 128 + (lane & 31)) * DKB + (((2 * ks + (lane >> 5)) ^ ((lane >> 2) & 3)) << 4);
   }
-  if (op.map) return make_rsrc(uniform_ptr(op.base), op.extent);
-  return make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
-}
-
-__device__ __forceinline__ void dma_stage(__amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[DIPW],
-                                          const uint32_t (&coff)[DIPW], uint32_t kb, uint32_t kbytes,
-                                          lds_char *dst) {
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#pragma unroll
-  for (int q = 0; q < DIPW; ++q) {
-    const uint32_t o = (kb + coff[q] < kbytes) ? off[q] + kb : 0x80000000u;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(dst + (4 * q + w) * 1024),
-                                             16, o, 0, 0, 0);
+  // K chunks at or past kbytes (bytes per row) read zero
+  __device__ __forceinline__ void dma(int k, int q, uint32_t kbytes, lds_char *slice) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t kb = (uint32_t)k * DKB;
+    lds_dma16(rs, (kb + coff[q] < kbytes) ? off[q] + kb : 0x80000000u, slice + (4 * q + w) * 1024);
   }
-}
+  __device__ __forceinline__ i32x4 frag(const lds_char *slice, int sub, int blk) const {
+    return *(const lds_i32x4 *)(slice + fo[sub] + blk * 32 * DKB);
+  }
+};
 
-template <int DT>
-__device__ __forceinline__ void mfma_block(const i32x4 (&af)[4], const i32x4 (&bf)[4], f32x16 (&acc)[4][4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) Mfma<DT>::run(af[i], bf[j], acc[i][j]);
-}
+// MN-contiguous 16-bit operand: instruction q of wave w fills K-rows (4 q + w) * 2 and + 1 of the slice (lanes
+// 0..31, 32..63), lane i taking physical chunk i & 31.
+struct OpCols {
+  const char *base;  // the tile's first column in K-row 0
+  int64_t ld;        // bytes per K-row
+  int64_t bytes;     // bytes addressable from base (the operand's rows x ld, less the column offset)
+  uint32_t krows;    // K-rows that exist
+  uint32_t roff[DIPW];
+  int rowq[DIPW];
+  int fa[4];         // fragment byte offsets of blocks 0..3 (sub-step 0, lower half)
 
-__device__ __forceinline__ void read_frags(const lds_char *s, int aoff, int boff, i32x4 (&af)[4], i32x4 (&bf)[4]) {
+  __device__ __forceinline__ void init(const Operand &op, int64_t col0, int wsub, uint32_t krows_) {
+    const int w = threadIdx.x >> 6, i = threadIdx.x & 63, l = i;
+    base = op.base + col0 * 2;
+    ld = op.ld;
+    bytes = op.rows * op.ld - col0 * 2;
+    krows = (int64_t)krows_ < op.rows ? krows_ : (uint32_t)op.rows;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) af[i] = *(const lds_i32x4 *)(s + aoff + i * 32 * DKB);
+    for (int q = 0; q < DIPW; ++q) {
+      const int r = (4 * q + w) * 2 + (i >> 5);
+      rowq[q] = r;
+      roff[q] = (uint32_t)(r * ld) + (uint32_t)((((i & 31) ^ (4 * (r & 3)))) << 4);
+    }
+    const int g = l >> 4, s = l & 15;
+    const int krow = 8 * (g >> 1) + (s >> 2);  // + 16 sub, + 4 for the upper half (r & 3 unchanged)
+    const int j = 2 * (g & 1) + ((s & 3) >> 1);
+    const int intra = (s & 1) * 8;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) bf[j] = *(const lds_i32x4 *)(s + boff + j * 32 * DKB);
-}
-
-// Fragment q (0..7) of a sub-step: A block q (q < 4) or B block q - 4.
-__device__ __forceinline__ void read_frag(const lds_char *s, int aoff, int boff, int q, i32x4 (&af)[4],
-                                          i32x4 (&bf)[4]) {
-  if (q < 4) af[q] = *(const lds_i32x4 *)(s + aoff + q * 32 * DKB);
-  else bf[q - 4] = *(const lds_i32x4 *)(s + boff + (q - 4) * 32 * DKB);
-}
-
-// One DMA instruction q (0..DIPW-1) of an operand slice (see dma_stage).
-__device__ __forceinline__ void dma_one(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t coff, uint32_t kb,
-                                        uint32_t kbytes, lds_char *dst, int q) {
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t o = (kb + coff < kbytes) ? off + kb : 0x80000000u;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)(dst + (4 * q + w) * 1024),
-                                           16, o, 0, 0, 0);
-}
+    for (int blk = 0; blk < 4; ++blk)
+      fa[blk] = krow * 512 + (16 * wsub + 4 * (blk ^ (s >> 2)) + j) * 16 + intra;
+  }
+  // K-rows at or past krows read zero; so do columns past the operand's last byte (an edge tile's columns past
+  // the row end read the next row, whose products land in discarded output columns)
+  __device__ __forceinline__ void dma(int k, int q, uint32_t /*kbytes*/, lds_char *slice) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t skip = (int64_t)k * 32 * ld;
+    const int64_t left = bytes - skip;
+    // every term is wave-uniform; readfirstlane says so, or the compiler wraps the load in a waterfall loop
+    const uint32_t ext = __builtin_amdgcn_readfirstlane(
+        left <= 0 ? 0u : (left < 32 * ld ? (uint32_t)left : (uint32_t)(32 * ld)));
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(uniform_ptr(base + (left > 0 ? skip : 0)), ext);
+    const uint32_t row = (uint32_t)k * 32 + (uint32_t)rowq[q];
+    lds_dma16(rs, row < krows ? roff[q] : 0x80000000u, slice + (4 * q + w) * 1024);
+  }
+  // Issued as inline asm: the compiler cannot tell the transposing read from a read of the LDS that the
+  // in-flight DMA is writing, and would drain every outstanding DMA (vmcnt(0)) before it. Stage data is
+  // ordered by the mainloop's own vmcnt waits and barriers, and the mainloop waits lgkmcnt(0) at the start
+  // of each sub-step, before the first MFMA that can consume a fragment read under the previous one.
+  __device__ __forceinline__ i32x4 frag(const lds_char *slice, int sub, int blk) const {
+    const uint32_t p = (uint32_t)(uintptr_t)(slice + fa[blk] + sub * 16 * 512);
+    i32x2 lo, hi;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(p));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:2048" : "=v"(hi) : "v"(p));
+    i32x4 r;
+    r[0] = lo[0];
+    r[1] = lo[1];
+    r[2] = hi[0];
+    r[3] = hi[1];
+    return r;
+  }
+};
 
 // Instruction order is fixed in the source: a scheduling fence after every MFMA / load keeps the fragment
 // reads of the next sub-step early (so register allocation cannot fold them onto fragments still in use)
 // and spreads the DMA issues evenly between MFMAs.
 #define OCTO_FENCE() __builtin_amdgcn_sched_barrier(0)
 
-// smem: DNSTAGE * DSTAGE bytes; stage s at s * DSTAGE, A rows first then B rows.
+// smem: DNSTAGE * DSTAGE bytes; stage s at s * DSTAGE, A slice first then B slice. `krows` bounds the K-rows
+// of MN-contiguous operands.
 //
-// Stage j's A slice is issued right after the barrier that frees its slot (in iteration j - DNSTAGE), its
-// B slice under the first sub-step of the next iteration (into the slot stage j - DNSTAGE left), so the
-// 2 * DIPW DMA instructions of a stage are spread over two sub-steps. With a ring of 2 both slices go
-// after the barrier.
-template <int DT>
+// Stage j's A slice is issued right after the barrier that frees its slot (in iteration j - DNSTAGE), its B slice
+// under the first sub-step of the next iteration (into the slot stage j - DNSTAGE left), so the 2 * DIPW DMA
+// instructions of a stage are spread over two sub-steps.
+template <int DT, typename OA, typename OB>
 __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B, int64_t m0, int64_t n0, int64_t K_eff,
                                              lds_char *smem, f32x16 (&acc)[4][4]) {
-  constexpr bool SPLIT = DNSTAGE >= 3;
-  const int lane = threadIdx.x & 63;
+  static_assert(DNSTAGE >= 3, "ring depth");
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
 #pragma unroll
@@ -379,94 +415,70 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
   const int nk = (int)((kbytes + DKB - 1) / DKB);
   if (nk == 0) return;
 
-  uint32_t offa[DIPW], offb[DIPW], ca[DIPW], cb[DIPW];
-  const __amdgpu_buffer_rsrc_t rsa = dma_rows(A, m0, offa, ca);
-  const __amdgpu_buffer_rsrc_t rsb = dma_rows(B, n0, offb, cb);
+  OA opa;
+  OB opb;
+  opa.init(A, m0, wm, (uint32_t)K_eff);
+  opb.init(B, n0, wn, (uint32_t)K_eff);
 
-  const int f = swz_row(lane);
-  int aoff[DNSUB], boff[DNSUB];
 #pragma unroll
-  for (int ks = 0; ks < DNSUB; ++ks) {
-    const int pc = ((2 * ks + (lane >> 5)) ^ f) << 4;
-    aoff[ks] = (wm * 128 + (lane & 31)) * DKB + pc;
-    boff[ks] = 256 * DKB + (wn * 128 + (lane & 31)) * DKB + pc;
-  }
-
-  if constexpr (SPLIT) {
+  for (int st = 0; st < DNSTAGE; ++st) {
 #pragma unroll
-    for (int s = 0; s < DNSTAGE - 1; ++s) {
-      dma_stage(rsa, offa, ca, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE);
-      dma_stage(rsb, offb, cb, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE + 256 * DKB);
+    for (int q = 0; q < DIPW; ++q) opa.dma(st, q, kbytes, smem + st * DSTAGE);
+    if (st < DNSTAGE - 1) {
+#pragma unroll
+      for (int q = 0; q < DIPW; ++q) opb.dma(st, q, kbytes, smem + st * DSTAGE + DSLICE);
     }
-    dma_stage(rsa, offa, ca, (uint32_t)(DNSTAGE - 1) * DKB, kbytes, smem + (DNSTAGE - 1) * DSTAGE);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 2) + DIPW));
-  } else {
-#pragma unroll
-    for (int s = 0; s < DNSTAGE; ++s) {
-      dma_stage(rsa, offa, ca, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE);
-      dma_stage(rsb, offb, cb, (uint32_t)s * DKB, kbytes, smem + s * DSTAGE + 256 * DKB);
-    }
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 1)));
   }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 2) + DIPW));  // stage 0 landed
   __builtin_amdgcn_s_barrier();
 
   i32x4 fa[2][4], fb[2][4];
-  read_frags(smem, aoff[0], boff[0], fa[0], fb[0]);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    fa[0][b] = opa.frag(smem, 0, b);
+    fb[0][b] = opb.frag(smem + DSLICE, 0, b);
+  }
   int slot = 0;                 // k % DNSTAGE
   int prev_slot = DNSTAGE - 1;  // (k - 1) % DNSTAGE
   for (int k = 0; k < nk; ++k) {
     const int next_slot = (slot + 1 == DNSTAGE) ? 0 : slot + 1;
     const lds_char *cur = smem + slot * DSTAGE;
+    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // this sub-step's fragments (read under the previous one) are in
     OCTO_FENCE();
-    // sub-steps 0 .. DNSUB - 2: read the next sub-step's fragments under the first 8 MFMAs
+    // sub-step 0: read sub-step 1's fragments under the first 8 MFMAs; the B slice of stage k + DNSTAGE - 1
+    // (into the slot stage k - 1 left) under the last 8
 #pragma unroll
-    for (int sub = 0; sub + 1 < DNSUB; ++sub) {
-      const uint32_t kbB = (uint32_t)(k + DNSTAGE - 1) * DKB;
-      lds_char *dstB = smem + prev_slot * DSTAGE + 256 * DKB;
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        Mfma<DT>::run(fa[sub & 1][q >> 2], fb[sub & 1][q & 3], acc[q >> 2][q & 3]);
+    for (int q = 0; q < 16; ++q) {
+      Mfma<DT>::run(fa[0][q >> 2], fb[0][q & 3], acc[q >> 2][q & 3]);
+      OCTO_FENCE();
+      if (q < 8) {
+        if (q < 4) fa[1][q] = opa.frag(cur, 1, q);
+        else fb[1][q - 4] = opb.frag(cur + DSLICE, 1, q - 4);
         OCTO_FENCE();
-        if (q < 8) {
-          read_frag(cur, aoff[sub + 1], boff[sub + 1], q, fa[(sub + 1) & 1], fb[(sub + 1) & 1]);
-          OCTO_FENCE();
-        } else if (SPLIT && sub == 0) {
-          // B slice of stage k + DNSTAGE - 1, DIPW instructions over MFMAs 8..15
-          constexpr int every = 8 / DIPW;
-          if ((q - 8) % every == every - 1) {
-            const int d = (q - 8) / every;
-            dma_one(rsb, offb[d], cb[d], kbB, kbytes, dstB, d);
-            OCTO_FENCE();
-          }
-        }
+      } else if ((q & 1) == 1) {
+        opb.dma(k + DNSTAGE - 1, (q - 8) >> 1, kbytes, smem + prev_slot * DSTAGE + DSLICE);
+        OCTO_FENCE();
       }
     }
     __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);                                // this wave's reads of stage k are done
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 2)));     // stage k + 1 landed (this wave's part)
     __builtin_amdgcn_s_barrier();                                          // ... in every wave; stage k is free
     OCTO_FENCE();
-    // last sub-step: read the next stage's first fragments under the first 8 MFMAs, refill stage k's
-    // buffer (stage k + DNSTAGE) under the last 8
-    lds_char *refill = smem + slot * DSTAGE;
-    const uint32_t kb = (uint32_t)(k + DNSTAGE) * DKB;
+    // sub-step 1: read the next stage's first fragments under the first 8 MFMAs, refill stage k's slot with
+    // stage k + DNSTAGE's A slice under the last 8
     const lds_char *nxt = smem + next_slot * DSTAGE;
-    constexpr int LASTF = (DNSUB - 1) & 1;
-    constexpr int NV = SPLIT ? DIPW : 2 * DIPW;  // DMA instructions under the last sub-step
+    lds_char *refill = smem + slot * DSTAGE;
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      Mfma<DT>::run(fa[LASTF][q >> 2], fb[LASTF][q & 3], acc[q >> 2][q & 3]);
+      Mfma<DT>::run(fa[1][q >> 2], fb[1][q & 3], acc[q >> 2][q & 3]);
       OCTO_FENCE();
       if (q < 8) {
-        read_frag(nxt, aoff[0], boff[0], q, fa[0], fb[0]);
+        if (q < 4) fa[0][q] = opa.frag(nxt, 0, q);
+        else fb[0][q - 4] = opb.frag(nxt + DSLICE, 0, q - 4);
         OCTO_FENCE();
-      } else {
-        // NV DMA instructions over MFMAs 8..15: A slice first, then (ring of 2) the B slice
-#pragma unroll
-        for (int d = (q - 8) * NV / 8; d < (q - 7) * NV / 8; ++d) {
-          if (d < DIPW) dma_one(rsa, offa[d], ca[d], kb, kbytes, refill, d);
-          else dma_one(rsb, offb[d - DIPW], cb[d - DIPW], kb, kbytes, refill + 256 * DKB, d - DIPW);
-          OCTO_FENCE();
-        }
+      } else if ((q & 1) == 1) {
+        opa.dma(k + DNSTAGE, (q - 8) >> 1, kbytes, refill);
+        OCTO_FENCE();
       }
     }
     prev_slot = slot;

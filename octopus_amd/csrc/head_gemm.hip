@@ -5,8 +5,9 @@
 //   gemm_dz    : the same tile recomputed -> dz = g (onehot - p) / T * post'(z), written as bf16 in
 //                the row-major [tokens, V] layout and/or the vocab-major [V, tokens] layout
 //                (backward recompute, lm_head.py:118-121 under checkpoint)
-//   gemm_store : plain C = A . B^T with fp32/bf16/f16 output, optionally accumulated
-//                (grad_h = dz . W, grad_W = dz^T . h)
+//   gemm_store : plain C = A . B^T with fp32/bf16/f16 output, optionally accumulated, with either operand
+//                K-contiguous or MN-contiguous (grad_h = dz . W reads W as stored; grad_W = dz^T . h reads dz
+//                and the gathered hidden rows as stored)
 //
 // Orientation: the first operand (MFMA "A", tile rows) of gemm_stats / gemm_dz is the vocabulary,
 // the second (tile columns) the tokens. In the 32x32 MFMA output layout a lane holds one column
@@ -111,7 +112,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
   f32x16 acc[4][4];
   if constexpr (A_FP8) mainloop<DT, true>(A, B, m0, n0, s.K, smem, acc);
-  else mainloop_dma<DT>(A, B, m0, n0, s.K, smem, acc);
+  else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
   pre_transform<A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
@@ -338,7 +339,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
   f32x16 acc[4][4];
   if constexpr (A_FP8) mainloop<DT, true>(A, B, m0, n0, s.K, smem, acc);
-  else mainloop_dma<DT>(A, B, m0, n0, s.K, smem, acc);
+  else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
   if constexpr (A_FP8) pre_transform<true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
@@ -353,9 +354,11 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
 // ---- epilogue: plain store -------------------------------------------------------------------
 
-template <typename OT, bool ACC, bool EDGE>
-__device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], OT *C, int64_t ldc, int64_t m0, int64_t n0,
-                                           int64_t mvalid, int64_t nvalid, int wm, int wn, int lane) {
+// C = acc (+ addend, fp32, same strides) (+ C when ACC), rounded once to OT.
+template <typename OT, bool ACC, bool ADD, bool EDGE>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], OT *C, const float *addend, int64_t ldc,
+                                           int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int wm, int wn,
+                                           int lane) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -363,33 +366,43 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], OT *C, int
       const int rr = acc_row(wm, i, v, lane);
       if (EDGE && rr >= mvalid) continue;
       OT *crow = C + (m0 + rr) * ldc + n0;
+      const float *arow = ADD ? addend + (m0 + rr) * ldc + n0 : nullptr;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int cc = acc_col(wn, j, lane);
         if (EDGE && cc >= nvalid) continue;
         float x = acc[i][j][v];
+        if (ADD) x += arow[cc];
         if (ACC) x += (float)crow[cc];
         crow[cc] = (OT)x;
       }
     }
 }
 
+template <typename OT, bool ACC, bool ADD>
+__device__ __forceinline__ void store_edge(const f32x16 (&acc)[4][4], OT *C, const float *addend, int64_t ldc,
+                                           int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int wm, int wn,
+                                           int lane) {
+  if (mvalid < TM || nvalid < TN) store_tile<OT, ACC, ADD, true>(acc, C, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+  else store_tile<OT, ACC, ADD, false>(acc, C, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+}
+
 template <typename OT>
-__device__ __forceinline__ void store_any(const f32x16 (&acc)[4][4], void *C, int64_t ldc, int64_t m0, int64_t n0,
-                                          int64_t mvalid, int64_t nvalid, int accumulate) {
+__device__ __forceinline__ void store_any(const f32x16 (&acc)[4][4], void *C, const float *addend, int64_t ldc,
+                                          int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int accumulate) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
-  const bool edge = mvalid < TM || nvalid < TN;
   OT *c = (OT *)C;
   if (accumulate) {
-    if (edge) store_tile<OT, true, true>(acc, c, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
-    else store_tile<OT, true, false>(acc, c, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    if (addend) store_edge<OT, true, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    else store_edge<OT, true, false>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
   } else {
-    if (edge) store_tile<OT, false, true>(acc, c, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
-    else store_tile<OT, false, false>(acc, c, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    if (addend) store_edge<OT, false, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    else store_edge<OT, false, false>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
   }
 }
 
-template <int DT, int OT>
+// LAYOUT bit 0: A is MN-contiguous (OpCols), bit 1: B is.
+template <int DT, int OT, int LAYOUT>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
@@ -402,8 +415,10 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (mvalid <= 0 || nvalid <= 0) return;
 
   f32x16 acc[4][4];
-  mainloop_dma<DT>(A, B, m0, n0, K_eff, smem, acc);
-  store_any<typename Elem<OT>::T>(acc, e.C, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
+  typedef typename std::conditional<(LAYOUT & 1) != 0, OpCols, OpRows>::type OA;
+  typedef typename std::conditional<(LAYOUT & 2) != 0, OpCols, OpRows>::type OB;
+  mainloop_dma<DT, OA, OB>(A, B, m0, n0, K_eff, smem, acc);
+  store_any<typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
 }
 
 // ---- host launchers ----------------------------------------------------------------------------
@@ -451,24 +466,36 @@ int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operan
   return octo_fail(OCTO_EUNSUPPORTED, "gemm_dz: dtype %d", dt);
 }
 
-template <int DT>
+template <int DT, int LAYOUT>
 static int go_store(const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e, hipStream_t st) {
   switch (e.dtype) {
-    case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16, LAYOUT>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16, LAYOUT>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32, LAYOUT>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
     default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
   }
   OCTO_CHECK_LAUNCH("gemm_store");
   return OCTO_OK;
 }
 
-int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
+// MN-contiguous operands (layout != 0) take 16-bit types only.
+template <int DT>
+static int go_store_layout(int layout, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
+                           hipStream_t st) {
+  switch (layout) {
+    case 0: return go_store<DT, 0>(A, B, s, e, st);
+    case 2: if constexpr (DT != OCTO_F32) return go_store<DT, 2>(A, B, s, e, st); break;
+    case 3: if constexpr (DT != OCTO_F32) return go_store<DT, 3>(A, B, s, e, st); break;
+  }
+  return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: layout %d for dtype %d", layout, DT);
+}
+
+int launch_gemm_store(int dt, int layout, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
                       hipStream_t st) {
   switch (dt) {
-    case OCTO_BF16: return go_store<OCTO_BF16>(A, B, s, e, st);
-    case OCTO_F16: return go_store<OCTO_F16>(A, B, s, e, st);
-    case OCTO_F32: return go_store<OCTO_F32>(A, B, s, e, st);
+    case OCTO_BF16: return go_store_layout<OCTO_BF16>(layout, A, B, s, e, st);
+    case OCTO_F16: return go_store_layout<OCTO_F16>(layout, A, B, s, e, st);
+    case OCTO_F32: return go_store_layout<OCTO_F32>(layout, A, B, s, e, st);
   }
   return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: dtype %d", dt);
 }

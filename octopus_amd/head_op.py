@@ -120,17 +120,17 @@ def head_bwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
     if need_rows:
         # compact-order rows; scattered (runs of equal idx summed) into grad_rows below
         gh = grad_rows if idx is None else torch.empty(n_max, d, dtype=rows2.dtype, device=rows2.device)
-    gw32 = torch.empty(V, d, dtype=torch.float32, device=rows2.device) if need_weight else None
+    if need_weight:  # written in the weight's dtype (summed in fp32 inside, rounded once)
+        grad_w = torch.empty(V, d, dtype=weight.dtype, device=rows2.device)
     _lib.call("octo_head_bwd", _p(rows2), rows2.shape[0], rows2.stride(0), _dtype_code(rows2),
               _p(weight2), weight2.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
               n_max, d, V, flags, inv_T, pre, post, int(use_tanh), _p(lse.contiguous()),
-              _p(g.contiguous()), _p(gh), d, _dtype_code(rows2) if need_rows else _lib.F32, _p(gw32),
+              _p(g.contiguous()), _p(gh), d, _dtype_code(rows2) if need_rows else _lib.F32,
+              _p(grad_w if need_weight else None), _dtype_code(grad_w) if need_weight else _lib.F32,
               _p(ws), ws.numel(), _stream(rows2))
     if need_rows and idx is not None:
         _lib.call("octo_rows_scatter", _p(gh), d, _dtype_code(gh), _p(idx), _p(count), n_max, d,
                   _p(grad_rows), grad_rows.stride(0), _dtype_code(grad_rows), 0, _stream(rows2))
-    if need_weight:
-        grad_w = gw32 if weight.dtype == torch.float32 else gw32.to(weight.dtype)
     return grad_rows, grad_w
 
 

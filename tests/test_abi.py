@@ -31,11 +31,17 @@ def test_workspace_query():
     V, d = 151936, 2560
     fwd = _lib.workspace_bytes(32768, d, V, _lib.BF16, 0)
     assert fwd >= 32768 * ((V + 255) // 256) * 16
+    Vp = (V + 255) // 256 * 256
+    # 16-bit: one token-major dz stage [P, V_pad] and the gathered hidden rows [P, d]
     bwd = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_BACKWARD)
     no_gw = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_BACKWARD | _lib.WS_NO_GRADW)
-    Vp = (V + 255) // 256 * 256
-    assert bwd >= d * Vp * 2 + 2 * 32768 * Vp * 2 + d * 32768 * 2
-    assert no_gw < bwd
+    assert bwd >= 32768 * Vp * 2 + d * 32768 * 2 and bwd < 2 * 32768 * Vp * 2
+    assert no_gw >= 32768 * Vp * 2 and no_gw < bwd
+    # two passes of a 16-bit grad_W keep fp32 partial sums
+    assert _lib.workspace_bytes(65536, d, V, _lib.BF16, _lib.WS_BACKWARD) >= bwd + V * d * 4
+    # fp32: W^T [d, V_pad], h^T [d, P] and dz in both layouts
+    f32 = _lib.workspace_bytes(32768, d, V, _lib.F32, _lib.WS_BACKWARD)
+    assert f32 >= (d * Vp + 2 * 32768 * Vp + d * 32768) * 4
     with pytest.raises(ValueError):
         _lib.workspace_bytes(-1, d, V, _lib.BF16, 0)
 
