@@ -169,6 +169,8 @@ def main() -> int:
 
     def step():
         idx, count, out, lse = forward()
+        if cfg.backward == "none":  # a forward-only workload: logprob and entropy of every scored row
+            return out
         loss, g_flat = loss_grad(out)
         return backward(idx, count, lse, g_flat)
 
@@ -198,9 +200,11 @@ def main() -> int:
         ev[0].record()
         idx, count, out, lse = forward()
         ev[1].record()
-        loss, g_flat = loss_grad(out)
+        if cfg.backward != "none":
+            loss, g_flat = loss_grad(out)
         ev[2].record()
-        backward(idx, count, lse, g_flat)
+        if cfg.backward != "none":
+            backward(idx, count, lse, g_flat)
         ev[3].record()
         torch.cuda.synchronize()
         fwd_ms.append(ev[0].elapsed_time(ev[1]))
@@ -213,14 +217,16 @@ def main() -> int:
     exe_flop = {"full": 8, "hidden": 6, "none": 2}[cfg.backward] * n * d * V
     peak = PEAK_BF16 if cfg.dtype != torch.float32 else PEAK_F32
     step_s = ms / 1e3
-    # every GEMM kernel of the path is one dense contraction of 2 * n * d * V FLOP per launch (the pass
-    # holds all n scored rows at this size): logits (gemm_stats), logits again -> dz (gemm_dz),
-    # dz . W (gemm_store_grad_h), dz^T . h (gemm_store_grad_w)
-    flop_launch = 2 * n * d * V
-    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
-    dom_achieved = flop_launch / (kernels[dom]["avg_ms"] / 1e3)
+    # every GEMM kernel of the path is one dense contraction of 2 * n * d * V FLOP per step: logits
+    # (gemm_stats), logits again -> dz (gemm_dz), dz . W (gemm_store_grad_h), dz^T . h (gemm_store_grad_w);
+    # a kernel launched in several row passes does 2 * n * d * V / launches per launch on average
+    flop_step = 2 * n * d * V
     for k in kernels.values():
-        k["tflops"] = flop_launch / (k["avg_ms"] / 1e3) / 1e12
+        k["flop_per_launch"] = flop_step / k["launches_per_step"]
+        k["tflops"] = k["flop_per_launch"] / (k["avg_ms"] / 1e3) / 1e12
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+    flop_launch = kernels[dom]["flop_per_launch"]
+    dom_achieved = flop_launch / (kernels[dom]["avg_ms"] / 1e3)
     result = {
         "metric": "packed tokens/sec fwd+bwd logprob @ d=2560,V=151936 bf16; % MFMA peak",
         "value": cfg.N / step_s,
@@ -236,7 +242,8 @@ def main() -> int:
         "data": "synthetic (seeded: hidden N(0,1) RMS-normalised, W N(0,0.02), Zipf(1.1) targets)",
         "config": {"workload": f"{cfg.name}: packed tree micro-batch, fused fwd+bwd GRPO logprob head",
                    "N_packed": cfg.N, "scored_rows": n, "d": d, "V": V, "temperature": cfg.temperature,
-                   "backward": cfg.backward, "parallelism": "single GPU"},
+                   "backward": cfg.backward, "weight": "fp8 e4m3 + row scales" if cfg.fp8_weight else "as hidden",
+                   "parallelism": "single GPU"},
         "mfma_frac_algorithmic": alg_flop / step_s / peak,
         "mfma_frac_executed": exe_flop / step_s / peak,
         "phase_ms": {"forward": fwd_ms, "backward": bwd_ms},
@@ -244,8 +251,9 @@ def main() -> int:
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": dom_achieved / 1e12, "peak": peak / 1e12,
                      "unit": "TFLOP/s", "frac": dom_achieved / peak,
                      "traffic": recorded_traffic(dom, cfg.name),
-                     "per_launch": f"2*n*d*V = {flop_launch:.4g} FLOP (n={n} scored rows), HIP events around "
-                                   f"each launch over the timed steps"},
+                     "per_launch": f"2*n*d*V / launches = {flop_launch:.4g} FLOP (n={n} scored rows, "
+                                   f"{kernels[dom]['launches_per_step']:g} launches per step), HIP events "
+                                   f"around each launch over the timed steps"},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cfg, n)

@@ -89,7 +89,7 @@ int octo_compact_rows(const uint8_t *mask, int64_t n, int64_t *idx, int32_t *cou
  *   outputs          : logp[r], ent[r], lse[r] (any may be NULL) and, if out2 != NULL,
  *                      out2[row * ld_out2 + {0,1}] = {logp, entropy} with row = idx[r] under
  *                      OCTO_OUT_SCATTER, else r. Rows of out2 not written are left untouched.
- * Requires d % 8 == 0 (bf16/f16/fp8) or d % 4 == 0 (f32), inv_T > 0, pre * post > 0 when !use_tanh. */
+ * Requires d % 8 == 0 (bf16/f16), d % 16 == 0 (fp8) or d % 4 == 0 (f32), inv_T > 0, pre * post > 0 when !use_tanh. */
 int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                   const void *w, int64_t ldw, int w_dtype, const float *w_scale,
                   const int64_t *labels, const int64_t *idx, const int32_t *count,

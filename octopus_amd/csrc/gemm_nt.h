@@ -6,13 +6,10 @@
 // each owns a 128 x 128 sub-tile as 4 x 4 accumulators of v_mfma_f32_32x32x16_{bf16,f16}
 // (v_mfma_f32_32x32x2_f32 for fp32), i.e. all 256 accumulation registers of a wave.
 //
-// Two mainloops feed the MFMAs from LDS:
-//   mainloop_dma  (every bf16 / f16 / f32 contraction): the A and B K-slices go straight from global memory
-//                 into a ring of LDS stages by buffer_load_dwordx4 ... lds (no register hop), with the
-//                 instruction order fixed in the source: fragment reads a sub-step ahead of their MFMAs and
-//                 the DMA issues spread one per two MFMAs;
-//   mainloop      (fp8 weights): register-staged, so that e4m3 bytes can be widened to bf16 on the way
-//                 into LDS; K advances 128 bytes per step, double buffered (2 x 64 KB).
+// The mainloop feeds the MFMAs from LDS: the A and B K-slices go straight from global memory into a ring of
+// LDS stages by buffer_load_dwordx4 ... lds (no register hop), with the instruction order fixed in the source:
+// fragment reads a sub-step ahead of their MFMAs and the DMA issues spread between MFMAs. fp8 (e4m3) weights
+// travel to LDS as bytes and are widened to bf16 in registers, after the fragment read.
 //
 // Global loads are raw buffer loads: rows past the operand's end and K chunks past K read as zero
 // (voffset >= 2^31 is out of range), so partial tiles need no branches in the loop. Operand rows can
@@ -30,9 +27,7 @@ namespace octo {
 
 constexpr int TM = 256;          // tile rows (M)
 constexpr int TN = 256;          // tile cols (N)
-constexpr int KB = 128;          // K bytes per step
 constexpr int NTHREADS = 256;
-constexpr int TILE_BYTES = 256 * KB;  // one operand K-slice in LDS: 32 KB
 
 typedef __attribute__((address_space(3))) char lds_char;
 typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
@@ -101,146 +96,11 @@ template <> struct Mfma<OCTO_F32> {
   }
 };
 
-// 8 OCP e4m3 bytes -> 8 bf16 (exact), as one 16-byte chunk.
-__device__ __forceinline__ i32x4 fp8x8_to_bf16x8(i32x2 q) {
-  i32x4 o;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    uint32_t w = (uint32_t)q[h];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      float lo = e4m3_to_f32((w >> (16 * p)) & 0xffu);
-      float hi = e4m3_to_f32((w >> (16 * p + 8)) & 0xffu);
-      // fp32 -> bf16 is exact here (3 mantissa bits): keep the top 16 bits
-      o[2 * h + p] = (int)((__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u));
-    }
-  }
-  return o;
-}
-
 __device__ __forceinline__ const char *uniform_ptr(const char *p) {
   const uint64_t v = (uint64_t)p;
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
   return (const char *)(((uint64_t)hi << 32) | lo);
-}
-
-// Buffer resource and per-thread row offsets of one operand tile (rows row0 .. row0 + 255); the
-// thread loads rows (t >> 3) + 32 q, q = 0..7, at 16-byte chunk t & 7 of each K step.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t operand_rows(const Operand &op, int64_t row0, uint32_t (&off)[8]) {
-  const int t = threadIdx.x;
-  const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
-  if (op.map) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int r = (t >> 3) + 32 * q;
-      off[q] = (r < valid) ? (uint32_t)(op.map[row0 + r] * op.ld) : 0x80000000u;
-    }
-    return make_rsrc(uniform_ptr(op.base), op.extent);
-  }
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const int r = (t >> 3) + 32 * q;
-    off[q] = (r < valid) ? (uint32_t)(r * op.ld) : 0x80000000u;
-  }
-  return make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
-}
-
-// Stage one K step (kb = its first byte in a source row) into regs. A chunk past the row's K bytes
-// (kbytes) reads zero. FP8: the source holds 1 byte per element, widened to bf16.
-template <bool FP8>
-__device__ __forceinline__ void load_step(__amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[8], uint32_t kb,
-                                          uint32_t kbytes, i32x4 (&reg)[8]) {
-  const int c = threadIdx.x & 7;
-  constexpr uint32_t CH = FP8 ? 8 : 16;
-  const uint32_t kc = kb + c * CH;
-  const uint32_t dead = (kc < kbytes) ? 0u : 0x80000000u;
-#pragma unroll
-  for (int q = 0; q < 8; ++q) {
-    const uint32_t o = (off[q] | dead) + kc;
-    if constexpr (FP8) reg[q] = fp8x8_to_bf16x8(buf_load8(rs, (int)o));
-    else reg[q] = buf_load16(rs, (int)o);
-  }
-}
-
-__device__ __forceinline__ void lds_store_slice(lds_char *buf, const i32x4 (&reg)[8]) {
-  const int t = threadIdx.x;
-  const int r = t >> 3, c = t & 7;
-  lds_char *p = buf + r * KB + ((c ^ (r & 7)) << 4);
-#pragma unroll
-  for (int q = 0; q < 8; ++q) *(lds_i32x4 *)(p + q * 32 * KB) = reg[q];
-}
-
-// The mainloop. acc[i][j] is the 32x32 block (wm*128 + 32 i, wn*128 + 32 j) of the tile.
-// smem: SMEM_BYTES of LDS: [A0 | B0 | A1 | B1].
-template <int DT, bool A_FP8>
-__device__ __forceinline__ void mainloop(const Operand &A, const Operand &B, int64_t m0, int64_t n0, int64_t K_eff,
-                                         lds_char *smem, f32x16 (&acc)[4][4]) {
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int wm = w >> 1, wn = w & 1;
-
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  constexpr int ebytes = (DT == OCTO_F32) ? 4 : 2;
-  const uint32_t kbytes = (uint32_t)(K_eff * ebytes);               // staged bytes per row
-  const uint32_t kbytes_a = A_FP8 ? (uint32_t)K_eff : kbytes;        // source bytes per A row
-  const int nkt = (int)((kbytes + KB - 1) / KB);
-  if (nkt == 0) return;
-  constexpr uint32_t KBA = A_FP8 ? KB / 2 : KB;                      // source bytes per A step
-
-  uint32_t offa[8], offb[8];
-  const __amdgpu_buffer_rsrc_t rsa = operand_rows(A, m0, offa);
-  const __amdgpu_buffer_rsrc_t rsb = operand_rows(B, n0, offb);
-
-  // fragment byte offsets within a K-slice: row = base + (lane & 31), chunk = 2 ks + (lane >> 5)
-  int aoff[4], boff[4];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const int pc = ((2 * ks + (lane >> 5)) ^ (lane & 7)) << 4;
-    aoff[ks] = (wm * 128 + (lane & 31)) * KB + pc;
-    boff[ks] = TILE_BYTES + (wn * 128 + (lane & 31)) * KB + pc;
-  }
-
-  i32x4 ra[8], rb[8];
-  load_step<A_FP8>(rsa, offa, 0, kbytes_a, ra);
-  load_step<false>(rsb, offb, 0, kbytes, rb);
-  lds_store_slice(smem, ra);
-  lds_store_slice(smem + TILE_BYTES, rb);
-  __syncthreads();
-
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int cur = (kt & 1) * (2 * TILE_BYTES);
-    const bool more = kt + 1 < nkt;
-    if (more) {
-      load_step<A_FP8>(rsa, offa, (uint32_t)(kt + 1) * KBA, kbytes_a, ra);
-      load_step<false>(rsb, offb, (uint32_t)(kt + 1) * KB, kbytes, rb);
-    }
-    const lds_char *s = smem + cur;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      i32x4 af[4], bfr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *(const lds_i32x4 *)(s + aoff[ks] + i * 32 * KB);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bfr[j] = *(const lds_i32x4 *)(s + boff[ks] + j * 32 * KB);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) Mfma<DT>::run(af[i], bfr[j], acc[i][j]);
-    }
-    if (more) {
-      lds_char *nxt = smem + (2 * TILE_BYTES - cur);
-      lds_store_slice(nxt, ra);
-      lds_store_slice(nxt + TILE_BYTES, rb);
-    }
-    __syncthreads();
-  }
 }
 
 // ---- direct-to-LDS mainloop -----------------------------------------------------------------------
@@ -266,6 +126,12 @@ __device__ __forceinline__ void mainloop(const Operand &A, const Operand &B, int
 //     which the XOR spreads over all 64 banks exactly twice.
 //     The buffer descriptor is rebuilt per stage at the stage's first K-row, so operands larger than 4 GB stay
 //     within 32-bit offsets; K-rows at or past `krows` read zero.
+//   OpRowsF8 (K-contiguous e4m3 rows): a slice is 256 rows x 32 bytes (the same 32 K values per stage). Chunk c
+//     (0, 1) of row r sits at physical chunk c ^ ((r >> 3) & 1), so 16 lanes reading one logical chunk of 16
+//     consecutive rows cover all 64 banks once. One ds_read_b128 per block and stage serves both sub-steps:
+//     lane l holds row l & 31, K values 16 (l >> 5) + 0..15, and sub-step s widens K values 16 (l >> 5) + 8 s
+//     + 0..7 to bf16. The contraction does not depend on the order of K inside a stage, so the B operand of an
+//     fp8 GEMM (OpRowsT<true>) reads the same permutation: chunk 2 (l >> 5) + s instead of 2 s + (l >> 5).
 constexpr int DKB = 64;                    // K bytes per stage
 constexpr int DSLICE = 256 * DKB;          // one operand's stage slice (16 KB)
 constexpr int DSTAGE = 2 * DSLICE;         // A + B bytes per stage
@@ -275,22 +141,24 @@ constexpr int DSTAGE = 2 * DSLICE;         // A + B bytes per stage
 constexpr int DNSTAGE = OCTO_NSTAGE;       // ring depth
 constexpr int DIPW = 4;                    // DMA instructions per wave per operand and stage
 constexpr int DNSUB = 2;                   // 16-byte-fragment sub-steps per stage
-// LDS of one GEMM workgroup: the register-staged mainloop's 2 x (A + B) 32 KB slices or the DMA ring.
-constexpr int SMEM_BYTES = (4 * TILE_BYTES > DNSTAGE * DSTAGE) ? 4 * TILE_BYTES : DNSTAGE * DSTAGE;
+// LDS of one GEMM workgroup: the DMA ring.
+constexpr int SMEM_BYTES = DNSTAGE * DSTAGE;
 static_assert(SMEM_BYTES <= 160 * 1024, "LDS budget");
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] + vmcnt[5:4] at bits 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int WAIT_LGKM0 = 15 | (3 << 14) | (7 << 4);
-static_assert(2 * DIPW * DNSTAGE <= 63, "vmcnt range");
 
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, lds_char *dst) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, voff, 0, 0, 0);
 }
 
 // K-contiguous operand: instruction q of wave w fills slice rows (4 q + w) * 16 .. + 16; lane i takes row
-// + (i >> 2) and physical chunk i & 3.
-struct OpRows {
+// + (i >> 2) and physical chunk i & 3. KPERM: the fragment order of an fp8 GEMM's B operand (see OpRowsF8).
+template <bool KPERM>
+struct OpRowsT {
+  static constexpr int NI = DIPW;     // DMA instructions per wave and stage
+  static constexpr bool FP8 = false;  // one byte per element, widened after the fragment read
   __amdgpu_buffer_rsrc_t rs;
   uint32_t off[DIPW], coff[DIPW];
   int fo[DNSUB];  // fragment byte offsets in the slice (block 0)
@@ -310,8 +178,10 @@ struct OpRows {
     if (op.map) rs = make_rsrc(uniform_ptr(op.base), op.extent);
     else rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
 #pragma unroll
-    for (int ks = 0; ks < DNSUB; ++ks)
-      fo[ks] = (wsub * 128 + (lane & 31)) * DKB + (((2 * ks + (lane >> 5)) ^ ((lane >> 2) & 3)) << 4);
+    for (int ks = 0; ks < DNSUB; ++ks) {
+      const int c = KPERM ? 2 * (lane >> 5) + ks : 2 * ks + (lane >> 5);
+      fo[ks] = (wsub * 128 + (lane & 31)) * DKB + ((c ^ ((lane >> 2) & 3)) << 4);
+    }
   }
   // K chunks at or past kbytes (bytes per row) read zero
   __device__ __forceinline__ void dma(int k, int q, uint32_t kbytes, lds_char *slice) const {
@@ -323,10 +193,61 @@ struct OpRows {
     return *(const lds_i32x4 *)(slice + fo[sub] + blk * 32 * DKB);
   }
 };
+using OpRows = OpRowsT<false>;
+
+// K-contiguous e4m3 operand: instruction q of wave w fills slice rows (4 q + w) * 32 .. + 32; lane i takes row
+// + (i >> 1) and physical chunk i & 1. Rows must hold whole 16-byte chunks of K (K a multiple of 16).
+struct OpRowsF8 {
+  static constexpr int NI = 2;
+  static constexpr bool FP8 = true;
+  static constexpr int RB = DKB / 2;  // bytes per slice row
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t off[NI], coff[NI];
+  int fo;  // fragment byte offset in the slice (block 0)
+
+  __device__ __forceinline__ void init(const Operand &op, int64_t row0, int wsub, uint32_t /*krows*/) {
+    const int w = threadIdx.x >> 6, i = threadIdx.x & 63, lane = i;
+    const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int r = (4 * q + w) * 32 + (i >> 1);
+      coff[q] = (uint32_t)(((i & 1) ^ ((r >> 3) & 1)) << 4);
+      uint32_t rowoff;
+      if (r < valid) rowoff = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
+      else rowoff = 0x80000000u;
+      off[q] = rowoff + coff[q];
+    }
+    if (op.map) rs = make_rsrc(uniform_ptr(op.base), op.extent);
+    else rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
+    fo = (wsub * 128 + (lane & 31)) * RB + (((lane >> 5) ^ ((lane >> 3) & 1)) << 4);
+  }
+  // kbytes: K bytes per row (one per element)
+  __device__ __forceinline__ void dma(int k, int q, uint32_t kbytes, lds_char *slice) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t kb = (uint32_t)k * RB;
+    lds_dma16(rs, (kb + coff[q] < kbytes) ? off[q] + kb : 0x80000000u, slice + (4 * q + w) * 1024);
+  }
+  // 16 e4m3 values of row l & 31 of block blk, both sub-steps
+  __device__ __forceinline__ i32x4 frag(const lds_char *slice, int /*sub*/, int blk) const {
+    return *(const lds_i32x4 *)(slice + fo + blk * 32 * RB);
+  }
+  // sub-step s's 8 values as bf16 (exact: e4m3 has 3 mantissa bits and a narrower exponent range)
+  static __device__ __forceinline__ i32x4 widen(const i32x4 &raw, int s) {
+    i32x4 o;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      o[2 * h] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[2 * s + h], 1.0f, false));
+      o[2 * h + 1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[2 * s + h], 1.0f, true));
+    }
+    return o;
+  }
+};
 
 // MN-contiguous 16-bit operand: instruction q of wave w fills K-rows (4 q + w) * 2 and + 1 of the slice (lanes
 // 0..31, 32..63), lane i taking physical chunk i & 31.
 struct OpCols {
+  static constexpr int NI = DIPW;
+  static constexpr bool FP8 = false;
   const char *base;  // the tile's first column in K-row 0
   int64_t ld;        // bytes per K-row
   int64_t bytes;     // bytes addressable from base (the operand's rows x ld, less the column offset)
@@ -395,12 +316,17 @@ struct OpCols {
 // of MN-contiguous operands.
 //
 // Stage j's A slice is issued right after the barrier that frees its slot (in iteration j - DNSTAGE), its B slice
-// under the first sub-step of the next iteration (into the slot stage j - DNSTAGE left), so the 2 * DIPW DMA
-// instructions of a stage are spread over two sub-steps.
+// under the first sub-step of the next iteration (into the slot stage j - DNSTAGE left), so the DMA instructions
+// of a stage are spread over two sub-steps. An fp8 A operand reads its fragments once per stage (under sub-step 1
+// of the previous stage) and widens them under sub-step 0.
 template <int DT, typename OA, typename OB>
 __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B, int64_t m0, int64_t n0, int64_t K_eff,
                                              lds_char *smem, f32x16 (&acc)[4][4]) {
   static_assert(DNSTAGE >= 3, "ring depth");
+  static_assert(!OB::FP8 && (!OA::FP8 || DT == OCTO_BF16), "fp8: A operand, bf16 MFMAs");
+  constexpr int NA = OA::NI, NB = OB::NI, NPS = NA + NB;  // DMA instructions per wave and stage
+  constexpr int SPA = 8 / NA, SPB = 8 / NB;                // MFMAs between two DMA issues
+  static_assert(NPS * DNSTAGE <= 63, "vmcnt range");
   const int w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1;
 #pragma unroll
@@ -412,6 +338,7 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
 
   constexpr int ebytes = (DT == OCTO_F32) ? 4 : 2;
   const uint32_t kbytes = (uint32_t)(K_eff * ebytes);
+  const uint32_t kbytes_a = OA::FP8 ? (uint32_t)K_eff : kbytes;
   const int nk = (int)((kbytes + DKB - 1) / DKB);
   if (nk == 0) return;
 
@@ -423,19 +350,20 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
 #pragma unroll
   for (int st = 0; st < DNSTAGE; ++st) {
 #pragma unroll
-    for (int q = 0; q < DIPW; ++q) opa.dma(st, q, kbytes, smem + st * DSTAGE);
+    for (int q = 0; q < NA; ++q) opa.dma(st, q, kbytes_a, smem + st * DSTAGE);
     if (st < DNSTAGE - 1) {
 #pragma unroll
-      for (int q = 0; q < DIPW; ++q) opb.dma(st, q, kbytes, smem + st * DSTAGE + DSLICE);
+      for (int q = 0; q < NB; ++q) opb.dma(st, q, kbytes, smem + st * DSTAGE + DSLICE);
     }
   }
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 2) + DIPW));  // stage 0 landed
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(NPS * (DNSTAGE - 2) + NA));  // stage 0 landed
   __builtin_amdgcn_s_barrier();
 
-  i32x4 fa[2][4], fb[2][4];
+  i32x4 fa[2][4], fb[2][4], ra[4];  // ra: an fp8 A operand's raw fragments (both sub-steps)
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    fa[0][b] = opa.frag(smem, 0, b);
+    if constexpr (OA::FP8) ra[b] = opa.frag(smem, 0, b);
+    else fa[0][b] = opa.frag(smem, 0, b);
     fb[0][b] = opb.frag(smem + DSLICE, 0, b);
   }
   int slot = 0;                 // k % DNSTAGE
@@ -445,24 +373,34 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
     const lds_char *cur = smem + slot * DSTAGE;
     __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // this sub-step's fragments (read under the previous one) are in
     OCTO_FENCE();
-    // sub-step 0: read sub-step 1's fragments under the first 8 MFMAs; the B slice of stage k + DNSTAGE - 1
-    // (into the slot stage k - 1 left) under the last 8
+    if constexpr (OA::FP8) {
+      fa[0][0] = OA::widen(ra[0], 0);
+      OCTO_FENCE();
+    }
+    // sub-step 0: read sub-step 1's fragments under the first 8 MFMAs (fp8 A: widen them instead); the B slice
+    // of stage k + DNSTAGE - 1 (into the slot stage k - 1 left) under the last 8
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       Mfma<DT>::run(fa[0][q >> 2], fb[0][q & 3], acc[q >> 2][q & 3]);
       OCTO_FENCE();
-      if (q < 8) {
+      if constexpr (OA::FP8) {
+        if ((q & 3) == 0 && q < 12) fa[0][(q >> 2) + 1] = OA::widen(ra[(q >> 2) + 1], 0);
+        if ((q & 3) == 2) fa[1][q >> 2] = OA::widen(ra[q >> 2], 1);
+        if (q < 4) fb[1][q] = opb.frag(cur + DSLICE, 1, q);
+        OCTO_FENCE();
+      } else if (q < 8) {
         if (q < 4) fa[1][q] = opa.frag(cur, 1, q);
         else fb[1][q - 4] = opb.frag(cur + DSLICE, 1, q - 4);
         OCTO_FENCE();
-      } else if ((q & 1) == 1) {
-        opb.dma(k + DNSTAGE - 1, (q - 8) >> 1, kbytes, smem + prev_slot * DSTAGE + DSLICE);
+      }
+      if (q >= 8 && (q - 8) % SPB == SPB - 1) {
+        opb.dma(k + DNSTAGE - 1, (q - 8) / SPB, kbytes, smem + prev_slot * DSTAGE + DSLICE);
         OCTO_FENCE();
       }
     }
-    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);                                // this wave's reads of stage k are done
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * DIPW * (DNSTAGE - 2)));     // stage k + 1 landed (this wave's part)
-    __builtin_amdgcn_s_barrier();                                          // ... in every wave; stage k is free
+    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);                           // this wave's reads of stage k are done
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(NPS * (DNSTAGE - 2)));     // stage k + 1 landed (this wave's part)
+    __builtin_amdgcn_s_barrier();                                     // ... in every wave; stage k is free
     OCTO_FENCE();
     // sub-step 1: read the next stage's first fragments under the first 8 MFMAs, refill stage k's slot with
     // stage k + DNSTAGE's A slice under the last 8
@@ -473,11 +411,16 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
       Mfma<DT>::run(fa[1][q >> 2], fb[1][q & 3], acc[q >> 2][q & 3]);
       OCTO_FENCE();
       if (q < 8) {
-        if (q < 4) fa[0][q] = opa.frag(nxt, 0, q);
-        else fb[0][q - 4] = opb.frag(nxt + DSLICE, 0, q - 4);
+        if (q < 4) {
+          if constexpr (OA::FP8) ra[q] = opa.frag(nxt, 0, q);
+          else fa[0][q] = opa.frag(nxt, 0, q);
+        } else {
+          fb[0][q - 4] = opb.frag(nxt + DSLICE, 0, q - 4);
+        }
         OCTO_FENCE();
-      } else if ((q & 1) == 1) {
-        opa.dma(k + DNSTAGE, (q - 8) >> 1, kbytes, refill);
+      }
+      if (q >= 8 && (q - 8) % SPA == SPA - 1) {
+        opa.dma(k + DNSTAGE, (q - 8) / SPA, kbytes_a, refill);
         OCTO_FENCE();
       }
     }

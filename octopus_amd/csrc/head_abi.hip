@@ -152,11 +152,11 @@ int check_common(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const 
   cm.wesz = elem_bytes(w_dtype);
   cm.dt = staged_dtype(w_dtype);
   cm.fp8 = fp8;
-  const int kq = (h_dtype == OCTO_F32) ? 4 : 8;
+  const int kq = (h_dtype == OCTO_F32) ? 4 : (fp8 ? 16 : 8);
   OCTO_CHECK_ARG(d % kq == 0, "head: d=%d must be a multiple of %d", d, kq);
   OCTO_CHECK_ARG(ldh >= d && ldw >= d, "head: row strides below d");
   OCTO_CHECK_ARG((ldh * cm.hesz) % 16 == 0 && ((uintptr_t)h) % 16 == 0, "head: hidden rows must be 16-byte aligned");
-  OCTO_CHECK_ARG((ldw * cm.wesz) % (fp8 ? 8 : 16) == 0 && ((uintptr_t)w) % 16 == 0,
+  OCTO_CHECK_ARG((ldw * cm.wesz) % 16 == 0 && ((uintptr_t)w) % 16 == 0,
                  "head: weight rows must be 16-byte aligned");
   OCTO_CHECK_ARG(!fp8 || ((uintptr_t)w_scale) % 16 == 0, "head: w_scale must be 16-byte aligned");
   OCTO_CHECK_ARG(256 * ldh * cm.hesz < (int64_t)0x7fffffff && 256 * ldw * cm.wesz < (int64_t)0x7fffffff,

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (nvalid <= 0) return;
 
   f32x16 acc[4][4];
-  if constexpr (A_FP8) mainloop<DT, true>(A, B, m0, n0, s.K, smem, acc);
+  if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
   else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
@@ -338,7 +338,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (nvalid <= 0) return;
 
   f32x16 acc[4][4];
-  if constexpr (A_FP8) mainloop<DT, true>(A, B, m0, n0, s.K, smem, acc);
+  if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
   else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;

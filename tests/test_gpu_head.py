@@ -68,6 +68,40 @@ def test_backward_matches_oracle(dtype, shape):
         assert _rel(hd.grad.cpu(), gh) <= bar and _rel(Wd.grad.cpu(), gw) <= bar, (T, post)
 
 
+FP8_SHAPES = [(1, 64, 100), (300, 64, 1000), (513, 256, 5000), (256, 48, 777), (70, 2560, 3000)]
+
+
+@pytest.mark.parametrize("shape", FP8_SHAPES, ids=[f"{n}x{d}x{V}" for n, d, V in FP8_SHAPES])
+def test_fp8_weights_match_oracle_on_dequantised_weights(shape):
+    """e4m3 weights with per-row scales (bf16 hidden rows): logprob / entropy and grad_hidden against the oracle on
+    the dequantised weights (e4m3 value x row scale), every row and through a compacted subset."""
+    from octopus_amd.workloads import quantise_fp8_rows
+    n, d, V = shape
+    h, W, y = _inputs(n, d, V, torch.bfloat16, seed=3)
+    Wq, scale = quantise_fp8_rows(W)
+    W32 = Wq.float() * scale[:, None]
+    g = torch.randn(n, generator=torch.Generator().manual_seed(5))
+    for T, post in ((1.0, Post()), (0.7, Post(0.5, 2.0, True))):
+        hd = h.to(DEV).requires_grad_(True)
+        out = fused_head(hd, Wq.to(DEV), y.to(DEV), T, post, w_scale=scale.to(DEV))
+        (out[:, 0] * g.to(DEV)).sum().backward()
+        lp, ent, _ = ohead.head_forward(h, W32, y, T, post.pre, post.post, post.tanh)
+        assert (out[:, 0].cpu().double() - lp).abs().max() <= 2e-3, (T, post)
+        assert (out[:, 1].cpu().double() - ent).abs().max() <= 2e-3, (T, post)
+        gh, _ = ohead.head_backward(h, W32, y, T, g, post.pre, post.post, post.tanh, want_w=False)
+        assert _rel(hd.grad.cpu(), gh) <= 1e-2, (T, post)
+    # scored subset: rows gathered through idx, outputs scattered back
+    mask = torch.rand(n, generator=torch.Generator().manual_seed(6)) < 0.6
+    mask[0] = True
+    idx, count = head_op.compact_rows(mask.to(DEV))
+    out = fused_head(h.to(DEV), Wq.to(DEV), y.to(DEV), 1.0, idx=idx, count=count, labels_via_idx=True,
+                     scatter=True, w_scale=scale.to(DEV)).cpu()
+    lp, ent, _ = ohead.head_forward(h[mask], W32, y[mask], 1.0)
+    assert (out[~mask] == 0).all()
+    assert (out[mask, 0].double() - lp).abs().max() <= 2e-3
+    assert (out[mask, 1].double() - ent).abs().max() <= 2e-3
+
+
 def test_compaction_is_bit_exact_nonzero():
     rng = np.random.default_rng(0)
     for n in (1, 63, 64, 65, 1023, 1024, 1025, 32768, 131072 + 7):
