@@ -22,6 +22,7 @@ import platform
 import sys
 import time
 
+import numpy as np
 import torch
 
 PEAK_BF16 = 2.5e15  # MI355X dense bf16 MFMA, FLOP/s (AMD public spec)
@@ -102,6 +103,69 @@ def library_gemms(workload: str, reps: int = 5) -> dict:
     return out
 
 
+def pairs_bench(workload: str, steps: int, warmup: int) -> dict:
+    """The label-pair section of the prefix tree (octo_label_pairs) at a root-plus-branches workload: the
+    sequences are root + branch, flattened (T_flat tokens), over the packed tree of N tokens; branch tokens are
+    scored. Device time from HIP events over `steps` calls; the host restatement (numpy np.unique, as the
+    reference runs it) timed beside it."""
+    from octopus_amd import head_op
+    from octopus_amd.rl.prefix_tree import build_tree, label_pairs as host_pairs
+    from octopus_amd.workloads import CONFIGS
+    cfg = CONFIGS[workload]
+    root, branches = cfg.segments[0], cfg.segments[1:]
+    if root[1] or not all(b[1] for b in branches):
+        raise SystemExit(f"--pairs takes a root-plus-branches workload (cfg3, cfg5), not {workload}")
+    rng = np.random.default_rng(5)
+    r_tok = rng.integers(0, cfg.V, root[0])
+    seqs = [np.concatenate([r_tok, rng.integers(0, cfg.V, n)]) for n, _, _ in branches]
+    flat = np.concatenate(seqs).astype(np.int64)
+    cu = np.array([0, *np.cumsum([len(x) for x in seqs])], dtype=np.int64)
+    scored = np.ones(len(flat), dtype=bool)
+    for a in cu[:-1]:
+        scored[a:a + root[0]] = False
+    tree = build_tree(flat, cu, scored=scored)
+    dev = torch.device("cuda", 0)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    fd, cud, f2t, sc = t(flat), t(cu), t(tree.flat_to_tree), t(scored)
+    T_tree = len(tree.tokens)
+    for _ in range(warmup):
+        head_op.label_pairs(fd, cud, f2t, T_tree, sc, True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        pos, lab, fp, count = head_op.label_pairs(fd, cud, f2t, T_tree, sc, True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    P = int(count[0].item())
+    assert P == len(tree.pair_pos) and torch.equal(pos[:P].cpu(), torch.from_numpy(tree.pair_pos))
+    # algorithmic bytes: flat token, tree position, scored flag read and flat_pair written per flat position;
+    # (position, label) written per pair
+    T = len(flat)
+    alg = T * (8 + 8 + 1 + 8) + P * 16
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < 2.0:
+        host_pairs(flat, cu, tree.flat_to_tree, scored)
+        reps += 1
+    host_s = (time.perf_counter() - t0) / reps
+    return {"metric": "label pairs per second (prefix_tree.py:156-166 on the device)", "value": T / (ms / 1e3),
+            "unit": "flat tokens/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": ms,
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+            "data": "synthetic (seeded tokens; root prompt unscored, branches scored)",
+            "config": {"workload": f"{workload}: {len(seqs)} sequences of root {root[0]} + branch, label pairs",
+                       "T_flat": T, "T_tree": T_tree, "pairs": P},
+            "roofline": {"kernel": "octo_label_pairs (9 launches)", "bound": "hbm",
+                         "achieved": alg / (ms / 1e3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                         "frac": alg / (ms / 1e3) / PEAK_HBM, "traffic": None,
+                         "per_launch": f"{alg} algorithmic bytes per call (25 B per flat position + 16 B per "
+                                       f"pair); the call is launch- and latency-bound at this size"},
+            "cpu_baseline": {"value": T / host_s, "unit": "flat tokens/s", "cores": 1, "kind": "port",
+                             "sample": f"host label_pairs (numpy np.unique over (position, label)) on the same "
+                                       f"{T} flat positions, {reps} runs, {host_s * 1e3:.2f} ms each; host: "
+                                       f"{_cpu_model()}"}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -112,6 +176,9 @@ def main() -> int:
     ap.add_argument("--hipblaslt", action="store_true",
                     help="only time torch.matmul (hipBLASLt) on the four plain GEMMs of the workload's step, "
                          "without any epilogue, for context; then exit")
+    ap.add_argument("--pairs", action="store_true",
+                    help="only time the device label-pair section of the prefix tree (octo_label_pairs) at the "
+                         "workload's tree against the host numpy restatement; then exit")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB three times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes), then exit")
@@ -127,6 +194,9 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4}), flush=True)
+        return 0
+    if args.pairs:
+        print(json.dumps(pairs_bench(args.workload, args.steps, args.warmup)), flush=True)
         return 0
     if args.hipblaslt:
         print(json.dumps(library_gemms(args.workload)), flush=True)

@@ -27,6 +27,8 @@
  *   octopus/rl/lm_head.py:124-130  _scored_rows     -> octo_compact_rows + OCTO_ROWS_VIA_IDX /
  *                                                     OCTO_OUT_SCATTER modes of octo_head_fwd
  *   octopus/rl/prefix_tree.py:416-421 tree_head_output -> octo_pairs_expand / octo_pairs_grad
+ *   octopus/rl/prefix_tree.py:156-166 build_tree, label-pair section (np.unique over packed
+ *                                     (position, label)) -> octo_label_pairs
  *   AReaL grpo_loss_fn (cited by docs/rl-plan-episodes.md:496-497, constants grpo.yaml:103-118)
  *                                                  -> octo_grpo_grad
  */
@@ -59,6 +61,7 @@ extern "C" {
 #define OCTO_GRADW_ACCUMULATE 4  /* grad_w += contribution (else grad_w = contribution)               */
 #define OCTO_WS_BACKWARD      8  /* octo_head_workspace_bytes: size for octo_head_bwd                 */
 #define OCTO_WS_NO_GRADW     16  /* octo_head_workspace_bytes: backward without grad_w                */
+#define OCTO_PAIRS_NONE_AS_COUNT 1 /* octo_label_pairs: positions without a pair get the pair count  */
 
 const char *octo_version(void);
 const char *octo_last_error(void);
@@ -133,6 +136,23 @@ int octo_pairs_expand(const float *pairs, int64_t P, int C, const int64_t *flat_
  * (grad_pairs is overwritten). */
 int octo_pairs_grad(const float *grad_flat, int64_t T, int C, const int64_t *flat_pair, int64_t P,
                     float *grad_pairs, void *stream);
+
+/* Label pairs of a prefix tree (prefix_tree.py:156-166), on the device. Flat position p asks when
+ * scored[p] != 0 (scored NULL: every p), p + 1 < T_flat and p is not the last position of its
+ * sequence (p != cu[s + 1] - 1 for any s < n_seq; cu holds n_seq + 1 device offsets, a -1 read as the
+ * last flat position); its ask is (flat_to_tree[p], flat[p + 1]). Distinct asks are the pairs, numbered in
+ * ascending (tree position, label) order:
+ *   pair_pos[i], pair_label[i]  for i < P (both hold at least T_flat entries; later ones unspecified);
+ *   flat_pair[p]                the pair of p's ask, else -1 (OCTO_PAIRS_NONE_AS_COUNT: P, the index of the
+ *                               appended zero row of prefix_tree.py:203-205);
+ *   count[0] = P, count[1] = asks whose flat_to_tree entry lies outside [0, T_tree) (ignored; 0 for a
+ *                               valid tree). Both written on the device.
+ * flat and flat_to_tree hold T_flat entries; T_flat, T_tree < 2^31. ws: octo_label_pairs_workspace_bytes. */
+int octo_label_pairs_workspace_bytes(int64_t T_flat, int64_t T_tree, size_t *bytes);
+int octo_label_pairs(const int64_t *flat, int64_t T_flat, const int64_t *cu, int64_t n_seq,
+                     const int64_t *flat_to_tree, int64_t T_tree, const uint8_t *scored,
+                     int64_t *pair_pos, int64_t *pair_label, int64_t *flat_pair, int32_t *count,
+                     int flags, void *ws, size_t ws_bytes, void *stream);
 
 /* dst[idx[r], :d] (+)= src[r, :d] for r < *count, with idx ascending (repeats allowed: the rows of
  * one run are summed in fp32 first). dst rows not named by idx are untouched; accumulate != 0 adds

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "libocto_head.so")
 OK, EINVAL, EWORKSPACE, EUNSUPPORTED, EHIP = 0, -1, -2, -3, -4
 BF16, F16, F32, FP8E4M3 = 0, 1, 2, 3
 ROWS_VIA_IDX, OUT_SCATTER, GRADW_ACCUMULATE, WS_BACKWARD, WS_NO_GRADW = 1, 2, 4, 8, 16
+PAIRS_NONE_AS_COUNT = 1
 
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -44,6 +45,8 @@ SIGNATURES = {
     "octo_pairs_grad": [_p, _i64, _i32, _p, _i64, _p, _p],
     "octo_rows_scatter": [_p, _i64, _i32, _p, _p, _i64, _i32, _p, _i64, _i32, _i32, _p],
     "octo_gather_f32": [_p, _i64, _p, _p, _i64, _p, _p],
+    "octo_label_pairs_workspace_bytes": [_i64, _i64, ctypes.POINTER(_sz)],
+    "octo_label_pairs": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i32, _p, _sz, _p],
     "octo_grpo_workspace_bytes": [ctypes.POINTER(_sz)],
     "octo_grpo_grad": [_p, _p, _p, _p, _p, _i64, _f32, _f32, _f32, _p, _p, _p, _sz, _p],
 }

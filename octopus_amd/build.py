@@ -19,7 +19,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libocto_head.so")
-SOURCES = ["head_abi.hip", "head_gemm.hip", "head_aux.hip"]
+SOURCES = ["head_abi.hip", "head_gemm.hip", "head_aux.hip", "tree_pairs.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 generation (the host pass warns it does not know the

@@ -49,8 +49,8 @@ struct TimedLaunch {
   TimedLaunch(const char *n, hipStream_t s) : name(n), st(s) {
     if (!g_timing) return;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess || hipEventRecord(a, st) != hipSuccess) {
-      if (a) hipEventDestroy(a);
-      if (b) hipEventDestroy(b);
+      if (a) (void)hipEventDestroy(a);
+      if (b) (void)hipEventDestroy(b);
       a = b = nullptr;
     }
   }
@@ -60,8 +60,8 @@ struct TimedLaunch {
       std::lock_guard<std::mutex> lk(g_timing_mu);
       g_timed.push_back({name, a, b});
     } else {
-      hipEventDestroy(a);
-      hipEventDestroy(b);
+      (void)hipEventDestroy(a);
+      (void)hipEventDestroy(b);
     }
     a = b = nullptr;
   }
@@ -252,8 +252,8 @@ const char *octo_last_error(void) { return g_err; }
 int octo_timing_enable(int on) {
   std::lock_guard<std::mutex> lk(g_timing_mu);
   for (auto &t : g_timed) {
-    hipEventDestroy(t.a);
-    hipEventDestroy(t.b);
+    (void)hipEventDestroy(t.a);
+    (void)hipEventDestroy(t.b);
   }
   g_timed.clear();
   g_timing = on != 0;

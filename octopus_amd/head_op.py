@@ -288,6 +288,38 @@ torch.library.register_autograd("octohead::pairs_expand", _pairs_backward, setup
 
 # ---- masked-row compaction -----------------------------------------------------------------------
 
+def label_pairs(flat: Tensor, cu: Tensor, flat_to_tree: Tensor, T_tree: int, scored: Optional[Tensor] = None,
+                none_as_count: bool = False) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """The label pairs of prefix_tree.py:156-166 on the device: (pair_pos [T_flat], pair_label [T_flat],
+    flat_pair [T_flat], count [2] int32), with count[0] = P pairs in pair_pos / pair_label[:P], sorted by
+    (tree position, label); flat_pair = -1 (none_as_count: P) where a position has no pair; count[1] = asks
+    whose tree position lay outside [0, T_tree) (0 for a valid tree). No host synchronisation."""
+    dev = flat.device
+    flat = _index(flat.reshape(-1))
+    f2t = _index(flat_to_tree.reshape(-1))
+    cu = _index(cu.reshape(-1).to(dev))
+    T = flat.numel()
+    if f2t.numel() != T:
+        raise ValueError(f"label_pairs: flat_to_tree has {f2t.numel()} entries for {T} flat positions")
+    sc = None
+    if scored is not None:
+        sc = scored.reshape(-1)
+        if sc.numel() != T:
+            raise ValueError(f"label_pairs: scored has {sc.numel()} entries for {T} flat positions")
+        sc = (sc != 0).contiguous().view(torch.uint8) if sc.dtype != torch.uint8 else sc.contiguous()
+    nbytes = ctypes.c_size_t(0)
+    _lib.call("octo_label_pairs_workspace_bytes", T, int(T_tree), ctypes.byref(nbytes))
+    ws = _workspace(nbytes.value, flat)
+    pair_pos = torch.empty(T, dtype=torch.int64, device=dev)
+    pair_label = torch.empty(T, dtype=torch.int64, device=dev)
+    flat_pair = torch.empty(T, dtype=torch.int64, device=dev)
+    count = torch.empty(2, dtype=torch.int32, device=dev)
+    _lib.call("octo_label_pairs", _p(flat), T, _p(cu), cu.numel() - 1, _p(f2t), int(T_tree), _p(sc), _p(pair_pos),
+              _p(pair_label), _p(flat_pair), _p(count), _lib.PAIRS_NONE_AS_COUNT if none_as_count else 0, _p(ws),
+              ws.numel(), _stream(flat))
+    return pair_pos, pair_label, flat_pair, count
+
+
 def compact_rows(mask: Tensor) -> tuple[Tensor, Tensor]:
     """(idx [n] int64, count [1] int32): idx[:count] = positions of the true entries, ascending, as
     mask.nonzero()[:, 0]; count stays on the device (no host synchronisation)."""

@@ -210,7 +210,8 @@ def _pair_rows(self):
     def rows_fn(rows, y):
         return _chunked_rows(self, rows, y)
 
-    rows_fn.octopus_fused_rows = lambda hidden2d, pair_pos, y: _hip_head(self, hidden2d, y, idx=pair_pos)
+    rows_fn.octopus_fused_rows = lambda hidden2d, pair_pos, y, count=None: _hip_head(self, hidden2d, y, idx=pair_pos,
+                                                                                      count=count)
     return rows_fn
 
 

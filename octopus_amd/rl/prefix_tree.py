@@ -37,6 +37,7 @@ class Tree:
     pair_pos: np.ndarray  # (P,) tree position whose hidden state scores a label
     pair_label: np.ndarray  # (P,) that label (the next token)
     flat_pair: np.ndarray  # (T_flat,) pair of each flat position, -1 when none
+    flat_to_tree: np.ndarray | None = None  # (T_flat,) tree position of each flat token (input of on_device)
 
 
 def _shared_run(seqs: list, ids: list, offset: int) -> int:
@@ -97,7 +98,7 @@ def build_tree(flat: np.ndarray, cu, mounts=None, scored: np.ndarray | None = No
     flat_to_tree = np.concatenate([nodes[t].path if t >= 0 else np.empty(0, dtype=np.int64) for t in terminal]
                                   + [np.empty(0, dtype=np.int64)])
     pair_pos, pair_label, flat_pair = label_pairs(flat, cu, flat_to_tree, scored)
-    return Tree(tree_tokens, nodes, position_ids, pair_pos, pair_label, flat_pair)
+    return Tree(tree_tokens, nodes, position_ids, pair_pos, pair_label, flat_pair, flat_to_tree)
 
 
 def label_pairs(flat: np.ndarray, cu, flat_to_tree: np.ndarray, scored: np.ndarray | None = None):
@@ -121,7 +122,13 @@ def label_pairs(flat: np.ndarray, cu, flat_to_tree: np.ndarray, scored: np.ndarr
 
 class TreeMeta:
     """The tree's pair tensors on a device (prefix_tree.py:200-205): pair_pos, pair_label and flat_pair,
-    with -1 (no pair) mapped to P, the index of an appended zero row."""
+    with -1 (no pair) mapped to P, the index of an appended zero row.
+
+    `TreeMeta.on_device` builds the same pairs on a HIP device instead of on the host: then pair_pos and
+    pair_label have T_flat entries of which the first P are the pairs, P stays on the device (`pair_count`),
+    and flat_pair holds -1 where a position has no pair."""
+
+    pair_count = None  # [1] int32 on the device when the pairs were built there
 
     def __init__(self, tree: Tree, device):
         self.n_tokens = len(tree.tokens)
@@ -130,6 +137,19 @@ class TreeMeta:
         flat_pair = tree.flat_pair.copy()
         flat_pair[flat_pair < 0] = len(tree.pair_pos)
         self.flat_pair = torch.from_numpy(flat_pair).to(device)
+
+    @classmethod
+    def on_device(cls, flat: torch.Tensor, cu: torch.Tensor, flat_to_tree: torch.Tensor, n_tokens: int,
+                  scored: torch.Tensor | None = None) -> "TreeMeta":
+        """The pair section of build_tree (prefix_tree.py:156-166) run by the octo_label_pairs kernels on the
+        device of `flat`: flat [T_flat] tokens, cu [n_seq + 1] sequence offsets, flat_to_tree [T_flat] tree
+        position of each flat token (the tree built on the host), n_tokens = T_tree."""
+        from octopus_amd.head_op import label_pairs
+        self = cls.__new__(cls)
+        self.n_tokens = int(n_tokens)
+        self.pair_pos, self.pair_label, self.flat_pair, count = label_pairs(flat, cu, flat_to_tree, n_tokens, scored)
+        self.pair_count = count[:1]
+        return self
 
 
 def tree_head_output(chunk_fn, hidden: torch.Tensor, meta: TreeMeta) -> torch.Tensor:
@@ -140,8 +160,13 @@ def tree_head_output(chunk_fn, hidden: torch.Tensor, meta: TreeMeta) -> torch.Te
     gathers the pair rows inside its GEMM instead of materialising them, and the expansion is the
     octohead::pairs_expand kernel."""
     fused = getattr(chunk_fn, "octopus_fused_rows", None)
+    if meta.pair_count is not None and not (hidden.is_cuda and fused is not None):
+        raise ValueError("pairs built on the device (TreeMeta.on_device) need a HIP hidden and the bound head")
     if hidden.is_cuda and fused is not None:
-        pairs = fused(hidden[0], meta.pair_pos, meta.pair_label)
+        if meta.pair_count is not None:  # P on the device: rows at and past it are left out by the head
+            pairs = fused(hidden[0], meta.pair_pos, meta.pair_label, count=meta.pair_count)
+        else:
+            pairs = fused(hidden[0], meta.pair_pos, meta.pair_label)
     else:
         pairs = chunk_fn(hidden[0].index_select(0, meta.pair_pos), meta.pair_label)
     if hidden.is_cuda and pairs.dtype == torch.float32:

@@ -85,6 +85,15 @@ def test_small_entry_point_checks():
     with pytest.raises(ValueError):
         _lib.call("octo_grpo_grad", P, None, None, P, P, 4, 0.2, 0.28, 5.0, P, None, None, 0, None)
     assert _lib.grpo_workspace_bytes() >= 4
+    nbytes = ctypes.c_size_t(0)
+    _lib.call("octo_label_pairs_workspace_bytes", 131072, 114688, ctypes.byref(nbytes))
+    assert nbytes.value >= 131072 * 13 + 114688 * 20
+    with pytest.raises(ValueError):
+        _lib.call("octo_label_pairs_workspace_bytes", 1 << 31, 5, ctypes.byref(nbytes))
+    with pytest.raises(ValueError):  # unknown flag
+        _lib.call("octo_label_pairs", P, 7, P, 2, P, 5, None, P, P, P, P, 8, P, 1 << 20, None)
+    with pytest.raises(ValueError):  # no workspace
+        _lib.call("octo_label_pairs", P, 7, P, 2, P, 5, None, P, P, P, P, 0, None, 0, None)
 
 
 def test_timing_hook_without_launches():

@@ -41,6 +41,7 @@ def test_build_tree_matches_the_trie_oracle(seed):
     tree = build_tree(flat, cu, scored=scored)
     tokens, f2t, posid = opairs.tree_positions(flat, cu)
     assert np.array_equal(tree.tokens, tokens) and np.array_equal(tree.position_ids, posid)
+    assert np.array_equal(tree.flat_to_tree, f2t)
     pos, lab, fp = opairs.pairs(flat, cu, scored)
     assert np.array_equal(tree.pair_pos, pos) and np.array_equal(tree.pair_label, lab)
     assert np.array_equal(tree.flat_pair, fp)
