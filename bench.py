@@ -166,6 +166,50 @@ def pairs_bench(workload: str, steps: int, warmup: int) -> dict:
                                        f"{_cpu_model()}"}}
 
 
+def quantise_bench(workload: str, steps: int, warmup: int) -> dict:
+    """The per-row e4m3 weight quantiser (octo_quantise_fp8_rows) on the workload's [V, d] bf16 weight: HIP events
+    over `steps` calls, HBM roofline on its algorithmic bytes (weight read once, codes and scales written); the
+    torch CPU quantisation of 64 rows timed beside it, scaled to V rows."""
+    from octopus_amd import head_op
+    from octopus_amd.workloads import CONFIGS, quantise_fp8_rows as torch_quantise
+    cfg = CONFIGS[workload]
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(1)
+    W = (torch.randn(cfg.V, cfg.d, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    for _ in range(warmup):
+        head_op.quantise_fp8_rows(W)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        q, scale = head_op.quantise_fp8_rows(W)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    alg = cfg.V * cfg.d * (2 + 1) + cfg.V * 4
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    sample = W[:4096].cpu()
+    reps, t0 = 0, time.perf_counter()
+    while reps < 3 or time.perf_counter() - t0 < 2.0:
+        torch_quantise(sample)
+        reps += 1
+    host_s = (time.perf_counter() - t0) / reps * cfg.V / sample.shape[0]
+    return {"metric": "fp8 e4m3 per-row weight quantisation", "value": cfg.V / (ms / 1e3), "unit": "rows/s",
+            "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": ms, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16 -> e4m3",
+            "data": "synthetic (seeded W ~ N(0, 0.02))",
+            "config": {"workload": f"{workload} weight [{cfg.V}, {cfg.d}] bf16 -> e4m3 + row scales"},
+            "roofline": {"kernel": "quantise_fp8_kernel", "bound": "hbm", "achieved": alg / (ms / 1e3) / 1e9,
+                         "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": alg / (ms / 1e3) / PEAK_HBM,
+                         "traffic": None,
+                         "per_launch": f"{alg} algorithmic bytes (2 B read + 1 B written per weight, 4 B per row "
+                                       f"scale)"},
+            "cpu_baseline": {"value": cfg.V / host_s, "unit": "rows/s", "cores": threads, "kind": "port",
+                             "sample": f"torch CPU quantisation (workloads.quantise_fp8_rows) of 4096 rows, "
+                                       f"{reps} runs, scaled to {cfg.V} rows; host: {_cpu_model()}"}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -179,6 +223,9 @@ def main() -> int:
     ap.add_argument("--pairs", action="store_true",
                     help="only time the device label-pair section of the prefix tree (octo_label_pairs) at the "
                          "workload's tree against the host numpy restatement; then exit")
+    ap.add_argument("--quantise", action="store_true",
+                    help="only time the per-row fp8 weight quantiser (octo_quantise_fp8_rows) on the workload's "
+                         "weight; then exit")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB three times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against known bytes), then exit")
@@ -194,6 +241,9 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_each_way": src.numel() * 4}), flush=True)
+        return 0
+    if args.quantise:
+        print(json.dumps(quantise_bench(args.workload, args.steps, args.warmup)), flush=True)
         return 0
     if args.pairs:
         print(json.dumps(pairs_bench(args.workload, args.steps, args.warmup)), flush=True)

@@ -165,6 +165,15 @@ int octo_rows_scatter(const void *src, int64_t ld_src, int src_dtype, const int6
 int octo_gather_f32(const float *src, int64_t ld_src, const int64_t *idx, const int32_t *count,
                     int64_t n_max, float *out, void *stream);
 
+/* Per-row e4m3 quantisation of a weight matrix w [V, ldw] (BF16, F16 or F32) into the fp8 weight format that
+ * octo_head_fwd / octo_head_bwd take (FP8E4M3 with w_scale):
+ *   scale[v] = max(max_k |w[v, k]| / 448, 1e-12)                               (fp32; 448 = largest e4m3)
+ *   q[v * ldq + k] = e4m3(clamp(w[v, k] / scale[v], -448, 448))               (nearest, ties to even)
+ * for k < d; d % 4 == 0, rows and q aligned to 4 elements. The reference has no quantiser: this produces the
+ * weight format of its fp8-weight configuration (per-row scale = absmax / 448) on the device. */
+int octo_quantise_fp8_rows(const void *w, int64_t ldw, int w_dtype, int64_t V, int d,
+                           uint8_t *q, int64_t ldq, float *scale, void *stream);
+
 /* GRPO/PPO policy-gradient weight per token (AReaL grpo_loss_fn semantics):
  *   ratio r = exp(logp - prox)          (prox == NULL: prox = logp, i.e. reuse_train_logp)
  *   behaviour weight w = exp(prox - old) when old != NULL (decoupled loss), else 1;

@@ -6,6 +6,7 @@
 //   columns fwd/bwd  _head_columns over materialised logits
 //   pairs expand/grad, rows scatter, gather   the index plumbing of tree_head_output / _scored_rows
 //   grpo           the per-token policy-gradient weight g = dL/dlogp of the GRPO objective
+//   quantise_fp8   per-row e4m3 quantisation of a weight matrix (the fp8 weight format of the head)
 #include "octo_internal.h"
 
 namespace octo {
@@ -319,6 +320,55 @@ __global__ __launch_bounds__(256) void grpo_grad_kernel(const float *logp, const
   }
 }
 
+// ---- fp8 weight quantiser ---------------------------------------------------------------------------
+// One workgroup per row: the row's absmax in fp32, scale = max(absmax / 448, 1e-12), then every element divided by
+// the scale (IEEE fp32 division), clamped to +-448 and rounded to OCP e4m3, nearest even (v_cvt_pk_fp8_f32).
+// Four elements per thread and step (8 or 16 bytes loaded, 4 bytes stored); the second sweep re-reads the row
+// from cache.
+template <int DT>
+__device__ __forceinline__ f32x4 load4(const char *row, int k) {
+  f32x4 x;
+  if constexpr (DT == OCTO_F32) {
+    x = *(const f32x4 *)(row + 4 * k);
+  } else {
+    typedef typename Elem<DT>::T T;
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    const T4 v = *(const T4 *)(row + 2 * k);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (float)v[i];
+  }
+  return x;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void quantise_fp8_kernel(const char *w, int64_t ld_bytes, int d, uint8_t *q,
+                                                           int64_t ldq, float *scale) {
+  __shared__ float red[4];
+  const int64_t v = blockIdx.x;
+  const char *row = w + v * ld_bytes;
+  float m = 0.f;
+  for (int k = 4 * threadIdx.x; k < d; k += 1024) {
+    const f32x4 x = load4<DT>(row, k);
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3]))));
+  }
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = fmaxf(m / 448.f, 1e-12f);
+  uint8_t *qrow = q + v * ldq;
+  for (int k = 4 * threadIdx.x; k < d; k += 1024) {
+    const f32x4 x = load4<DT>(row, k);
+    float y[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(x[i] / s, -448.f), 448.f);
+    int packed = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    packed = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], packed, true);
+    *(int *)(qrow + k) = packed;
+  }
+  if (threadIdx.x == 0) scale[v] = s;
+}
+
 }  // namespace octo
 
 using namespace octo;
@@ -411,6 +461,29 @@ int octo_gather_f32(const float *src, int64_t ld_src, const int64_t *idx, const 
   hipLaunchKernelGGL(gather_f32_kernel, dim3((unsigned)cdiv(n_max, 256)), dim3(256), 0, (hipStream_t)stream, src,
                      ld_src, idx, count, n_max, out);
   OCTO_CHECK_LAUNCH("gather_f32");
+  return OCTO_OK;
+}
+
+int octo_quantise_fp8_rows(const void *w, int64_t ldw, int w_dtype, int64_t V, int d, uint8_t *q, int64_t ldq,
+                           float *scale, void *stream) {
+  OCTO_CHECK_ARG(w_dtype == OCTO_BF16 || w_dtype == OCTO_F16 || w_dtype == OCTO_F32, "quantise_fp8: dtype %d",
+                 w_dtype);
+  OCTO_CHECK_ARG(V >= 0 && V <= 0x7fffffff && d >= 0 && d % 4 == 0 && ldw >= d && ldq >= d,
+                 "quantise_fp8: bad shape V=%lld d=%d (d must be a multiple of 4)", (long long)V, d);
+  if (V == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(w && q && scale, "quantise_fp8: null pointer");
+  const int esz = w_dtype == OCTO_F32 ? 4 : 2;
+  OCTO_CHECK_ARG((ldw * esz) % (4 * esz) == 0 && ((uintptr_t)w) % (4 * esz) == 0 && ldq % 4 == 0 &&
+                     ((uintptr_t)q) % 4 == 0, "quantise_fp8: rows must be aligned to 4 elements");
+  const dim3 grid((unsigned)V);
+  hipStream_t st = (hipStream_t)stream;
+  const char *wc = (const char *)w;
+  switch (w_dtype) {
+    case OCTO_BF16: hipLaunchKernelGGL(quantise_fp8_kernel<OCTO_BF16>, grid, dim3(256), 0, st, wc, ldw * 2, d, q, ldq, scale); break;
+    case OCTO_F16: hipLaunchKernelGGL(quantise_fp8_kernel<OCTO_F16>, grid, dim3(256), 0, st, wc, ldw * 2, d, q, ldq, scale); break;
+    default: hipLaunchKernelGGL(quantise_fp8_kernel<OCTO_F32>, grid, dim3(256), 0, st, wc, ldw * 4, d, q, ldq, scale); break;
+  }
+  OCTO_CHECK_LAUNCH("quantise_fp8");
   return OCTO_OK;
 }
 

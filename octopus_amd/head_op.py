@@ -320,6 +320,17 @@ def label_pairs(flat: Tensor, cu: Tensor, flat_to_tree: Tensor, T_tree: int, sco
     return pair_pos, pair_label, flat_pair, count
 
 
+def quantise_fp8_rows(weight: Tensor) -> tuple[Tensor, Tensor]:
+    """(q [V, d] torch.float8_e4m3fn, scale [V] fp32) of a [V, d] bf16 / f16 / fp32 weight: the head's fp8 weight
+    format, scale = max(row absmax / 448, 1e-12), q = the quotient weight / scale rounded to e4m3 (nearest even)."""
+    w = weight.contiguous()
+    V, d = w.shape
+    q = torch.empty(V, d, dtype=torch.float8_e4m3fn, device=w.device)
+    scale = torch.empty(V, dtype=torch.float32, device=w.device)
+    _lib.call("octo_quantise_fp8_rows", _p(w), w.stride(0), _dtype_code(w), V, d, _p(q), d, _p(scale), _stream(w))
+    return q, scale
+
+
 def compact_rows(mask: Tensor) -> tuple[Tensor, Tensor]:
     """(idx [n] int64, count [1] int32): idx[:count] = positions of the true entries, ascending, as
     mask.nonzero()[:, 0]; count stays on the device (no host synchronisation)."""

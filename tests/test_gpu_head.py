@@ -286,3 +286,46 @@ def test_cfg1_matches_the_golden_fixture():
     out = fused_head(b.hidden.to(DEV), b.weight.to(DEV), b.labels.to(DEV), 1.0).cpu().double()
     assert (out[:, 0] - torch.from_numpy(z["logp"])).abs().max() <= 1e-5
     assert (out[:, 1] - torch.from_numpy(z["ent"])).abs().max() <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=["bf16", "f16", "f32"])
+def test_fp8_row_quantiser_is_bit_exact(dtype):
+    """octo_quantise_fp8_rows against the oracle (integer restatement of e4m3 rounding) and torch's float8
+    conversion: the same codes and scales, bit for bit; rows of zeros, ties and half-subnormals included."""
+    from octopus_amd.workloads import quantise_fp8_rows as torch_quantise
+    from oracle import fp8 as ofp8
+    g = torch.Generator().manual_seed(1)
+    W = torch.randn(777, 2560, generator=g) * 0.02
+    W[3] = 0.0
+    W[5, :6] = torch.tensor([448.0, 1.0625, -1.1875, 2.0 ** -10, 3 * 2.0 ** -10, -(2.0 ** -11)])
+    W = W.to(dtype)
+    q, scale = head_op.quantise_fp8_rows(W.to(DEV))
+    oq, oscale = ofp8.quantise_rows(W.float().numpy())
+    assert np.array_equal(scale.cpu().numpy(), oscale)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq)
+    tq, ts = torch_quantise(W)  # torch on the CPU: IEEE fp32 division, e4m3 round to nearest even
+    assert torch.equal(q.view(torch.uint8).cpu(), tq.view(torch.uint8)) and torch.equal(scale.cpu(), ts)
+
+
+def test_fp8_row_quantiser_at_full_size_feeds_the_head():
+    """The full [151,936, 2560] weight quantised on the device equals torch's CPU quantisation bit for bit, and
+    the head on it equals the head on the CPU-quantised weight bitwise."""
+    from octopus_amd.workloads import quantise_fp8_rows as torch_quantise
+    V, d = 151936, 2560
+    g = torch.Generator(device=DEV).manual_seed(1)
+    W = (torch.randn(V, d, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+    q, scale = head_op.quantise_fp8_rows(W)
+    Wc = W.cpu()
+    tq = torch.empty(V, d, dtype=torch.uint8)
+    ts = torch.empty(V)
+    for r0 in range(0, V, 16384):
+        a, b = torch_quantise(Wc[r0:r0 + 16384])
+        tq[r0:r0 + 16384], ts[r0:r0 + 16384] = a.view(torch.uint8), b
+    assert torch.equal(q.view(torch.uint8).cpu(), tq) and torch.equal(scale.cpu(), ts)
+    tq, ts = tq.to(DEV).view(torch.float8_e4m3fn), ts.to(DEV)
+    h = torch.randn(300, d, device=DEV, generator=g)
+    h = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    y = torch.randint(0, V, (300,), device=DEV, generator=g)
+    a = fused_head(h, q, y, 1.0, w_scale=scale)
+    b = fused_head(h, tq, y, 1.0, w_scale=ts)
+    assert torch.equal(a, b)

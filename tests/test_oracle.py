@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import fp8 as ofp8
 from oracle import grpo as ogrpo
 from oracle import head as ohead
 from oracle import pairs as opairs
@@ -265,3 +266,37 @@ def test_baseline_matches_the_oracle():
     assert torch.allclose(out[:, 0].double(), lp, atol=1e-5) and torch.allclose(out[:, 1].double(), ent, atol=1e-5)
     assert ((gh.double() - oh).norm() / oh.norm()).item() < 1e-5
     assert ((gw.double() - ow).norm() / ow.norm()).item() < 1e-5
+
+
+def test_e4m3_rounding_matches_torch_float8():
+    """oracle.fp8 against torch's float8_e4m3fn conversion: every finite code, the midpoints between neighbouring
+    codes (ties to even) and their fp32 neighbours, and a strided sweep of all fp32 bit patterns up to 448."""
+    codes = np.arange(256, dtype=np.uint8)
+    vals = ofp8.e4m3_value(codes)
+    assert np.array_equal(np.nan_to_num(vals[:127], nan=1e9),
+                          np.nan_to_num(torch.from_numpy(codes[:127]).view(torch.float8_e4m3fn).double().numpy(),
+                                        nan=1e9))
+    mag = np.unique(np.abs(vals[np.isfinite(vals)]))
+    mids = (mag[:-1] + mag[1:]) / 2
+    x = np.concatenate([vals[np.isfinite(vals)], mids, -mids]).astype(np.float32)
+    x = np.concatenate([x, np.nextafter(x, np.float32(np.inf)), np.nextafter(x, np.float32(-np.inf))])
+    sweep = np.arange(0, np.float32(448).view(np.uint32) + 1, 997, dtype=np.uint32).view(np.float32)
+    x = np.concatenate([x, sweep, -sweep])
+    x = x[np.abs(x) <= 448]
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ofp8.e4m3_bits(x), want)
+
+
+def test_fp8_row_quantiser_matches_torch():
+    from octopus_amd.workloads import quantise_fp8_rows
+    g = torch.Generator().manual_seed(0)
+    W = torch.randn(64, 96, generator=g) * 0.02
+    W[3] = 0.0
+    W[5, :4] = torch.tensor([448.0, 1.0625, -1.1875, 2.0 ** -10])  # scale 1: ties and a half-subnormal
+    for dt in (torch.float32, torch.bfloat16, torch.float16):
+        q, scale = ofp8.quantise_rows(W.to(dt).float().numpy())
+        tq, ts = quantise_fp8_rows(W.to(dt))
+        assert np.array_equal(scale, ts.numpy()) and np.array_equal(q, tq.view(torch.uint8).numpy())
+        # the dequantised weight is within half an e4m3 step of the row-scaled weight
+        deq = ofp8.e4m3_value(q) * scale[:, None]
+        assert np.all(np.abs(deq - W.to(dt).double().numpy()) <= scale[:, None] * 16 * (1 + 1e-6) + 1e-30)
