@@ -200,7 +200,7 @@ def quantise_bench(workload: str, steps: int, warmup: int) -> dict:
             "scaling": "weak", "vs_baseline": None, "dtype": "bf16 -> e4m3",
             "data": "synthetic (seeded W ~ N(0, 0.02))",
             "config": {"workload": f"{workload} weight [{cfg.V}, {cfg.d}] bf16 -> e4m3 + row scales"},
-            "roofline": {"kernel": "quantise_fp8_kernel", "bound": "hbm", "achieved": alg / (ms / 1e3) / 1e9,
+            "roofline": {"kernel": "quantise_fp8_rows_kernel", "bound": "hbm", "achieved": alg / (ms / 1e3) / 1e9,
                          "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": alg / (ms / 1e3) / PEAK_HBM,
                          "traffic": None,
                          "per_launch": f"{alg} algorithmic bytes (2 B read + 1 B written per weight, 4 B per row "

@@ -321,10 +321,10 @@ __global__ __launch_bounds__(256) void grpo_grad_kernel(const float *logp, const
 }
 
 // ---- fp8 weight quantiser ---------------------------------------------------------------------------
-// One workgroup per row: the row's absmax in fp32, scale = max(absmax / 448, 1e-12), then every element divided by
-// the scale (IEEE fp32 division), clamped to +-448 and rounded to OCP e4m3, nearest even (v_cvt_pk_fp8_f32).
-// Four elements per thread and step (8 or 16 bytes loaded, 4 bytes stored); the second sweep re-reads the row
-// from cache.
+// Per row: the absmax in fp32, scale = max(absmax / 448, 1e-12), then every element divided by the scale (IEEE
+// fp32 division), clamped to +-448 and rounded to OCP e4m3, nearest even (v_cvt_pk_fp8_f32).
+// General form (any d % 4 == 0): one workgroup per row, four elements per thread and step (8 or 16 bytes loaded,
+// 4 bytes stored); the second sweep re-reads the row from cache.
 template <int DT>
 __device__ __forceinline__ f32x4 load4(const char *row, int k) {
   f32x4 x;
@@ -367,6 +367,53 @@ __global__ __launch_bounds__(256) void quantise_fp8_kernel(const char *w, int64_
     *(int *)(qrow + k) = packed;
   }
   if (threadIdx.x == 0) scale[v] = s;
+}
+
+// One wave per row, the row held in registers (d <= 4096, d % 8 == 0): lane l takes elements 512 c + 8 l .. + 8 of
+// chunk c (16-byte loads of bf16 / f16, 2 x 16 for fp32), the absmax is a wave reduction, and the codes go out as
+// 8 bytes per lane and chunk. Four rows per workgroup.
+constexpr int QF8_MAXC = 8;
+template <int DT>
+__global__ __launch_bounds__(256) void quantise_fp8_rows_kernel(const char *w, int64_t ld_bytes, int64_t V, int d,
+                                                                uint8_t *q, int64_t ldq, float *scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v >= V) return;
+  const char *row = w + v * ld_bytes;
+  float x[QF8_MAXC][8];
+  float m = 0.f;
+#pragma unroll
+  for (int c = 0; c < QF8_MAXC; ++c) {
+    const int k = c * 512 + lane * 8;
+    if (k < d) {
+      const f32x4 a = load4<DT>(row, k), b = load4<DT>(row, k + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[c][i] = a[i];
+        x[c][4 + i] = b[i];
+        m = fmaxf(m, fmaxf(fabsf(a[i]), fabsf(b[i])));
+      }
+    }
+  }
+  m = wave_max(m);
+  const float s = fmaxf(m / 448.f, 1e-12f);
+  uint8_t *qrow = q + v * ldq;
+#pragma unroll
+  for (int c = 0; c < QF8_MAXC; ++c) {
+    const int k = c * 512 + lane * 8;
+    if (k < d) {
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(x[c][i] / s, -448.f), 448.f);
+      i32x2 o;
+      o[0] = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+      o[0] = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], o[0], true);
+      o[1] = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+      o[1] = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], o[1], true);
+      *(i32x2 *)(qrow + k) = o;
+    }
+  }
+  if (lane == 0) scale[v] = s;
 }
 
 }  // namespace octo
@@ -475,9 +522,20 @@ int octo_quantise_fp8_rows(const void *w, int64_t ldw, int w_dtype, int64_t V, i
   const int esz = w_dtype == OCTO_F32 ? 4 : 2;
   OCTO_CHECK_ARG((ldw * esz) % (4 * esz) == 0 && ((uintptr_t)w) % (4 * esz) == 0 && ldq % 4 == 0 &&
                      ((uintptr_t)q) % 4 == 0, "quantise_fp8: rows must be aligned to 4 elements");
-  const dim3 grid((unsigned)V);
   hipStream_t st = (hipStream_t)stream;
   const char *wc = (const char *)w;
+  if (d % 8 == 0 && d <= QF8_MAXC * 512 && ldq % 8 == 0 && ((uintptr_t)q) % 8 == 0 && ldw % 8 == 0 &&
+      ((uintptr_t)w) % 16 == 0) {  // one wave per row, the row in registers
+    const dim3 g4((unsigned)cdiv(V, 4));
+    switch (w_dtype) {
+      case OCTO_BF16: hipLaunchKernelGGL(quantise_fp8_rows_kernel<OCTO_BF16>, g4, dim3(256), 0, st, wc, ldw * 2, V, d, q, ldq, scale); break;
+      case OCTO_F16: hipLaunchKernelGGL(quantise_fp8_rows_kernel<OCTO_F16>, g4, dim3(256), 0, st, wc, ldw * 2, V, d, q, ldq, scale); break;
+      default: hipLaunchKernelGGL(quantise_fp8_rows_kernel<OCTO_F32>, g4, dim3(256), 0, st, wc, ldw * 4, V, d, q, ldq, scale); break;
+    }
+    OCTO_CHECK_LAUNCH("quantise_fp8");
+    return OCTO_OK;
+  }
+  const dim3 grid((unsigned)V);
   switch (w_dtype) {
     case OCTO_BF16: hipLaunchKernelGGL(quantise_fp8_kernel<OCTO_BF16>, grid, dim3(256), 0, st, wc, ldw * 2, d, q, ldq, scale); break;
     case OCTO_F16: hipLaunchKernelGGL(quantise_fp8_kernel<OCTO_F16>, grid, dim3(256), 0, st, wc, ldw * 2, d, q, ldq, scale); break;

@@ -295,16 +295,19 @@ def test_fp8_row_quantiser_is_bit_exact(dtype):
     from octopus_amd.workloads import quantise_fp8_rows as torch_quantise
     from oracle import fp8 as ofp8
     g = torch.Generator().manual_seed(1)
-    W = torch.randn(777, 2560, generator=g) * 0.02
-    W[3] = 0.0
-    W[5, :6] = torch.tensor([448.0, 1.0625, -1.1875, 2.0 ** -10, 3 * 2.0 ** -10, -(2.0 ** -11)])
-    W = W.to(dtype)
-    q, scale = head_op.quantise_fp8_rows(W.to(DEV))
-    oq, oscale = ofp8.quantise_rows(W.float().numpy())
-    assert np.array_equal(scale.cpu().numpy(), oscale)
-    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq)
-    tq, ts = torch_quantise(W)  # torch on the CPU: IEEE fp32 division, e4m3 round to nearest even
-    assert torch.equal(q.view(torch.uint8).cpu(), tq.view(torch.uint8)) and torch.equal(scale.cpu(), ts)
+    # d 2560: one wave per row, the row in registers; d 4100 (above 4096) and 36 (not a multiple of 8): the
+    # workgroup-per-row form
+    for V, d in ((777, 2560), (33, 4100), (50, 36)):
+        W = torch.randn(V, d, generator=g) * 0.02
+        W[3] = 0.0
+        W[5, :6] = torch.tensor([448.0, 1.0625, -1.1875, 2.0 ** -10, 3 * 2.0 ** -10, -(2.0 ** -11)])
+        W = W.to(dtype)
+        q, scale = head_op.quantise_fp8_rows(W.to(DEV))
+        oq, oscale = ofp8.quantise_rows(W.float().numpy())
+        assert np.array_equal(scale.cpu().numpy(), oscale), (V, d)
+        assert np.array_equal(q.view(torch.uint8).cpu().numpy(), oq), (V, d)
+        tq, ts = torch_quantise(W)  # torch on the CPU: IEEE fp32 division, e4m3 round to nearest even
+        assert torch.equal(q.view(torch.uint8).cpu(), tq.view(torch.uint8)) and torch.equal(scale.cpu(), ts)
 
 
 def test_fp8_row_quantiser_at_full_size_feeds_the_head():
