@@ -103,9 +103,9 @@ __device__ __forceinline__ const char *uniform_ptr(const char *p) {
   return (const char *)(((uint64_t)hi << 32) | lo);
 }
 
-// ---- direct-to-LDS mainloop -----------------------------------------------------------------------
+// ---- 4-stage mainloop (fp32 operands, fp8 weights) --------------------------------------------------
 //
-// K advances 64 bytes of the staged type per stage (32 bf16 / f16, 16 fp32). Each operand's stage slice (16 KB)
+// K advances 64 bytes of the staged type per stage (32 bf16, 16 fp32). Each operand's stage slice (16 KB)
 // is written straight into LDS by buffer_load_dwordx4 ... lds: a wave instruction moves 1 KB, lane i's 16 bytes
 // landing at the instruction's LDS base + 16 i, so the LDS layout is chosen by which global chunk each lane
 // fetches. DNSTAGE stages form a ring (A slice, then B slice, per stage). One bare s_barrier per stage (no
@@ -117,15 +117,6 @@ __device__ __forceinline__ const char *uniform_ptr(const char *p) {
 //     physical chunk c ^ ((r >> 2) & 3), so a 16-lane pass of fragment reads (rows r0..r0+15 of one logical
 //     chunk) covers all 64 banks once. A fragment is one ds_read_b128: lane l holds row l & 31 of a 32-row
 //     block, K chunk 2 sub + (l >> 5).
-//   OpCols (MN-contiguous, 16-bit types): a slice is 32 K-rows x 512 bytes (256 columns). Chunk c of K-row r
-//     sits at physical chunk c ^ 4 (r & 3). A fragment is two ds_read_b64_tr_b16 (gfx950 transposing reads):
-//     within each 16-lane group, output lane i, element e comes from source lane 4 e + (i >> 2), element i & 3;
-//     so source lane s of group g reads K-row 16 sub + 8 (g >> 1) + (s >> 2) (+ 4 for the upper half) at
-//     columns 16 (g & 1) + 4 (s & 3) .. + 4 of the block, and lane l receives column l & 31 at the 8 K values
-//     16 sub + 8 (l >> 5) + 0..7, the MFMA operand layout. The 64 lanes of one read cover 8 K-rows x 64 bytes,
-//     which the XOR spreads over all 64 banks exactly twice.
-//     The buffer descriptor is rebuilt per stage at the stage's first K-row, so operands larger than 4 GB stay
-//     within 32-bit offsets; K-rows at or past `krows` read zero.
 //   OpRowsF8 (K-contiguous e4m3 rows): a slice is 256 rows x 32 bytes (the same 32 K values per stage). Chunk c
 //     (0, 1) of row r sits at physical chunk c ^ ((r >> 3) & 1), so 16 lanes reading one logical chunk of 16
 //     consecutive rows cover all 64 banks once. One ds_read_b128 per block and stage serves both sub-steps:
@@ -240,70 +231,6 @@ struct OpRowsF8 {
       o[2 * h + 1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[2 * s + h], 1.0f, true));
     }
     return o;
-  }
-};
-
-// MN-contiguous 16-bit operand: instruction q of wave w fills K-rows (4 q + w) * 2 and + 1 of the slice (lanes
-// 0..31, 32..63), lane i taking physical chunk i & 31.
-struct OpCols {
-  static constexpr int NI = DIPW;
-  static constexpr bool FP8 = false;
-  const char *base;  // the tile's first column in K-row 0
-  int64_t ld;        // bytes per K-row
-  int64_t bytes;     // bytes addressable from base (the operand's rows x ld, less the column offset)
-  uint32_t krows;    // K-rows that exist
-  uint32_t roff[DIPW];
-  int rowq[DIPW];
-  int fa[4];         // fragment byte offsets of blocks 0..3 (sub-step 0, lower half)
-
-  __device__ __forceinline__ void init(const Operand &op, int64_t col0, int wsub, uint32_t krows_) {
-    const int w = threadIdx.x >> 6, i = threadIdx.x & 63, l = i;
-    base = op.base + col0 * 2;
-    ld = op.ld;
-    bytes = op.rows * op.ld - col0 * 2;
-    krows = (int64_t)krows_ < op.rows ? krows_ : (uint32_t)op.rows;
-#pragma unroll
-    for (int q = 0; q < DIPW; ++q) {
-      const int r = (4 * q + w) * 2 + (i >> 5);
-      rowq[q] = r;
-      roff[q] = (uint32_t)(r * ld) + (uint32_t)((((i & 31) ^ (4 * (r & 3)))) << 4);
-    }
-    const int g = l >> 4, s = l & 15;
-    const int krow = 8 * (g >> 1) + (s >> 2);  // + 16 sub, + 4 for the upper half (r & 3 unchanged)
-    const int j = 2 * (g & 1) + ((s & 3) >> 1);
-    const int intra = (s & 1) * 8;
-#pragma unroll
-    for (int blk = 0; blk < 4; ++blk)
-      fa[blk] = krow * 512 + (16 * wsub + 4 * (blk ^ (s >> 2)) + j) * 16 + intra;
-  }
-  // K-rows at or past krows read zero; so do columns past the operand's last byte (an edge tile's columns past
-  // the row end read the next row, whose products land in discarded output columns)
-  __device__ __forceinline__ void dma(int k, int q, uint32_t /*kbytes*/, lds_char *slice) const {
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t skip = (int64_t)k * 32 * ld;
-    const int64_t left = bytes - skip;
-    // every term is wave-uniform; readfirstlane says so, or the compiler wraps the load in a waterfall loop
-    const uint32_t ext = __builtin_amdgcn_readfirstlane(
-        left <= 0 ? 0u : (left < 32 * ld ? (uint32_t)left : (uint32_t)(32 * ld)));
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(uniform_ptr(base + (left > 0 ? skip : 0)), ext);
-    const uint32_t row = (uint32_t)k * 32 + (uint32_t)rowq[q];
-    lds_dma16(rs, row < krows ? roff[q] : 0x80000000u, slice + (4 * q + w) * 1024);
-  }
-  // Issued as inline asm: the compiler cannot tell the transposing read from a read of the LDS that the
-  // in-flight DMA is writing, and would drain every outstanding DMA (vmcnt(0)) before it. Stage data is
-  // ordered by the mainloop's own vmcnt waits and barriers, and the mainloop waits lgkmcnt(0) at the start
-  // of each sub-step, before the first MFMA that can consume a fragment read under the previous one.
-  __device__ __forceinline__ i32x4 frag(const lds_char *slice, int sub, int blk) const {
-    const uint32_t p = (uint32_t)(uintptr_t)(slice + fa[blk] + sub * 16 * 512);
-    i32x2 lo, hi;
-    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(lo) : "v"(p));
-    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:2048" : "=v"(hi) : "v"(p));
-    i32x4 r;
-    r[0] = lo[0];
-    r[1] = lo[1];
-    r[2] = hi[0];
-    r[3] = hi[1];
-    return r;
   }
 };
 
@@ -427,6 +354,189 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
     prev_slot = slot;
     slot = next_slot;
   }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
+  __builtin_amdgcn_s_barrier();
+}
+
+// ---- full-line mainloop: K = 64 per stage, a 5-slot ring ------------------------------------------
+//
+// For 16-bit types. A stage holds K = 64 (128 bytes of every operand row), so each row fetch of a K-contiguous
+// operand is one whole 128-byte cache line; with 64-byte rows (the 4-stage ring above) every line is requested
+// twice, once per half, which doubles the L1 -> L2 requests and stalls the address unit on the L1.
+//
+// A stage is two 32 KB slices (A, B). The LDS holds five slices, 2.5 stages: stage j's A slice sits in slot
+// 2 j mod 5, its B slice in slot 2 j + 1 mod 5. One s_barrier per stage, B_k, placed before the last of stage
+// k's four sub-steps, means "every wave has read stage k" (its last fragments are read under sub-step 2) and
+// "stage k + 1 has landed in every wave". It frees stage k's two slots; stage k + 2's B slice goes into the
+// first (issued under sub-step 3), and stage k + 3's A slice into the second (issued under sub-steps 0 and 1 of
+// stage k + 1, i.e. under the iteration that issues all of stage k + 3... see the loop). So iteration k issues
+// stage k + 2 whole: its A slice under sub-steps 0 and 1 (slot freed at B_(k-1)), its B slice under sub-step 3
+// (slot freed at B_k). At B_k only stage k + 2's A slice may still be in flight: vmcnt(8).
+//
+//   OpRows128 (K-contiguous rows): a slice is 256 rows x 128 bytes. Chunk c (0..7) of row r sits at physical
+//     chunk c ^ ((r >> 1) & 7), so a 16-lane pass of fragment reads (rows r0..r0+15, r0 a multiple of 16, of
+//     one logical chunk) covers all 64 banks once. DMA instruction q of wave w fills slice rows (4 q + w) * 8 ..
+//     + 8; lane i takes row + (i >> 3) and physical chunk i & 7, so the 8 lanes of a row fetch its 128 bytes.
+//     A fragment is one ds_read_b128: lane l holds row l & 31 of a 32-row block, K chunk 2 sub + (l >> 5).
+constexpr int EKB = 128;              // K bytes per stage and row
+constexpr int ESLICE = 256 * EKB;     // one operand's stage slice (32 KB)
+constexpr int ENSLOT = 5;             // ring slots
+constexpr int ENI = 8;                // DMA instructions per wave, operand and stage
+constexpr int SMEM_RING5 = ENSLOT * ESLICE;
+static_assert(SMEM_RING5 <= 160 * 1024, "LDS budget");
+
+struct OpRows128 {
+  static constexpr int NI = ENI;
+  static constexpr bool FP8 = false;
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t off[ENI];
+  uint32_t coff;
+  int fo[4];  // fragment byte offsets of sub-steps 0..3 (block 0)
+
+  __device__ __forceinline__ void init(const Operand &op, int64_t row0, int wsub, uint32_t /*krows*/) {
+    const int w = threadIdx.x >> 6, i = threadIdx.x & 63, lane = i;
+    const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
+    // row (4 q + w) * 8 + (i >> 3): its swizzle ((row >> 1) & 7) = (4 (w & 1) + (i >> 4)) & 7 for every q
+    coff = (uint32_t)(((i & 7) ^ ((4 * (w & 1) + (i >> 4)) & 7)) << 4);
+#pragma unroll
+    for (int q = 0; q < ENI; ++q) {
+      const int r = (4 * q + w) * 8 + (i >> 3);
+      uint32_t rowoff;
+      if (r < valid) rowoff = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
+      else rowoff = 0x80000000u;
+      off[q] = rowoff + coff;
+    }
+    if (op.map) rs = make_rsrc(uniform_ptr(op.base), op.extent);
+    else rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
+    const int row = wsub * 128 + (lane & 31);
+    const int hs = (lane >> 5) ^ ((lane >> 1) & 7);  // chunk (2 sub + h) ^ swizzle = (2 sub) ^ (h ^ swizzle)
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) fo[sub] = row * EKB + (((2 * sub) ^ hs) << 4);
+  }
+  // K chunks at or past kbytes (bytes per row) read zero
+  __device__ __forceinline__ void dma(int k, int q, uint32_t kbytes, lds_char *slice) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t kb = (uint32_t)k * EKB;
+    lds_dma16(rs, (kb + coff < kbytes) ? off[q] + kb : 0x80000000u, slice + (4 * q + w) * 1024);
+  }
+  __device__ __forceinline__ i32x4 frag(const lds_char *slice, int sub, int blk) const {
+    return *(const lds_i32x4 *)(slice + fo[sub] + blk * 32 * EKB);
+  }
+};
+
+// The 16-bit GEMMs (bf16 / f16 operands, no fp8 widening) run the ring loop; fp32 and fp8 the 4-stage one.
+__host__ __device__ constexpr bool ring5_ok(int dt, bool fp8) { return (dt == OCTO_BF16 || dt == OCTO_F16) && !fp8; }
+
+// One stage of the ring loop: four sub-steps of 16 MFMAs. DMA: issue stage k + 2 (A under sub-steps 0, 1; B under
+// sub-step 3). NEXT: a stage k + 1 exists (barrier B_k, and its first fragments are read under sub-step 3).
+template <int DT, typename OA, typename OB, bool DMA, bool NEXT>
+__device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int k, int sa, uint32_t kbytes,
+                                            lds_char *smem, i32x4 (&fa)[2][4], i32x4 (&fb)[2][4],
+                                            f32x16 (&acc)[4][4]) {
+  // slots: stage k at (sa, sa + 1), stage k + 1 at (sa + 2, sa + 3), stage k + 2's A at sa + 4, its B at sa
+  auto slot = [&](int d) -> lds_char * { const int x = sa + d; return smem + (x >= ENSLOT ? x - ENSLOT : x) * ESLICE; };
+  const lds_char *cA = slot(0), *cB = slot(1);
+  const lds_char *nA = slot(2), *nB = slot(3);
+  lds_char *dA = slot(4), *dB = slot(0);
+#pragma unroll
+  for (int sub = 0; sub < 4; ++sub) {
+    if (sub == 3 && NEXT) {
+      __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // this wave's reads of stage k are done
+      if (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(ENI));  // stage k + 1 landed (k + 2's A may be in flight)
+      else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      __builtin_amdgcn_s_barrier();  // ... in every wave; stage k's slots are free
+    } else {
+      __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // this sub-step's fragments are in
+    }
+    OCTO_FENCE();
+    const int cur = sub & 1, nxt = cur ^ 1;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      Mfma<DT>::run(fa[cur][q >> 2], fb[cur][q & 3], acc[q >> 2][q & 3]);
+      OCTO_FENCE();
+      if (q < 8) {
+        if (sub < 3) {
+          if (q < 4) fa[nxt][q] = opa.frag(cA, sub + 1, q);
+          else fb[nxt][q - 4] = opb.frag(cB, sub + 1, q - 4);
+          OCTO_FENCE();
+        } else if (NEXT) {
+          if (q < 4) fa[nxt][q] = opa.frag(nA, 0, q);
+          else fb[nxt][q - 4] = opb.frag(nB, 0, q - 4);
+          OCTO_FENCE();
+        }
+      }
+      if (DMA) {
+        if (sub < 2 && q >= 8 && (q & 1)) {  // A slice of stage k + 2: 4 instructions per sub-step
+          opa.dma(k + 2, 4 * sub + ((q - 8) >> 1), kbytes, dA);
+          OCTO_FENCE();
+        }
+        if (sub == 3 && (q & 1)) {  // B slice of stage k + 2
+          opb.dma(k + 2, q >> 1, kbytes, dB);
+          OCTO_FENCE();
+        }
+      }
+    }
+  }
+}
+
+// smem: SMEM_RING5 bytes. 16-bit types only.
+template <int DT, typename OA, typename OB>
+__device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &B, int64_t m0, int64_t n0,
+                                               int64_t K_eff, lds_char *smem, f32x16 (&acc)[4][4]) {
+  static_assert(DT == OCTO_BF16 || DT == OCTO_F16, "16-bit operands");
+  static_assert(OA::NI == ENI && OB::NI == ENI, "8 DMA instructions per wave and slice");
+  const int w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const uint32_t kbytes = (uint32_t)(K_eff * 2);
+  const int nk = (int)((kbytes + EKB - 1) / EKB);
+  if (nk == 0) return;
+
+  OA opa;
+  OB opb;
+  opa.init(A, m0, wm, (uint32_t)K_eff);
+  opb.init(B, n0, wn, (uint32_t)K_eff);
+
+  // prologue: stages 0 and 1 into slots 0..3
+#pragma unroll
+  for (int q = 0; q < ENI; ++q) opa.dma(0, q, kbytes, smem);
+#pragma unroll
+  for (int q = 0; q < ENI; ++q) opb.dma(0, q, kbytes, smem + ESLICE);
+  if (nk > 1) {
+#pragma unroll
+    for (int q = 0; q < ENI; ++q) opa.dma(1, q, kbytes, smem + 2 * ESLICE);
+#pragma unroll
+    for (int q = 0; q < ENI; ++q) opb.dma(1, q, kbytes, smem + 3 * ESLICE);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * ENI));  // stage 0 landed
+  } else {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  }
+  __builtin_amdgcn_s_barrier();
+
+  i32x4 fa[2][4], fb[2][4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    fa[0][b] = opa.frag(smem, 0, b);
+    fb[0][b] = opb.frag(smem + ESLICE, 0, b);
+  }
+  int sa = 0;  // slot of stage k's A slice: 2 k mod 5
+  int k = 0;
+  for (; k + 2 < nk; ++k) {
+    ring5_stage<DT, OA, OB, true, true>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
+    sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
+  }
+  if (k + 1 < nk) {
+    ring5_stage<DT, OA, OB, false, true>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
+    sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
+    ++k;
+  }
+  ring5_stage<DT, OA, OB, false, false>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
   __builtin_amdgcn_s_barrier();
 }

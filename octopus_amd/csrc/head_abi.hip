@@ -93,33 +93,29 @@ FwdLayout fwd_layout(int64_t n_max, int V) {
   return L;
 }
 
-// 16-bit weights and hidden rows take the transposed-read backward: dz is staged once, token-major, and the
-// gradient GEMMs read W, dz and the gathered hidden rows as stored. fp32 and fp8 weights stage W^T, h^T and
-// both dz layouts for K-contiguous operands.
-bool tr_path(int w_dtype) { return w_dtype == OCTO_BF16 || w_dtype == OCTO_F16; }
-
+// The backward stages every gradient GEMM operand K-contiguous, so each row fetch of the GEMM mainloop is one
+// whole cache line: W^T [d, V_pad] for grad_h = dz . W, the pass's hidden rows transposed to h^T [d, P] for
+// grad_W = dz^T . h, and dz in both layouts (token-major for grad_h, vocab-major for grad_W).
 struct BwdLayout {
   int64_t P, V_pad, passes;
   int esz;
-  bool tr;
   size_t wt, ht, dza, dzb, gacc, total;
 };
 BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw) {
   BwdLayout L;
   L.esz = elem_bytes(staged_dtype(w_dtype));
-  L.tr = tr_path(w_dtype);
   L.V_pad = round_up(V, TM);
   L.P = n_max == 0 ? 0 : (round_up(n_max, TN) < kPassRows ? round_up(n_max, TN) : kPassRows);
   L.passes = L.P == 0 ? 0 : cdiv(n_max, L.P);
   size_t off = 0;
-  L.wt = off;  // W^T [d, V_pad] (K-contiguous path, grad_h)
-  if (!L.tr && need_gh) off += align_up((size_t)d * L.V_pad * L.esz);
-  L.ht = off;  // K-contiguous path: h^T [d, P]; transposed path: gathered rows [P, d]
+  L.wt = off;  // W^T [d, V_pad] (grad_h)
+  if (need_gh) off += align_up((size_t)d * L.V_pad * L.esz);
+  L.ht = off;  // h^T [d, P] of the pass's rows (grad_W)
   if (need_gw) off += align_up((size_t)d * L.P * L.esz);
-  L.dza = off;  // dz [P, V_pad], token-major
-  if (need_gh || (L.tr && need_gw)) off += align_up((size_t)L.P * L.V_pad * L.esz);
-  L.dzb = off;  // dz [V_pad, P], vocab-major (K-contiguous path, grad_W)
-  if (!L.tr && need_gw) off += align_up((size_t)L.V_pad * L.P * L.esz);
+  L.dza = off;  // dz [P, V_pad], token-major (grad_h)
+  if (need_gh) off += align_up((size_t)L.P * L.V_pad * L.esz);
+  L.dzb = off;  // dz [V_pad, P], vocab-major (grad_W)
+  if (need_gw) off += align_up((size_t)L.V_pad * L.P * L.esz);
   L.gacc = off;  // fp32 grad_W partial sums across passes, for a 16-bit grad_W
   if (need_gw && L.passes > 1 && w_dtype != OCTO_F32) off += align_up((size_t)V * d * sizeof(float));
   L.total = off;
@@ -384,9 +380,8 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
   const int esz = L.esz;
   const bool gw_staged = need_gw && L.passes > 1 && gw_dtype != OCTO_F32;  // fp32 partials in gacc
 
-  // K-contiguous path: W^T [d, V_pad] in the staged type (fp8 weights: their exact bf16 values; the row scale
-  // is in dz)
-  if (!L.tr && need_gh) {
+  // W^T [d, V_pad] in the staged type (fp8 weights: their exact bf16 values; the row scale is in dz)
+  if (need_gh) {
     rc = launch_transpose(w, ldw, w_dtype, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt, L.V_pad, cm.dt, st);
     if (rc) return rc;
   }
@@ -401,9 +396,9 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm);
     const GemmShape s1 = shape(V, rows, d, kGroupM, 2, count, r0);
     DzArgs e;
-    e.dzA = (need_gh || (L.tr && need_gw)) ? dza : nullptr;
+    e.dzA = need_gh ? dza : nullptr;
     e.ldA = L.V_pad;
-    e.dzB = (!L.tr && need_gw) ? dzb : nullptr;
+    e.dzB = need_gw ? dzb : nullptr;
     e.ldB = L.P;
     e.lse = lse;
     e.g = g;
@@ -423,15 +418,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
 
     if (need_gh) {  // grad_h[rows] = dz . W   (K = V_pad)
       const Operand A2 = plain_operand(dza, L.V_pad * esz, rows, count, r0);
-      Operand B2;
-      int layout;
-      if (L.tr) {  // W [V, d] read as stored: K-rows = vocabulary rows
-        B2 = plain_operand(w, ldw * esz, V, nullptr, 0);
-        layout = 2;
-      } else {
-        B2 = plain_operand(wt, L.V_pad * esz, d, nullptr, 0);
-        layout = 0;
-      }
+      const Operand B2 = plain_operand(wt, L.V_pad * esz, d, nullptr, 0);
       const GemmShape s2 = shape(rows, d, L.V_pad, kGroupM, 1, count, r0);
       StoreArgs o;
       o.C = (char *)grad_h + r0 * ld_gh * elem_bytes(gh_dtype);
@@ -441,29 +428,17 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       o.accumulate = 0;
       {
         TimedLaunch t("gemm_store_grad_h", st);
-        rc = launch_gemm_store(cm.dt, layout, A2, B2, s2, o, st);
+        rc = launch_gemm_store(cm.dt, A2, B2, s2, o, st);
       }
       if (rc) return rc;
     }
     if (need_gw) {  // grad_W += dz^T . h   (K = this pass's rows)
       const int64_t rows_pad = round_up(rows, TN);
-      Operand A3, B3;
-      int layout;
-      if (L.tr) {  // dz [P, V_pad] and the gathered rows [P, d] read as stored: K-rows = the pass's tokens
-        rc = launch_gather_rows(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, cm.hesz, idx ? idx + r0 : nullptr,
-                                count, r0, rows, rows_pad, d, ht, d, st);
-        if (rc) return rc;
-        A3 = plain_operand(dza, L.V_pad * esz, rows_pad, nullptr, 0);
-        B3 = plain_operand(ht, (int64_t)d * esz, rows_pad, nullptr, 0);
-        layout = 3;
-      } else {
-        rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, nullptr,
-                              idx ? idx + r0 : nullptr, count, r0, rows, rows_pad, d, ht, L.P, cm.dt, st);
-        if (rc) return rc;
-        A3 = plain_operand(dzb, L.P * esz, L.V_pad, nullptr, 0);
-        B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
-        layout = 0;
-      }
+      rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, nullptr,
+                            idx ? idx + r0 : nullptr, count, r0, rows, rows_pad, d, ht, L.P, cm.dt, st);
+      if (rc) return rc;
+      const Operand A3 = plain_operand(dzb, L.P * esz, L.V_pad, nullptr, 0);
+      const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
       const GemmShape s3 = shape(V, d, rows, kGroupM, 3, count, r0);
       StoreArgs o;
       const bool acc_out = flags & OCTO_GRADW_ACCUMULATE;
@@ -481,7 +456,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       o.ldc = d;
       {
         TimedLaunch t("gemm_store_grad_w", st);
-        rc = launch_gemm_store(cm.dt, layout, A3, B3, s3, o, st);
+        rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st);
       }
       if (rc) return rc;
     }

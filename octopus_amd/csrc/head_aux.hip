@@ -1,7 +1,6 @@
 // Memory-bound kernels of the LM-head path and their C-ABI entry points:
 //   merge          per-row merge of the vocab-tile softmax partials + target logit -> logp, entropy, lse
-//   gather_rows    the pass's hidden rows gathered into one contiguous block (16-bit backward)
-//   transpose      K-contiguous copies (W^T, gathered h^T) feeding the fp32 / fp8-weight backward GEMMs
+//   transpose      K-contiguous copies (W^T, gathered h^T) feeding the backward's gradient GEMMs
 //   compact_rows   masked-row compaction, ascending (torch.nonzero order), count left on the device
 //   columns fwd/bwd  _head_columns over materialised logits
 //   pairs expand/grad, rows scatter, gather   the index plumbing of tree_head_output / _scored_rows
@@ -102,34 +101,6 @@ int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float
   hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, st, src, ld_src, src_dtype, map, count, count_off, rows,
                      rows_pad, cols, dst, ld_dst, dst_dtype);
   OCTO_CHECK_LAUNCH("transpose");
-  return OCTO_OK;
-}
-
-// ---- row gather --------------------------------------------------------------------------------------
-// One workgroup per destination row, 16-byte chunks; rows at or past the valid count are written as zeros.
-__global__ __launch_bounds__(256) void gather_rows_kernel(const char *src, int64_t ld_src, const int64_t *map,
-                                                          const int32_t *count, int64_t count_off, int64_t rows,
-                                                          int64_t row_bytes, char *dst, int64_t ld_dst) {
-  const int64_t r = blockIdx.x;
-  const bool ok = r < dev_count(count, count_off, rows);
-  const char *s = ok ? src + (map ? map[r] : r) * ld_src : nullptr;
-  char *d = dst + r * ld_dst;
-  for (int64_t c = (int64_t)threadIdx.x * 16; c < row_bytes; c += 256 * 16) {
-    i32x4 v = {0, 0, 0, 0};
-    if (ok) v = *(const i32x4 *)(s + c);
-    *(i32x4 *)(d + c) = v;
-  }
-}
-
-int launch_gather_rows(const void *src, int64_t ld_src, int esz, const int64_t *map, const int32_t *count,
-                       int64_t count_off, int64_t rows, int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst,
-                       hipStream_t st) {
-  if (rows_pad == 0 || cols == 0) return OCTO_OK;
-  if ((cols * esz) % 16 || (ld_src * esz) % 16 || (ld_dst * esz) % 16)
-    return octo_fail(OCTO_EINVAL, "gather_rows: rows must be whole 16-byte chunks");
-  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)rows_pad), dim3(256), 0, st, (const char *)src, ld_src * esz,
-                     map, count, count_off, rows, cols * esz, (char *)dst, ld_dst * esz);
-  OCTO_CHECK_LAUNCH("gather_rows");
   return OCTO_OK;
 }
 

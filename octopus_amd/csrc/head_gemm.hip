@@ -5,9 +5,8 @@
 //   gemm_dz    : the same tile recomputed -> dz = g (onehot - p) / T * post'(z), written as bf16 in
 //                the row-major [tokens, V] layout and/or the vocab-major [V, tokens] layout
 //                (backward recompute, lm_head.py:118-121 under checkpoint)
-//   gemm_store : plain C = A . B^T with fp32/bf16/f16 output, optionally accumulated, with either operand
-//                K-contiguous or MN-contiguous (grad_h = dz . W reads W as stored; grad_W = dz^T . h reads dz
-//                and the gathered hidden rows as stored)
+//   gemm_store : plain C = A . B^T with fp32/bf16/f16 output, optionally accumulated: grad_h = dz . W from a
+//                staged W^T, grad_W = dz^T . h from vocab-major dz and a staged h^T (both operands K-contiguous)
 //
 // Orientation: the first operand (MFMA "A", tile rows) of gemm_stats / gemm_dz is the vocabulary,
 // the second (tile columns) the tokens. In the 32x32 MFMA output layout a lane holds one column
@@ -102,7 +101,8 @@ __device__ __forceinline__ void stats_cols(f32x16 (&acc)[4][4], int64_t m0, int 
 
 template <int DT, bool A_FP8, bool TANH>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stats_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
-  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
+  constexpr bool R5 = ring5_ok(DT, A_FP8);
+  __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
@@ -112,6 +112,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
   f32x16 acc[4][4];
   if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
+  else if constexpr (R5) mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
   else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
@@ -329,7 +330,8 @@ __device__ __forceinline__ void dz_store_staged(const f32x16 (&acc)[4][4], const
 
 template <int DT, bool A_FP8, bool TANH>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_dz_kernel(Operand A, Operand B, GemmShape s, DzArgs e) {
-  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
+  constexpr bool R5 = ring5_ok(DT, A_FP8);
+  __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
@@ -339,6 +341,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
   f32x16 acc[4][4];
   if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
+  else if constexpr (R5) mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
   else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
@@ -401,10 +404,10 @@ __device__ __forceinline__ void store_any(const f32x16 (&acc)[4][4], void *C, co
   }
 }
 
-// LAYOUT bit 0: A is MN-contiguous (OpCols), bit 1: B is.
-template <int DT, int OT, int LAYOUT>
+template <int DT, int OT>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
-  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
+  constexpr bool R5 = ring5_ok(DT, false);
+  __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
@@ -415,9 +418,8 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (mvalid <= 0 || nvalid <= 0) return;
 
   f32x16 acc[4][4];
-  typedef typename std::conditional<(LAYOUT & 1) != 0, OpCols, OpRows>::type OA;
-  typedef typename std::conditional<(LAYOUT & 2) != 0, OpCols, OpRows>::type OB;
-  mainloop_dma<DT, OA, OB>(A, B, m0, n0, K_eff, smem, acc);
+  if constexpr (R5) mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, K_eff, smem, acc);
+  else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
   store_any<typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
 }
 
@@ -466,36 +468,24 @@ int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operan
   return octo_fail(OCTO_EUNSUPPORTED, "gemm_dz: dtype %d", dt);
 }
 
-template <int DT, int LAYOUT>
+template <int DT>
 static int go_store(const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e, hipStream_t st) {
   switch (e.dtype) {
-    case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16, LAYOUT>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16, LAYOUT>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32, LAYOUT>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
     default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
   }
   OCTO_CHECK_LAUNCH("gemm_store");
   return OCTO_OK;
 }
 
-// MN-contiguous operands (layout != 0) take 16-bit types only.
-template <int DT>
-static int go_store_layout(int layout, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
-                           hipStream_t st) {
-  switch (layout) {
-    case 0: return go_store<DT, 0>(A, B, s, e, st);
-    case 2: if constexpr (DT != OCTO_F32) return go_store<DT, 2>(A, B, s, e, st); break;
-    case 3: if constexpr (DT != OCTO_F32) return go_store<DT, 3>(A, B, s, e, st); break;
-  }
-  return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: layout %d for dtype %d", layout, DT);
-}
-
-int launch_gemm_store(int dt, int layout, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
+int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
                       hipStream_t st) {
   switch (dt) {
-    case OCTO_BF16: return go_store_layout<OCTO_BF16>(layout, A, B, s, e, st);
-    case OCTO_F16: return go_store_layout<OCTO_F16>(layout, A, B, s, e, st);
-    case OCTO_F32: return go_store_layout<OCTO_F32>(layout, A, B, s, e, st);
+    case OCTO_BF16: return go_store<OCTO_BF16>(A, B, s, e, st);
+    case OCTO_F16: return go_store<OCTO_F16>(A, B, s, e, st);
+    case OCTO_F32: return go_store<OCTO_F32>(A, B, s, e, st);
   }
   return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: dtype %d", dt);
 }

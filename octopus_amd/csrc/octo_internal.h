@@ -46,8 +46,7 @@ int launch_gemm_stats(int dt, bool a_fp8, bool tanh, const Operand &A, const Ope
                       const StatsArgs &e, hipStream_t st);
 int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
                    const DzArgs &e, hipStream_t st);
-// layout bit 0: A MN-contiguous, bit 1: B MN-contiguous (16-bit types only); Operand.rows then counts K-rows.
-int launch_gemm_store(int dt, int layout, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
+int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
                       hipStream_t st);
 
 // ---- small kernels (head_aux.hip) ---------------------------------------------------------------
@@ -79,10 +78,6 @@ int launch_merge(const MergeArgs &a, hipStream_t st);
 // Source row r is row map[r] (or r) of src; dst holds the staged MFMA type (bf16/f16/f32).
 // dst[r, c] = src row map[r] (or r), element c, for r < rows_pad, c < cols; rows r at or past the valid count read 0.
 // Same dtype on both sides (a byte copy of 16-bit or 32-bit elements).
-int launch_gather_rows(const void *src, int64_t ld_src, int esz, const int64_t *map, const int32_t *count,
-                       int64_t count_off, int64_t rows, int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst,
-                       hipStream_t st);
-
 int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *src_scale,
                      const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
                      int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st);
