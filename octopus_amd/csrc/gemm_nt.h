@@ -413,6 +413,17 @@ struct OpRows128 {
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) fo[sub] = row * EKB + (((2 * sub) ^ hs) << 4);
   }
+  // A plain operand (no row map) whose first `valid` rows from row0 exist: no memory reads, so a persistent loop can
+  // re-point the DMA at its next tile without waiting on loads.
+  __device__ __forceinline__ void init_plain(const Operand &op, int64_t row0, int64_t valid) {
+    const int w = threadIdx.x >> 6, i = threadIdx.x & 63;
+#pragma unroll
+    for (int q = 0; q < ENI; ++q) {
+      const int r = (4 * q + w) * 8 + (i >> 3);
+      off[q] = (r < valid ? (uint32_t)(r * op.ld) : 0x80000000u) + coff;
+    }
+    rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
+  }
   // K chunks at or past kbytes (bytes per row) read zero
   __device__ __forceinline__ void dma(int k, int q, uint32_t kbytes, lds_char *slice) const {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -427,10 +438,11 @@ struct OpRows128 {
 // The 16-bit GEMMs (bf16 / f16 operands, no fp8 widening) run the ring loop; fp32 and fp8 the 4-stage one.
 __host__ __device__ constexpr bool ring5_ok(int dt, bool fp8) { return (dt == OCTO_BF16 || dt == OCTO_F16) && !fp8; }
 
-// One stage of the ring loop: four sub-steps of 16 MFMAs. DMA: issue stage k + 2 (A under sub-steps 0, 1; B under
-// sub-step 3). NEXT: a stage k + 1 exists (barrier B_k, and its first fragments are read under sub-step 3).
-template <int DT, typename OA, typename OB, bool DMA, bool NEXT>
-__device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int k, int sa, uint32_t kbytes,
+// One stage of the ring loop: four sub-steps of 16 MFMAs on the stage in slots (sa, sa + 1). DMA: issue stage kd of
+// the operands' current tile (stage k + 2 of the stream: A under sub-steps 0, 1; B under sub-step 3). NEXT: a stage
+// k + 1 exists (barrier B_k); XFRAG: its first fragments are read under sub-step 3 (else the caller reads them).
+template <int DT, typename OA, typename OB, bool DMA, bool NEXT, bool XFRAG = NEXT>
+__device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd, int sa, uint32_t kbytes,
                                             lds_char *smem, i32x4 (&fa)[2][4], i32x4 (&fb)[2][4],
                                             f32x16 (&acc)[4][4]) {
   // slots: stage k at (sa, sa + 1), stage k + 1 at (sa + 2, sa + 3), stage k + 2's A at sa + 4, its B at sa
@@ -459,7 +471,7 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int k,
           if (q < 4) fa[nxt][q] = opa.frag(cA, sub + 1, q);
           else fb[nxt][q - 4] = opb.frag(cB, sub + 1, q - 4);
           OCTO_FENCE();
-        } else if (NEXT) {
+        } else if (NEXT && XFRAG) {
           if (q < 4) fa[nxt][q] = opa.frag(nA, 0, q);
           else fb[nxt][q - 4] = opb.frag(nB, 0, q - 4);
           OCTO_FENCE();
@@ -467,11 +479,11 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int k,
       }
       if (DMA) {
         if (sub < 2 && q >= 8 && (q & 1)) {  // A slice of stage k + 2: 4 instructions per sub-step
-          opa.dma(k + 2, 4 * sub + ((q - 8) >> 1), kbytes, dA);
+          opa.dma(kd, 4 * sub + ((q - 8) >> 1), kbytes, dA);
           OCTO_FENCE();
         }
         if (sub == 3 && (q & 1)) {  // B slice of stage k + 2
-          opb.dma(k + 2, q >> 1, kbytes, dB);
+          opb.dma(kd, q >> 1, kbytes, dB);
           OCTO_FENCE();
         }
       }
@@ -528,7 +540,7 @@ __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &
   int sa = 0;  // slot of stage k's A slice: 2 k mod 5
   int k = 0;
   for (; k + 2 < nk; ++k) {
-    ring5_stage<DT, OA, OB, true, true>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
+    ring5_stage<DT, OA, OB, true, true>(opa, opb, k + 2, sa, kbytes, smem, fa, fb, acc);
     sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
   }
   if (k + 1 < nk) {
@@ -539,6 +551,119 @@ __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &
   ring5_stage<DT, OA, OB, false, false>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
   __builtin_amdgcn_s_barrier();
+}
+
+// ---- persistent tile stream (short-K GEMMs: the forward and the dz recompute, K = d) --------------------
+//
+// One workgroup per CU. Workgroup b walks the tiles of the one-shot grid b, b + G, b + 2 G, ... (G = grid size, a
+// multiple of 8, so every tile it visits belongs to its own XCD's share, as in tile_of), skipping tiles with no
+// valid row. The K-stages of its tiles form one continuous ring-5 stream: the stage two ahead is always in flight,
+// across tile boundaries, so a tile's first stages land while the previous tile finishes and its epilogue runs,
+// and no workgroup launch or pipeline fill sits between tiles. Both operands are plain (no row map) and the row
+// count is read once, so re-pointing the DMA at the next tile reads no memory inside the loop. Past the last tile
+// the DMA keeps running with every row out of range: it writes zeros into slots nobody reads again, and every
+// stage keeps the same instruction stream and the same vmcnt accounting.
+//
+// After a tile's last stage, epi(acc, mt, nt, nvalid, red) runs (nvalid: the tile's valid N rows); `red` is the
+// one 32 KB ring slot that is free at that point (the last stage's B slot: the stream's next DMA into it is issued
+// after the epilogue). A barrier follows the epilogue, so every wave is done with `red` before that DMA.
+__device__ __forceinline__ bool tile_at32(int mtiles, int ntiles, int group_m, int vb, int &mt, int &nt) {
+  const int x = vb & 7;
+  const int k = vb >> 3;
+  const int mx = (mtiles - x + 7) >> 3;
+  if (k >= mx * ntiles) return false;
+  const int span = group_m * ntiles;
+  const int gid = k / span;
+  const int first = gid * group_m;
+  const int gsize = (mx - first) < group_m ? (mx - first) : group_m;
+  const int local = k - gid * span;
+  mt = x + 8 * (first + local % gsize);
+  nt = local / gsize;
+  return true;
+}
+
+// s.count (if any) bounds N (count_on == 2). Requires K > 64 (two or more stages per tile).
+template <int DT, typename Epi>
+__device__ __forceinline__ void persistent_ring5(const Operand &A, const Operand &B, const GemmShape &s, lds_char *smem,
+                                                 Epi &&epi) {
+  static_assert(DT == OCTO_BF16 || DT == OCTO_F16, "16-bit operands");
+  const int w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int64_t ntot = dev_count(s.count, s.count_off, s.N);  // valid N rows, read once
+  const int mtiles = s.mtiles, ntiles = (int)cdiv(ntot, TN), gm = s.group_m;
+  const int nvb = (int)tile_grid(mtiles, ntiles);
+  const int G = (int)gridDim.x;
+  const uint32_t kbytes = (uint32_t)(s.K * 2);
+  const int nk = (int)((kbytes + EKB - 1) / EKB);
+
+  int cvb = (int)blockIdx.x, cmt = 0, cnt = 0;  // compute tile
+  while (cvb < nvb && !tile_at32(mtiles, ntiles, gm, cvb, cmt, cnt)) cvb += G;
+  if (cvb >= nvb) return;
+
+  OpRows128 opa, opb;
+  opa.init(A, (int64_t)cmt * TM, wm, (uint32_t)s.K);  // swizzle and fragment offsets; rows re-pointed per tile
+  opb.init(B, (int64_t)cnt * TN, wn, (uint32_t)s.K);
+  int fvb = cvb, fk = 2;  // fetch cursor: tile, next stage
+  int ahead = 0;          // tiles the fetch cursor is past the compute tile
+  auto point = [&](int mt, int nt, bool live) {
+    const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
+    opa.init_plain(A, m0, live ? A.rows - m0 : 0);
+    opb.init_plain(B, n0, live ? ntot - n0 : 0);
+  };
+  auto advance = [&]() {  // after a stage of the fetch tile was issued
+    if (fk < nk || fvb >= nvb) return;
+    int mt = 0, nt = 0, v = fvb + G;
+    while (v < nvb && !tile_at32(mtiles, ntiles, gm, v, mt, nt)) v += G;
+    fvb = v;
+    fk = 0;
+    if (v < nvb) ++ahead;
+    point(mt, nt, v < nvb);
+  };
+  point(cmt, cnt, true);
+
+#pragma unroll
+  for (int q = 0; q < ENI; ++q) opa.dma(0, q, kbytes, smem);
+#pragma unroll
+  for (int q = 0; q < ENI; ++q) opb.dma(0, q, kbytes, smem + ESLICE);
+#pragma unroll
+  for (int q = 0; q < ENI; ++q) opa.dma(1, q, kbytes, smem + 2 * ESLICE);
+#pragma unroll
+  for (int q = 0; q < ENI; ++q) opb.dma(1, q, kbytes, smem + 3 * ESLICE);
+  advance();
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * ENI));  // stage 0 landed
+  __builtin_amdgcn_s_barrier();
+
+  f32x16 acc[4][4];
+  i32x4 fa[2][4], fb[2][4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    fa[0][b] = opa.frag(smem, 0, b);
+    fb[0][b] = opb.frag(smem + ESLICE, 0, b);
+  }
+  int sa = 0;
+  while (true) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    for (int k = 0; k < nk; ++k) {
+      ring5_stage<DT, OpRows128, OpRows128, true, true>(opa, opb, fk, sa, kbytes, smem, fa, fb, acc);
+      ++fk;
+      advance();
+      sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
+    }
+    const int64_t n0 = (int64_t)cnt * TN;
+    epi(acc, cmt, cnt, (ntot - n0) < TN ? (ntot - n0) : (int64_t)TN, smem + (sa == 0 ? ENSLOT - 1 : sa - 1) * ESLICE);
+    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+    __builtin_amdgcn_s_barrier();  // every wave is done with the epilogue's slot
+    if (ahead == 0) break;
+    --ahead;
+    cvb += G;
+    while (!tile_at32(mtiles, ntiles, gm, cvb, cmt, cnt)) cvb += G;
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
 }
 
 // Row (M) and column (N) of accumulator element v of block (i, j), relative to the tile origin.

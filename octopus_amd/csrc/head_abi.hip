@@ -83,13 +83,17 @@ int staged_dtype(int w_dtype) { return w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_d
 
 struct FwdLayout {
   int64_t mtiles;
-  size_t part, total;
+  size_t part, rows, total;
 };
-FwdLayout fwd_layout(int64_t n_max, int V) {
+// part: (m, S, U) per (row, vocab tile). rows: the compacted hidden rows [n_max, d] when the forward GEMM is the
+// persistent one (16-bit operands), which takes plain operands.
+FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
   FwdLayout L;
   L.mtiles = cdiv(V, TM);
   L.part = 0;
-  L.total = align_up((size_t)n_max * L.mtiles * sizeof(f32x4));
+  L.rows = align_up((size_t)n_max * L.mtiles * sizeof(f32x4));
+  L.total = L.rows;
+  if (ring5_ok(w_dtype, false)) L.total += align_up((size_t)n_max * d * elem_bytes(w_dtype));
   return L;
 }
 
@@ -99,7 +103,7 @@ FwdLayout fwd_layout(int64_t n_max, int V) {
 struct BwdLayout {
   int64_t P, V_pad, passes;
   int esz;
-  size_t wt, ht, dza, dzb, gacc, total;
+  size_t wt, ht, dza, dzb, hit, gacc, total;
 };
 BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw) {
   BwdLayout L;
@@ -116,6 +120,8 @@ BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, boo
   if (need_gh) off += align_up((size_t)L.P * L.V_pad * L.esz);
   L.dzb = off;  // dz [V_pad, P], vocab-major (grad_W)
   if (need_gw) off += align_up((size_t)L.V_pad * L.P * L.esz);
+  L.hit = off;  // dz at each row's label [P] fp32 (16-bit dz epilogue)
+  if (L.esz == 2) off += align_up((size_t)L.P * sizeof(float));
   L.gacc = off;  // fp32 grad_W partial sums across passes, for a 16-bit grad_W
   if (need_gw && L.passes > 1 && w_dtype != OCTO_F32) off += align_up((size_t)V * d * sizeof(float));
   L.total = off;
@@ -282,7 +288,7 @@ int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flag
   if (flags & OCTO_WS_BACKWARD) {
     *bytes = bwd_layout(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW)).total;
   } else {
-    *bytes = fwd_layout(n_max, V).total;
+    *bytes = fwd_layout(n_max, d, V, w_dtype).total;
   }
   return OCTO_OK;
 }
@@ -298,13 +304,20 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
   if (rc) return rc;
   OCTO_CHECK_ARG(!out2 || ld_out2 >= 2, "head_fwd: ld_out2 < 2");
   if (n_max == 0) return OCTO_OK;
-  const FwdLayout L = fwd_layout(n_max, V);
+  const FwdLayout L = fwd_layout(n_max, d, V, w_dtype);
   if (!ws || ws_bytes < L.total)
     return octo_fail(OCTO_EWORKSPACE, "head_fwd: workspace %zu < %zu bytes", ws_bytes, L.total);
   hipStream_t st = (hipStream_t)stream;
 
   const Operand A = weight_operand(w, ldw, cm, V);
-  const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
+  Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
+  if (idx && ring5_ok(cm.dt, cm.fp8)) {  // the persistent GEMM reads the compacted rows as one block
+    void *rows = (char *)ws + L.rows;
+    rc = launch_gather_rows(h, h_rows, ldh * cm.hesz, idx, count, n_max, (int64_t)d * cm.hesz, rows,
+                            (int64_t)d * cm.hesz, st);
+    if (rc) return rc;
+    B = plain_operand(rows, (int64_t)d * cm.hesz, n_max, count, 0);
+  }
   const GemmShape s = shape(V, n_max, d, kGroupM, 2, count, 0);
   StatsArgs e;
   e.part = (f32x4 *)((char *)ws + L.part);
@@ -410,6 +423,36 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     e.c = cm.c;
     e.pre = cm.pre;
     e.gmul = cm.gmul;
+    e.hit = nullptr;
+    if (esz == 2) {  // the label entries of this pass's dz, written by the dz epilogue over its dense values
+      HitArgs ha;
+      ha.h = h;
+      ha.ldh = ldh;
+      ha.h_dtype = h_dtype;
+      ha.idx = idx;
+      ha.w = w;
+      ha.ldw = ldw;
+      ha.w_dtype = w_dtype;
+      ha.wscale = w_scale;
+      ha.labels = labels;
+      ha.label_idx = e.label_idx;
+      ha.lse = lse;
+      ha.g = g;
+      ha.count = count;
+      ha.r0 = r0;
+      ha.rows = rows;
+      ha.n_max = n_max;
+      ha.d = d;
+      ha.V = V;
+      ha.c = cm.c;
+      ha.pre = cm.pre;
+      ha.gmul = cm.gmul;
+      ha.use_tanh = use_tanh;
+      ha.hit = (float *)(wsb + L.hit);
+      rc = launch_hit(ha, st);
+      if (rc) return rc;
+      e.hit = ha.hit;
+    }
     {
       TimedLaunch t("gemm_dz", st);
       rc = launch_gemm_dz(cm.dt, cm.fp8, use_tanh != 0, Aw, Bh, s1, e, st);

@@ -1,6 +1,8 @@
 // Memory-bound kernels of the LM-head path and their C-ABI entry points:
 //   merge          per-row merge of the vocab-tile softmax partials + target logit -> logp, entropy, lse
+//   hit            per-row dz value at the label (the backward's dz epilogue writes it over the dense entry)
 //   transpose      K-contiguous copies (W^T, gathered h^T) feeding the backward's gradient GEMMs
+//   gather_rows    the compacted hidden rows as one contiguous block (the persistent forward GEMM's operand)
 //   compact_rows   masked-row compaction, ascending (torch.nonzero order), count left on the device
 //   columns fwd/bwd  _head_columns over materialised logits
 //   pairs expand/grad, rows scatter, gather   the index plumbing of tree_head_output / _scored_rows
@@ -66,6 +68,53 @@ int launch_merge(const MergeArgs &a, hipStream_t st) {
   return OCTO_OK;
 }
 
+// ---- dz label entries ----------------------------------------------------------------------------------
+// One wave per row: the target logit h . W_y in fp32 (as the forward's merge), then the dz value at the label with
+// the dz kernel's own formula, so the GEMM epilogue writes it over the dense entry -g p / T instead of testing every
+// element against the label.
+__global__ __launch_bounds__(256) void hit_kernel(HitArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= a.rows) return;
+  const int64_t r = a.r0 + i;
+  const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
+  float hv_out = 0.f;
+  if (r < cnt) {
+    const int64_t hrow = a.idx ? a.idx[r] : r;
+    const int64_t y = a.labels[a.label_idx ? a.label_idx[r] : r];
+    if (y >= 0 && y < a.V) {
+      float dot = 0.f;
+      for (int k = lane; k < a.d; k += 64) {
+        const float hv = load_as_f32(a.h, a.h_dtype, hrow * a.ldh + k);
+        float wv;
+        if (a.w_dtype == OCTO_FP8E4M3) wv = e4m3_to_f32(((const uint8_t *)a.w)[y * a.ldw + k]);
+        else wv = load_as_f32(a.w, a.w_dtype, y * a.ldw + k);
+        dot = __builtin_fmaf(hv, wv, dot);
+      }
+      dot = wave_sum(dot);
+      const bool f8 = a.w_dtype == OCTO_FP8E4M3;
+      const float x = f8 ? dot * a.wscale[y] : dot;
+      const float lse2 = a.lse[r] * OCTO_LOG2E, gs = a.g[r] * a.gmul;
+      float v;
+      if (a.use_tanh) {
+        const float th = ftanh(a.pre * x);
+        v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(th, a.c, -lse2)), gs) * (1.f - th * th);
+      } else {
+        v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(x, a.c, -lse2)), gs);
+      }
+      hv_out = f8 ? v * a.wscale[y] : v;
+    }
+  }
+  if (lane == 0) a.hit[i] = hv_out;
+}
+
+int launch_hit(const HitArgs &a, hipStream_t st) {
+  if (a.rows == 0) return OCTO_OK;
+  hipLaunchKernelGGL(hit_kernel, dim3((unsigned)cdiv(a.rows, 4)), dim3(256), 0, st, a);
+  OCTO_CHECK_LAUNCH("hit");
+  return OCTO_OK;
+}
+
 // ---- transpose -----------------------------------------------------------------------------------
 // dst[c, r] = src[row(r), c]: 64 x 64 tiles through LDS (fp32 words, padded against bank conflicts).
 __global__ __launch_bounds__(256) void transpose_kernel(const void *src, int64_t ld_src, int src_dtype,
@@ -101,6 +150,38 @@ int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float
   hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, st, src, ld_src, src_dtype, map, count, count_off, rows,
                      rows_pad, cols, dst, ld_dst, dst_dtype);
   OCTO_CHECK_LAUNCH("transpose");
+  return OCTO_OK;
+}
+
+// ---- row gather --------------------------------------------------------------------------------------
+// dst[r] = src[map[r]] for the rows below the device count (one workgroup per row, 16-byte chunks); a map entry
+// outside [0, src_rows) gives a zero row; rows at or past the count are left untouched (the GEMMs that read dst
+// treat them as absent).
+__global__ __launch_bounds__(256) void gather_rows_kernel(const char *src, int64_t src_rows, int64_t ld_src,
+                                                          const int64_t *map, const int32_t *count, int64_t rows,
+                                                          int64_t row_bytes, char *dst, int64_t ld_dst) {
+  const int64_t r = blockIdx.x;
+  if (r >= dev_count(count, 0, rows)) return;
+  const int64_t p = map[r];
+  const bool ok = p >= 0 && p < src_rows;
+  const char *s = src + (ok ? p : 0) * ld_src;
+  char *d = dst + r * ld_dst;
+  for (int64_t c = (int64_t)threadIdx.x * 16; c < row_bytes; c += 256 * 16) {
+    i32x4 v = {0, 0, 0, 0};
+    if (ok) v = *(const i32x4 *)(s + c);
+    *(i32x4 *)(d + c) = v;
+  }
+}
+
+int launch_gather_rows(const void *src, int64_t src_rows, int64_t ld_src_bytes, const int64_t *map,
+                       const int32_t *count, int64_t rows, int64_t row_bytes, void *dst, int64_t ld_dst_bytes,
+                       hipStream_t st) {
+  if (rows == 0 || row_bytes == 0) return OCTO_OK;
+  if (row_bytes % 16 || ld_src_bytes % 16 || ld_dst_bytes % 16)
+    return octo_fail(OCTO_EINVAL, "gather_rows: rows must be whole 16-byte chunks");
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, (const char *)src, src_rows,
+                     ld_src_bytes, map, count, rows, row_bytes, (char *)dst, ld_dst_bytes);
+  OCTO_CHECK_LAUNCH("gather_rows");
   return OCTO_OK;
 }
 

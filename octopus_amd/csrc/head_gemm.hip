@@ -132,16 +132,40 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   }
 }
 
+// Persistent form (16-bit operands, both plain): the tiles' K-stages run as one stream (persistent_ring5) and the
+// epilogue reduces through the free ring slot with bare barriers (no memory fence, so the next tile's DMA keeps
+// flowing underneath).
+template <int DT, bool TANH>
+__global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stats_persistent_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
+  lds_char *smem = (lds_char *)smem_;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  persistent_ring5<DT>(A, B, s, smem, [&](f32x16 (&acc)[4][4], int mt, int nt, int64_t nvalid, lds_char *slot) {
+    const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
+    pre_transform<false, TANH>(acc, m0, wm, lane, nullptr, e.V, e.pre);
+    lds_f32x4 *red = (lds_f32x4 *)slot;
+    if (m0 + TM > e.V) stats_cols<true>(acc, m0, wm, wn, lane, e.V, e.c, red);
+    else stats_cols<false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
+    __builtin_amdgcn_s_barrier();
+    const int t = threadIdx.x;
+    if (t < nvalid) {
+      const f32x4 a = red[t], b = red[256 + t];
+      Stat3 sa{a[0], a[1], a[2]}, sb{b[0], b[1], b[2]};
+      Stat3 r = stat_merge(sa, sb);
+      f32x4 o;
+      o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
+      e.part[(n0 + t) * e.mtiles + mt] = o;
+    }
+  });
+}
+
 // ---- epilogue: dz recompute ------------------------------------------------------------------
 //
-// dz of the 256 (vocab) x 256 (token) tile is computed in place in the accumulators, packed to 16-bit
-// and written out through LDS (the 128 KB stage ring, free after the mainloop) in two passes, so that
-// both global layouts are written as whole 512-byte row segments with 16-byte stores:
-//   dzA [token][vocab]: each lane holds 4 consecutive vocab rows of one token -> one 8-byte LDS write;
-//   dzB [vocab][token]: a 4 x 4 transpose inside each lane quad (DPP quad_perm) gives each lane 4
-//                       consecutive tokens of one vocab row -> one 8-byte LDS write.
-// LDS rows are 512 bytes; the 8-byte slot index is XOR-swizzled so the 32 lanes of a half-wave hit
-// distinct banks, and the read-back of 16 bytes stays a contiguous (possibly half-swapped) slot pair.
+// dz = g (onehot - p) / T x post'(z) of the 256 (vocab) x 256 (token) tile, written in both global layouts
+// (dzA [token][vocab] for grad_h, dzB [vocab][token] for grad_W). 16-bit types go through one LDS staging tile as
+// whole 512-byte and 256-byte row segments (dz_stage / dz_write below); fp32 is computed in place in the
+// accumulators and stored directly.
 
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -157,14 +181,6 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi, f16x2_t *) {
   p[0] = (_Float16)lo;
   p[1] = (_Float16)hi;
   return __builtin_bit_cast(uint32_t, p);
-}
-
-// quad lane exchanges (DPP quad_perm): swap with lane ^ 1, lane ^ 2
-__device__ __forceinline__ uint32_t quad_swap1(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, true);
-}
-__device__ __forceinline__ uint32_t quad_swap2(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, true);
 }
 
 // Stream a 256 x 512-byte LDS tile (rows stored with slot swizzle `s(row)` on 8-byte slots) to global
@@ -273,58 +289,114 @@ __device__ __forceinline__ void dz_store_direct(const f32x16 (&acc)[4][4], const
   }
 }
 
-// 16-bit dz through LDS (see the layout notes above).
-template <typename P2>
-__device__ __forceinline__ void dz_store_staged(const f32x16 (&acc)[4][4], const DzArgs &e, int64_t m0, int64_t n0,
-                                                int wm, int wn, int lane, lds_char *tile) {
-  if (e.dzA) {  // [token][vocab]
+// 16-bit dz through one LDS staging tile T (the ring, free after the mainloop): T[t] holds dz of token t (tile
+// column) over the tile's 256 vocabulary rows, as 64 slots of 8 bytes (4 consecutive rows); logical slot s of token t
+// sits at physical slot s ^ dz_swz(t). That one swizzle serves all three accesses without bank conflicts:
+//   - the accumulator writes (a half-wave: 32 tokens t & 31 = lane, one logical slot);
+//   - the token-major read-back (16 lanes: one token, 16 consecutive 16-byte pairs);
+//   - the vocab-major read-back by transposing reads (16 lanes: 16 tokens t & 31 in {8k + e}, one slot; the two
+//     16-lane groups of a 32-lane pass differ in bit 5 of t, which flips slot bit 2 and makes their sets disjoint).
+// The dense pass writes -g p / T x post' (x fp8 row scale) everywhere; after a barrier one thread per token writes the
+// label entry (launch_hit's value) over it, so no element is compared against the label.
+__device__ __forceinline__ int dz_swz(int t) { return (t & 31) ^ (((t >> 5) & 1) << 2); }
+
+typedef __attribute__((address_space(3))) short lds_short;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+template <typename P2, bool A_FP8, bool TANH, bool EDGE>
+__device__ __forceinline__ void dz_stage(const f32x16 (&acc)[4][4], const DzArgs &e, int64_t m0, int64_t n0,
+                                         int64_t nvalid, int wm, int wn, int lane, lds_char *tile) {
+  const int h = lane >> 5;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tt = acc_col(wn, j, lane);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int slot = (acc_row(wm, i, 4 * g4, lane) >> 2) ^ (tt & 31);
-          i32x2 pk;
-          pk[0] = (int)pack2(acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], (P2 *)nullptr);
-          pk[1] = (int)pack2(acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3], (P2 *)nullptr);
-          *(lds_i32x2 *)(tile + tt * 512 + slot * 8) = pk;
-        }
+  for (int j = 0; j < 4; ++j) {
+    const int tt = acc_col(wn, j, lane);
+    float lse2 = 0.f, ngs = 0.f;  // -g / T (0 for tokens past the pass's count: dz 0, also in K-padding)
+    if (tt < nvalid) {
+      const int64_t r = e.row_off + n0 + tt;
+      lse2 = e.lse[r] * OCTO_LOG2E;
+      ngs = -(e.g[r] * e.gmul);
     }
-    __syncthreads();
-    lds_tile_to_global(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return row & 31; });
-    __syncthreads();
+    const int sw = dz_swz(tt);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int rl = wm * 128 + i * 32 + 8 * g4 + 4 * h;  // first of this lane's 4 vocab rows in the tile
+        float d[4];
+        float sc[4] = {1.f, 1.f, 1.f, 1.f};
+        if constexpr (A_FP8) {
+          const int64_t row = m0 + rl;
+          if (row + 3 < e.V) {
+            const f32x4 q = *(const f32x4 *)(e.wscale + row);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) sc[u] = q[u];
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) sc[u] = (row + u < e.V) ? e.wscale[row + u] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float x = acc[i][j][4 * g4 + u];
+          if constexpr (TANH) {
+            const float th = ftanh(e.pre * x);
+            d[u] = ngs * fexp2(__builtin_fmaf(th, e.c, -lse2)) * (1.f - th * th);
+          } else {
+            d[u] = ngs * fexp2(__builtin_fmaf(x, e.c, -lse2));
+          }
+          if constexpr (A_FP8) d[u] *= sc[u];
+          if constexpr (EDGE) d[u] = (m0 + rl + u < e.V) ? d[u] : 0.f;
+        }
+        i32x2 pk;
+        pk[0] = (int)pack2(d[0], d[1], (P2 *)nullptr);
+        pk[1] = (int)pack2(d[2], d[3], (P2 *)nullptr);
+        *(lds_i32x2 *)(tile + tt * 512 + (((rl >> 2) ^ sw) << 3)) = pk;
+      }
   }
-  if (e.dzB) {  // [vocab][token]: 4 x 4 transpose inside each lane quad first
-    const int b = lane & 3;
-    const int rowsel = (b == 1) ? 2 : ((b == 2) ? 1 : b);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int slot0 = (acc_col(wn, j, lane) & ~3) >> 2;  // 4-token slot of this quad
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const uint32_t w01 = pack2(acc[i][j][4 * g4], acc[i][j][4 * g4 + 1], (P2 *)nullptr);
-          const uint32_t w23 = pack2(acc[i][j][4 * g4 + 2], acc[i][j][4 * g4 + 3], (P2 *)nullptr);
-          const uint32_t recv = quad_swap1((b & 1) ? w01 : w23);
-          // even lanes: rows r0, r0+1 of tokens (n, n+1); odd lanes: rows r0+2, r0+3 of tokens (n-1, n)
-          const uint32_t x = (b & 1) ? __builtin_amdgcn_perm(w23, recv, 0x05040100u)
-                                     : __builtin_amdgcn_perm(recv, w01, 0x05040100u);
-          const uint32_t y = (b & 1) ? __builtin_amdgcn_perm(w23, recv, 0x07060302u)
-                                     : __builtin_amdgcn_perm(recv, w01, 0x07060302u);
-          const uint32_t recv2 = quad_swap2((b & 2) ? x : y);
-          i32x2 pk;
-          pk[0] = (int)((b & 2) ? recv2 : x);
-          pk[1] = (int)((b & 2) ? y : recv2);
-          const int vr = acc_row(wm, i, 4 * g4, lane) + rowsel;
-          const int slot = slot0 ^ ((vr & 3) << 3);
-          *(lds_i32x2 *)(tile + vr * 512 + slot * 8) = pk;
-        }
+}
+
+template <typename P2>
+__device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0, int64_t nvalid, lds_char *tile) {
+  typedef typename std::conditional<std::is_same<P2, bf16x2>::value, __bf16, _Float16>::type ET;
+  const int t = threadIdx.x;
+  // the label entry of token t (column t of the tile), loaded before the barrier that ends the dense pass
+  int yl = -1;
+  float hv = 0.f;
+  if (t < nvalid) {
+    const int64_t r = e.row_off + n0 + t;
+    const int64_t y = e.labels[e.label_idx ? e.label_idx[r] : r] - m0;
+    if (y >= 0 && y < TM && m0 + y < e.V) {
+      yl = (int)y;
+      hv = e.hit[n0 + t];
     }
-    __syncthreads();
-    lds_tile_to_global(tile, (char *)e.dzB + (m0 * e.ldB + n0) * 2, e.ldB * 2, [](int row) { return (row & 3) << 3; });
+  }
+  __syncthreads();  // dense pass written
+  if (yl >= 0) {
+    const ET v = (ET)hv;
+    *(lds_short *)(tile + t * 512 + (((yl >> 2) ^ dz_swz(t)) << 3) + (yl & 3) * 2) = __builtin_bit_cast(short, v);
+  }
+  __syncthreads();
+  if (e.dzA)  // [token][vocab]: 512-byte rows
+    lds_tile_to_global(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return dz_swz(row); });
+  if (e.dzB) {  // [vocab][token] by transposing reads: a 16-lane group gives 4 vocab rows x 32 tokens, 8 per lane
+    const int w = t >> 6, l = t & 63, G = l >> 4, i = l & 15;
+    const int src = 8 * (i & 3) + (i >> 2);  // this lane's source token as a transposing-read source, 0..31
+#pragma unroll 4
+    for (int p = 0; p < 32; ++p) {
+      const int u = p * 4 + w;              // unit: 4 vocab rows (quad q) x 128 tokens (half)
+      const int q = u >> 1, tb = 128 * (u & 1) + 32 * G;
+      const int t1 = tb + src, t2 = t1 + 4;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + t1 * 512 + ((q ^ dz_swz(t1)) << 3)));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + t2 * 512 + ((q ^ dz_swz(t2)) << 3)));
+      i32x4 v;
+      v[0] = __builtin_bit_cast(i32x2, lo)[0];
+      v[1] = __builtin_bit_cast(i32x2, lo)[1];
+      v[2] = __builtin_bit_cast(i32x2, hi)[0];
+      v[3] = __builtin_bit_cast(i32x2, hi)[1];
+      const int vr = 4 * q + (i & 3);
+      *(i32x4 *)((char *)e.dzB + ((m0 + vr) * e.ldB + n0 + tb + 8 * (i >> 2)) * 2) = v;
+    }
   }
 }
 
@@ -346,12 +418,14 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
   if constexpr (A_FP8) pre_transform<true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-  dz_in_place<A_FP8, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
   if constexpr (DT == OCTO_F32) {
+    dz_in_place<A_FP8, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
     dz_store_direct(acc, e, m0, n0, wm, wn, lane);
   } else {
     typedef typename std::conditional<DT == OCTO_BF16, bf16x2, f16x2_t>::type P2;
-    dz_store_staged<P2>(acc, e, m0, n0, wm, wn, lane, smem);
+    if (m0 + TM > e.V) dz_stage<P2, A_FP8, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+    else dz_stage<P2, A_FP8, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+    dz_write<P2>(e, m0, n0, nvalid, smem);
   }
 }
 
@@ -427,8 +501,36 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
 static inline dim3 grid_of(const GemmShape &s) { return dim3((unsigned)tile_grid(s.mtiles, s.ntiles)); }
 
+// Workgroups of a persistent launch: one per CU, a multiple of 8 (the tile walk keeps each on its own XCD), at most
+// the one-shot grid.
+static unsigned persistent_grid(const GemmShape &s) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 8;
+    cus[dev] = n / 8 * 8;
+  }
+  const int64_t one_shot = tile_grid(s.mtiles, s.ntiles);
+  return (unsigned)(one_shot < cus[dev] ? one_shot : cus[dev]);
+}
+
+// The persistent forward takes 16-bit plain operands with at least two K-stages.
+static bool persistent_ok(int dt, bool fp8, const Operand &A, const Operand &B, const GemmShape &s) {
+  return ring5_ok(dt, fp8) && !A.map && !B.map && s.K > EKB / 2 && s.count_on != 1 && s.count_on != 3;
+}
+
 template <int DT, bool F8, bool TH>
 static int go_stats(const Operand &A, const Operand &B, const GemmShape &s, const StatsArgs &e, hipStream_t st) {
+  if constexpr (ring5_ok(DT, F8)) {
+    if (persistent_ok(DT, F8, A, B, s)) {
+      hipLaunchKernelGGL((gemm_stats_persistent_kernel<DT, TH>), dim3(persistent_grid(s)), dim3(NTHREADS), 0, st, A,
+                         B, s, e);
+      OCTO_CHECK_LAUNCH("gemm_stats");
+      return OCTO_OK;
+    }
+  }
   hipLaunchKernelGGL((gemm_stats_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
   OCTO_CHECK_LAUNCH("gemm_stats");
   return OCTO_OK;

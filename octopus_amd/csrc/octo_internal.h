@@ -31,8 +31,32 @@ struct DzArgs {
   int64_t row_off;
   int64_t V;
   const float *wscale;
+  const float *hit;  // 16-bit dz: the pass's label entries, hit[token] (launch_hit), written over the dense values
   float c, pre, gmul;
 };
+
+// The label entry of each row's dz, g (1 - p_y) / T x post'(z_y) (x the fp8 row scale), from an fp32 target logit:
+// hit[r - r0] for the compact rows r0 .. r0 + rows of a backward pass (0 past the count or for a label outside [0, V)).
+struct HitArgs {
+  const void *h;
+  int64_t ldh;
+  int h_dtype;
+  const int64_t *idx;        // compact row -> hidden row, or NULL
+  const void *w;
+  int64_t ldw;
+  int w_dtype;
+  const float *wscale;
+  const int64_t *labels;
+  const int64_t *label_idx;  // labels[label_idx[r]] when set
+  const float *lse, *g;
+  const int32_t *count;
+  int64_t r0, rows, n_max;
+  int d, V;
+  float c, pre, gmul;
+  int use_tanh;
+  float *hit;
+};
+int launch_hit(const HitArgs &a, hipStream_t st);
 
 struct StoreArgs {
   void *C;
@@ -78,6 +102,9 @@ int launch_merge(const MergeArgs &a, hipStream_t st);
 // Source row r is row map[r] (or r) of src; dst holds the staged MFMA type (bf16/f16/f32).
 // dst[r, c] = src row map[r] (or r), element c, for r < rows_pad, c < cols; rows r at or past the valid count read 0.
 // Same dtype on both sides (a byte copy of 16-bit or 32-bit elements).
+int launch_gather_rows(const void *src, int64_t src_rows, int64_t ld_src_bytes, const int64_t *map,
+                       const int32_t *count, int64_t rows, int64_t row_bytes, void *dst, int64_t ld_dst_bytes,
+                       hipStream_t st);
 int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *src_scale,
                      const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
                      int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st);
