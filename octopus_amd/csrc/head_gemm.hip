@@ -23,16 +23,16 @@ namespace octo {
 // ---- epilogue: online softmax statistics ----------------------------------------------------
 
 // acc *= per-vocab-row scale (fp8 weights), then the softcap tanh if any; then stats per token.
-template <bool A_FP8, bool TANH>
-__device__ __forceinline__ void pre_transform(f32x16 (&acc)[4][4], int64_t m0, int wm, int lane,
+template <class L, bool A_FP8, bool TANH>
+__device__ __forceinline__ void pre_transform(typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int lane,
                                               const float *wscale, int64_t V, float pre) {
   if constexpr (A_FP8) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float sc[16];
+    for (int i = 0; i < L::NI; ++i) {
+      float sc[L::NV];
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        int64_t row = m0 + acc_row(wm, i, 4 * g4, lane);
+      for (int g4 = 0; g4 < L::NV / 4; ++g4) {
+        int64_t row = m0 + L::row(wm, i, 4 * g4, lane);
         if (row + 3 < V) {
           f32x4 q = *(const f32x4 *)(wscale + row);
 #pragma unroll
@@ -43,58 +43,58 @@ __device__ __forceinline__ void pre_transform(f32x16 (&acc)[4][4], int64_t m0, i
         }
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < L::NJ; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] *= sc[v];
+        for (int v = 0; v < L::NV; ++v) acc[i][j][v] *= sc[v];
     }
   }
   if constexpr (TANH) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < L::NI; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < L::NJ; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = ftanh(pre * acc[i][j][v]);
+        for (int v = 0; v < L::NV; ++v) acc[i][j][v] = ftanh(pre * acc[i][j][v]);
   }
 }
 
 typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 
-template <bool MASK>
-__device__ __forceinline__ void stats_cols(f32x16 (&acc)[4][4], int64_t m0, int wm, int wn, int lane,
+template <class L, bool MASK>
+__device__ __forceinline__ void stats_cols(typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int wn, int lane,
                                            int64_t V, float c, lds_f32x4 *red) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < L::NJ; ++j) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < L::NI; ++i)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const bool ok = !MASK || (m0 + acc_row(wm, i, v, lane) < V);
+      for (int v = 0; v < L::NV; ++v) {
+        const bool ok = !MASK || (m0 + L::row(wm, i, v, lane) < V);
         if (ok) mx = fmaxf(mx, acc[i][j][v]);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = L::col_max(mx);
     const float m2 = mx * c;
     float S = 0.f, U = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < L::NI; ++i)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
+      for (int v = 0; v < L::NV; ++v) {
         const float t = __builtin_fmaf(acc[i][j][v], c, -m2);
         float e = fexp2(t);
         if (MASK) {
-          const bool ok = m0 + acc_row(wm, i, v, lane) < V;
+          const bool ok = m0 + L::row(wm, i, v, lane) < V;
           e = ok ? e : 0.f;
         }
         S += e;
         U = __builtin_fmaf(e, t, U);
       }
-    S += __shfl_xor(S, 32, 64);
-    U += __shfl_xor(U, 32, 64);
-    if (lane < 32) {
+    S = L::col_sum(S);
+    U = L::col_sum(U);
+    if (L::col_lane(lane)) {
       f32x4 o;
       o[0] = m2; o[1] = S; o[2] = U; o[3] = 0.f;
-      red[wm * 256 + acc_col(wn, j, lane)] = o;
+      red[wm * 256 + L::col(wn, j, lane)] = o;
     }
   }
 }
@@ -110,16 +110,22 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   const int64_t nvalid = dev_count(s.count, s.count_off + n0, s.N - n0);
   if (nvalid <= 0) return;
 
-  f32x16 acc[4][4];
-  if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
-  else if constexpr (R5) mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
-  else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
-
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
-  pre_transform<A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
   lds_f32x4 *red = (lds_f32x4 *)smem;
-  if (m0 + TM > e.V) stats_cols<true>(acc, m0, wm, wn, lane, e.V, e.c, red);
-  else stats_cols<false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  if constexpr (R5) {
+    f32x4 acc[8][8];
+    mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
+    pre_transform<Acc16, false, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+    if (m0 + TM > e.V) stats_cols<Acc16, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
+    else stats_cols<Acc16, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  } else {
+    f32x16 acc[4][4];
+    if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
+    else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
+    pre_transform<Acc32, A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+    if (m0 + TM > e.V) stats_cols<Acc32, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
+    else stats_cols<Acc32, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  }
   __syncthreads();
   const int t = threadIdx.x;
   if (t < nvalid) {
@@ -140,12 +146,12 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
   lds_char *smem = (lds_char *)smem_;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
-  persistent_ring5<DT>(A, B, s, smem, [&](f32x16 (&acc)[4][4], int mt, int nt, int64_t nvalid, lds_char *slot) {
+  persistent_ring5<DT>(A, B, s, smem, [&](f32x4 (&acc)[8][8], int mt, int nt, int64_t nvalid, lds_char *slot) {
     const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
-    pre_transform<false, TANH>(acc, m0, wm, lane, nullptr, e.V, e.pre);
+    pre_transform<Acc16, false, TANH>(acc, m0, wm, lane, nullptr, e.V, e.pre);
     lds_f32x4 *red = (lds_f32x4 *)slot;
-    if (m0 + TM > e.V) stats_cols<true>(acc, m0, wm, wn, lane, e.V, e.c, red);
-    else stats_cols<false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+    if (m0 + TM > e.V) stats_cols<Acc16, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
+    else stats_cols<Acc16, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
     __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
     __builtin_amdgcn_s_barrier();
     const int t = threadIdx.x;
@@ -291,38 +297,44 @@ __device__ __forceinline__ void dz_store_direct(const f32x16 (&acc)[4][4], const
 
 // 16-bit dz through one LDS staging tile T (the ring, free after the mainloop): T[t] holds dz of token t (tile
 // column) over the tile's 256 vocabulary rows, as 64 slots of 8 bytes (4 consecutive rows); logical slot s of token t
-// sits at physical slot s ^ dz_swz(t). That one swizzle serves all three accesses without bank conflicts:
-//   - the accumulator writes (a half-wave: 32 tokens t & 31 = lane, one logical slot);
+// sits at physical slot s ^ swz(t), the swizzle chosen per accumulator layout so that all three accesses are free of
+// bank conflicts:
+//   - the accumulator writes (Acc32: a half-wave = 32 tokens, one slot; Acc16: 16 tokens x 2 adjacent slots);
 //   - the token-major read-back (16 lanes: one token, 16 consecutive 16-byte pairs);
 //   - the vocab-major read-back by transposing reads (16 lanes: 16 tokens t & 31 in {8k + e}, one slot; the two
-//     16-lane groups of a 32-lane pass differ in bit 5 of t, which flips slot bit 2 and makes their sets disjoint).
+//     16-lane groups of a 32-lane pass differ in bit 5 of t, which moves their slots to disjoint sets).
 // The dense pass writes -g p / T x post' (x fp8 row scale) everywhere; after a barrier one thread per token writes the
 // label entry (launch_hit's value) over it, so no element is compared against the label.
-__device__ __forceinline__ int dz_swz(int t) { return (t & 31) ^ (((t >> 5) & 1) << 2); }
+template <class L> struct DzSwz;
+template <> struct DzSwz<Acc32> {
+  static __device__ __forceinline__ int at(int t) { return (t & 31) ^ (((t >> 5) & 1) << 2); }
+};
+template <> struct DzSwz<Acc16> {
+  static __device__ __forceinline__ int at(int t) { return (((t & 15) << 1) | ((t >> 4) & 1)) ^ (((t >> 5) & 1) << 3); }
+};
 
 typedef __attribute__((address_space(3))) short lds_short;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-template <typename P2, bool A_FP8, bool TANH, bool EDGE>
-__device__ __forceinline__ void dz_stage(const f32x16 (&acc)[4][4], const DzArgs &e, int64_t m0, int64_t n0,
-                                         int64_t nvalid, int wm, int wn, int lane, lds_char *tile) {
-  const int h = lane >> 5;
+template <class L, typename P2, bool A_FP8, bool TANH, bool EDGE>
+__device__ __forceinline__ void dz_stage(const typename L::V (&acc)[L::NI][L::NJ], const DzArgs &e, int64_t m0,
+                                         int64_t n0, int64_t nvalid, int wm, int wn, int lane, lds_char *tile) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tt = acc_col(wn, j, lane);
+  for (int j = 0; j < L::NJ; ++j) {
+    const int tt = L::col(wn, j, lane);
     float lse2 = 0.f, ngs = 0.f;  // -g / T (0 for tokens past the pass's count: dz 0, also in K-padding)
     if (tt < nvalid) {
       const int64_t r = e.row_off + n0 + tt;
       lse2 = e.lse[r] * OCTO_LOG2E;
       ngs = -(e.g[r] * e.gmul);
     }
-    const int sw = dz_swz(tt);
+    const int sw = DzSwz<L>::at(tt);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < L::NI; ++i)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int rl = wm * 128 + i * 32 + 8 * g4 + 4 * h;  // first of this lane's 4 vocab rows in the tile
+      for (int g4 = 0; g4 < L::NV / 4; ++g4) {
+        const int rl = L::row(wm, i, 4 * g4, lane);  // first of this lane's 4 vocab rows in the tile
         float d[4];
         float sc[4] = {1.f, 1.f, 1.f, 1.f};
         if constexpr (A_FP8) {
@@ -356,7 +368,7 @@ __device__ __forceinline__ void dz_stage(const f32x16 (&acc)[4][4], const DzArgs
   }
 }
 
-template <typename P2>
+template <class L, typename P2>
 __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0, int64_t nvalid, lds_char *tile) {
   typedef typename std::conditional<std::is_same<P2, bf16x2>::value, __bf16, _Float16>::type ET;
   const int t = threadIdx.x;
@@ -374,11 +386,11 @@ __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0
   __syncthreads();  // dense pass written
   if (yl >= 0) {
     const ET v = (ET)hv;
-    *(lds_short *)(tile + t * 512 + (((yl >> 2) ^ dz_swz(t)) << 3) + (yl & 3) * 2) = __builtin_bit_cast(short, v);
+    *(lds_short *)(tile + t * 512 + (((yl >> 2) ^ DzSwz<L>::at(t)) << 3) + (yl & 3) * 2) = __builtin_bit_cast(short, v);
   }
   __syncthreads();
   if (e.dzA)  // [token][vocab]: 512-byte rows
-    lds_tile_to_global(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return dz_swz(row); });
+    lds_tile_to_global(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return DzSwz<L>::at(row); });
   if (e.dzB) {  // [vocab][token] by transposing reads: a 16-lane group gives 4 vocab rows x 32 tokens, 8 per lane
     const int w = t >> 6, l = t & 63, G = l >> 4, i = l & 15;
     const int src = 8 * (i & 3) + (i >> 2);  // this lane's source token as a transposing-read source, 0..31
@@ -387,8 +399,8 @@ __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0
       const int u = p * 4 + w;              // unit: 4 vocab rows (quad q) x 128 tokens (half)
       const int q = u >> 1, tb = 128 * (u & 1) + 32 * G;
       const int t1 = tb + src, t2 = t1 + 4;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + t1 * 512 + ((q ^ dz_swz(t1)) << 3)));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + t2 * 512 + ((q ^ dz_swz(t2)) << 3)));
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + t1 * 512 + ((q ^ DzSwz<L>::at(t1)) << 3)));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + t2 * 512 + ((q ^ DzSwz<L>::at(t2)) << 3)));
       i32x4 v;
       v[0] = __builtin_bit_cast(i32x2, lo)[0];
       v[1] = __builtin_bit_cast(i32x2, lo)[1];
@@ -411,42 +423,48 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   const int64_t nvalid = dev_count(s.count, s.count_off + n0, s.N - n0);
   if (nvalid <= 0) return;
 
-  f32x16 acc[4][4];
-  if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
-  else if constexpr (R5) mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
-  else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
-
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
-  if constexpr (A_FP8) pre_transform<true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-  if constexpr (DT == OCTO_F32) {
-    dz_in_place<A_FP8, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
-    dz_store_direct(acc, e, m0, n0, wm, wn, lane);
+  typedef typename std::conditional<DT == OCTO_BF16, bf16x2, f16x2_t>::type P2;
+  if constexpr (R5) {
+    f32x4 acc[8][8];
+    mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
+    if (m0 + TM > e.V) dz_stage<Acc16, P2, false, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+    else dz_stage<Acc16, P2, false, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+    dz_write<Acc16, P2>(e, m0, n0, nvalid, smem);
   } else {
-    typedef typename std::conditional<DT == OCTO_BF16, bf16x2, f16x2_t>::type P2;
-    if (m0 + TM > e.V) dz_stage<P2, A_FP8, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-    else dz_stage<P2, A_FP8, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-    dz_write<P2>(e, m0, n0, nvalid, smem);
+    f32x16 acc[4][4];
+    if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
+    else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
+    if constexpr (A_FP8) pre_transform<Acc32, true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+    if constexpr (DT == OCTO_F32) {
+      dz_in_place<A_FP8, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
+      dz_store_direct(acc, e, m0, n0, wm, wn, lane);
+    } else {
+      if (m0 + TM > e.V) dz_stage<Acc32, P2, A_FP8, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+      else dz_stage<Acc32, P2, A_FP8, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+      dz_write<Acc32, P2>(e, m0, n0, nvalid, smem);
+    }
   }
 }
 
 // ---- epilogue: plain store -------------------------------------------------------------------
 
 // C = acc (+ addend, fp32, same strides) (+ C when ACC), rounded once to OT.
-template <typename OT, bool ACC, bool ADD, bool EDGE>
-__device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], OT *C, const float *addend, int64_t ldc,
-                                           int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int wm, int wn,
-                                           int lane) {
+template <class L, typename OT, bool ACC, bool ADD, bool EDGE>
+__device__ __forceinline__ void store_tile(const typename L::V (&acc)[L::NI][L::NJ], OT *C, const float *addend,
+                                           int64_t ldc, int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int wm,
+                                           int wn, int lane) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < L::NI; ++i)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int rr = acc_row(wm, i, v, lane);
+    for (int v = 0; v < L::NV; ++v) {
+      const int rr = L::row(wm, i, v, lane);
       if (EDGE && rr >= mvalid) continue;
       OT *crow = C + (m0 + rr) * ldc + n0;
       const float *arow = ADD ? addend + (m0 + rr) * ldc + n0 : nullptr;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int cc = acc_col(wn, j, lane);
+      for (int j = 0; j < L::NJ; ++j) {
+        const int cc = L::col(wn, j, lane);
         if (EDGE && cc >= nvalid) continue;
         float x = acc[i][j][v];
         if (ADD) x += arow[cc];
@@ -456,25 +474,26 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], OT *C, con
     }
 }
 
-template <typename OT, bool ACC, bool ADD>
-__device__ __forceinline__ void store_edge(const f32x16 (&acc)[4][4], OT *C, const float *addend, int64_t ldc,
-                                           int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int wm, int wn,
-                                           int lane) {
-  if (mvalid < TM || nvalid < TN) store_tile<OT, ACC, ADD, true>(acc, C, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
-  else store_tile<OT, ACC, ADD, false>(acc, C, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+template <class L, typename OT, bool ACC, bool ADD>
+__device__ __forceinline__ void store_edge(const typename L::V (&acc)[L::NI][L::NJ], OT *C, const float *addend,
+                                           int64_t ldc, int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int wm,
+                                           int wn, int lane) {
+  if (mvalid < TM || nvalid < TN) store_tile<L, OT, ACC, ADD, true>(acc, C, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+  else store_tile<L, OT, ACC, ADD, false>(acc, C, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
 }
 
-template <typename OT>
-__device__ __forceinline__ void store_any(const f32x16 (&acc)[4][4], void *C, const float *addend, int64_t ldc,
-                                          int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int accumulate) {
+template <class L, typename OT>
+__device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::NJ], void *C, const float *addend,
+                                          int64_t ldc, int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid,
+                                          int accumulate) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
   OT *c = (OT *)C;
   if (accumulate) {
-    if (addend) store_edge<OT, true, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
-    else store_edge<OT, true, false>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    if (addend) store_edge<L, OT, true, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    else store_edge<L, OT, true, false>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
   } else {
-    if (addend) store_edge<OT, false, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
-    else store_edge<OT, false, false>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    if (addend) store_edge<L, OT, false, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    else store_edge<L, OT, false, false>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
   }
 }
 
@@ -491,10 +510,15 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (s.count_on == 3) K_eff = round_up(dev_count(s.count, s.count_off, s.K), 64);
   if (mvalid <= 0 || nvalid <= 0) return;
 
-  f32x16 acc[4][4];
-  if constexpr (R5) mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, K_eff, smem, acc);
-  else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
-  store_any<typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
+  if constexpr (R5) {
+    f32x4 acc[8][8];
+    mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, K_eff, smem, acc);
+    store_any<Acc16, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
+  } else {
+    f32x16 acc[4][4];
+    mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
+    store_any<Acc32, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
+  }
 }
 
 // ---- host launchers ----------------------------------------------------------------------------
