@@ -4,15 +4,16 @@
 //
 // One workgroup = 256 threads = 4 wave64s computes a 256 x 256 tile of C; the waves sit 2 x 2 and
 // each owns a 128 x 128 sub-tile, i.e. all 256 accumulation registers of a wave: 8 x 8 blocks of
-// v_mfma_f32_16x16x32_{bf16,f16} in the 16-bit loop (Acc16), 4 x 4 blocks of v_mfma_f32_32x32x16_bf16 /
-// v_mfma_f32_32x32x2_f32 in the fp32 / fp8-weight loop (Acc32). Under the part's power limit the 16x16x32 form
+// v_mfma_f32_16x16x32_{bf16,f16} in the 16-bit loop (Acc16), 4 x 4 blocks of v_mfma_f32_32x32x2_f32 in the fp32
+// loop (Acc32). Under the part's power limit the 16x16x32 form
 // sustains 12% more bf16 FLOP/s than the 32x32x16 one on random operands (2.10 against 1.88 PFLOP/s, a
 // register-only loop on every SIMD), and each MFMA streams fewer accumulator bytes per FLOP.
 //
 // The mainloop feeds the MFMAs from LDS: the A and B K-slices go straight from global memory into a ring of
 // LDS stages by buffer_load_dwordx4 ... lds (no register hop), with the instruction order fixed in the source:
-// fragment reads a sub-step ahead of their MFMAs and the DMA issues spread between MFMAs. fp8 (e4m3) weights
-// travel to LDS as bytes and are widened to bf16 in registers, after the fragment read.
+// fragment reads a step ahead of their MFMAs and the DMA issues spread between MFMAs. fp8 (e4m3) weights are
+// widened to bf16 once per call (exactly: e4m3 has 3 mantissa bits) and run the 16-bit loop, their per-row scale
+// applied in the epilogue.
 //
 // Global loads are raw buffer loads: rows past the operand's end and K chunks past K read as zero
 // (voffset >= 2^31 is out of range), so partial tiles need no branches in the loop. Operand rows can
@@ -106,26 +107,19 @@ __device__ __forceinline__ const char *uniform_ptr(const char *p) {
   return (const char *)(((uint64_t)hi << 32) | lo);
 }
 
-// ---- 4-stage mainloop (fp32 operands, fp8 weights) --------------------------------------------------
+// ---- 4-stage mainloop (fp32 operands) ----------------------------------------------------------------
 //
-// K advances 64 bytes of the staged type per stage (32 bf16, 16 fp32). Each operand's stage slice (16 KB)
+// K advances 64 bytes per stage (16 fp32). Each operand's stage slice (16 KB)
 // is written straight into LDS by buffer_load_dwordx4 ... lds: a wave instruction moves 1 KB, lane i's 16 bytes
 // landing at the instruction's LDS base + 16 i, so the LDS layout is chosen by which global chunk each lane
 // fetches. DNSTAGE stages form a ring (A slice, then B slice, per stage). One bare s_barrier per stage (no
 // memory fence: the waits are explicit) separates "stage k + 1 landed in every wave" and "every wave has read
 // stage k" from the DMA that overwrites stage k's slot.
 //
-// An operand is streamed in one of two layouts:
-//   OpRows (K-contiguous rows, the NT case): a slice is 256 rows x 64 bytes. Chunk c of row r sits at
+// The operand (OpRows, K-contiguous rows): a slice is 256 rows x 64 bytes. Chunk c of row r sits at
 //     physical chunk c ^ ((r >> 2) & 3), so a 16-lane pass of fragment reads (rows r0..r0+15 of one logical
 //     chunk) covers all 64 banks once. A fragment is one ds_read_b128: lane l holds row l & 31 of a 32-row
 //     block, K chunk 2 sub + (l >> 5).
-//   OpRowsF8 (K-contiguous e4m3 rows): a slice is 256 rows x 32 bytes (the same 32 K values per stage). Chunk c
-//     (0, 1) of row r sits at physical chunk c ^ ((r >> 3) & 1), so 16 lanes reading one logical chunk of 16
-//     consecutive rows cover all 64 banks once. One ds_read_b128 per block and stage serves both sub-steps:
-//     lane l holds row l & 31, K values 16 (l >> 5) + 0..15, and sub-step s widens K values 16 (l >> 5) + 8 s
-//     + 0..7 to bf16. The contraction does not depend on the order of K inside a stage, so the B operand of an
-//     fp8 GEMM (OpRowsT<true>) reads the same permutation: chunk 2 (l >> 5) + s instead of 2 s + (l >> 5).
 constexpr int DKB = 64;                    // K bytes per stage
 constexpr int DSLICE = 256 * DKB;          // one operand's stage slice (16 KB)
 constexpr int DSTAGE = 2 * DSLICE;         // A + B bytes per stage
@@ -148,11 +142,9 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint32_t vo
 }
 
 // K-contiguous operand: instruction q of wave w fills slice rows (4 q + w) * 16 .. + 16; lane i takes row
-// + (i >> 2) and physical chunk i & 3. KPERM: the fragment order of an fp8 GEMM's B operand (see OpRowsF8).
-template <bool KPERM>
-struct OpRowsT {
+// + (i >> 2) and physical chunk i & 3.
+struct OpRows {
   static constexpr int NI = DIPW;     // DMA instructions per wave and stage
-  static constexpr bool FP8 = false;  // one byte per element, widened after the fragment read
   __amdgpu_buffer_rsrc_t rs;
   uint32_t off[DIPW], coff[DIPW];
   int fo[DNSUB];  // fragment byte offsets in the slice (block 0)
@@ -173,7 +165,7 @@ struct OpRowsT {
     else rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
 #pragma unroll
     for (int ks = 0; ks < DNSUB; ++ks) {
-      const int c = KPERM ? 2 * (lane >> 5) + ks : 2 * ks + (lane >> 5);
+      const int c = 2 * ks + (lane >> 5);
       fo[ks] = (wsub * 128 + (lane & 31)) * DKB + ((c ^ ((lane >> 2) & 3)) << 4);
     }
   }
@@ -187,55 +179,6 @@ struct OpRowsT {
     return *(const lds_i32x4 *)(slice + fo[sub] + blk * 32 * DKB);
   }
 };
-using OpRows = OpRowsT<false>;
-
-// K-contiguous e4m3 operand: instruction q of wave w fills slice rows (4 q + w) * 32 .. + 32; lane i takes row
-// + (i >> 1) and physical chunk i & 1. Rows must hold whole 16-byte chunks of K (K a multiple of 16).
-struct OpRowsF8 {
-  static constexpr int NI = 2;
-  static constexpr bool FP8 = true;
-  static constexpr int RB = DKB / 2;  // bytes per slice row
-  __amdgpu_buffer_rsrc_t rs;
-  uint32_t off[NI], coff[NI];
-  int fo;  // fragment byte offset in the slice (block 0)
-
-  __device__ __forceinline__ void init(const Operand &op, int64_t row0, int wsub, uint32_t /*krows*/) {
-    const int w = threadIdx.x >> 6, i = threadIdx.x & 63, lane = i;
-    const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
-#pragma unroll
-    for (int q = 0; q < NI; ++q) {
-      const int r = (4 * q + w) * 32 + (i >> 1);
-      coff[q] = (uint32_t)(((i & 1) ^ ((r >> 3) & 1)) << 4);
-      uint32_t rowoff;
-      if (r < valid) rowoff = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
-      else rowoff = 0x80000000u;
-      off[q] = rowoff + coff[q];
-    }
-    if (op.map) rs = make_rsrc(uniform_ptr(op.base), op.extent);
-    else rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
-    fo = (wsub * 128 + (lane & 31)) * RB + (((lane >> 5) ^ ((lane >> 3) & 1)) << 4);
-  }
-  // kbytes: K bytes per row (one per element)
-  __device__ __forceinline__ void dma(int k, int q, uint32_t kbytes, lds_char *slice) const {
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t kb = (uint32_t)k * RB;
-    lds_dma16(rs, (kb + coff[q] < kbytes) ? off[q] + kb : 0x80000000u, slice + (4 * q + w) * 1024);
-  }
-  // 16 e4m3 values of row l & 31 of block blk, both sub-steps
-  __device__ __forceinline__ i32x4 frag(const lds_char *slice, int /*sub*/, int blk) const {
-    return *(const lds_i32x4 *)(slice + fo + blk * 32 * RB);
-  }
-  // sub-step s's 8 values as bf16 (exact: e4m3 has 3 mantissa bits and a narrower exponent range)
-  static __device__ __forceinline__ i32x4 widen(const i32x4 &raw, int s) {
-    i32x4 o;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      o[2 * h] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[2 * s + h], 1.0f, false));
-      o[2 * h + 1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[2 * s + h], 1.0f, true));
-    }
-    return o;
-  }
-};
 
 // Instruction order is fixed in the source: a scheduling fence after every MFMA / load keeps the fragment
 // reads of the next sub-step early (so register allocation cannot fold them onto fragments still in use)
@@ -247,13 +190,11 @@ struct OpRowsF8 {
 //
 // Stage j's A slice is issued right after the barrier that frees its slot (in iteration j - DNSTAGE), its B slice
 // under the first sub-step of the next iteration (into the slot stage j - DNSTAGE left), so the DMA instructions
-// of a stage are spread over two sub-steps. An fp8 A operand reads its fragments once per stage (under sub-step 1
-// of the previous stage) and widens them under sub-step 0.
+// of a stage are spread over two sub-steps.
 template <int DT, typename OA, typename OB>
 __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B, int64_t m0, int64_t n0, int64_t K_eff,
                                              lds_char *smem, f32x16 (&acc)[4][4]) {
   static_assert(DNSTAGE >= 3, "ring depth");
-  static_assert(!OB::FP8 && (!OA::FP8 || DT == OCTO_BF16), "fp8: A operand, bf16 MFMAs");
   constexpr int NA = OA::NI, NB = OB::NI, NPS = NA + NB;  // DMA instructions per wave and stage
   constexpr int SPA = 8 / NA, SPB = 8 / NB;                // MFMAs between two DMA issues
   static_assert(NPS * DNSTAGE <= 63, "vmcnt range");
@@ -268,7 +209,6 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
 
   constexpr int ebytes = (DT == OCTO_F32) ? 4 : 2;
   const uint32_t kbytes = (uint32_t)(K_eff * ebytes);
-  const uint32_t kbytes_a = OA::FP8 ? (uint32_t)K_eff : kbytes;
   const int nk = (int)((kbytes + DKB - 1) / DKB);
   if (nk == 0) return;
 
@@ -280,7 +220,7 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
 #pragma unroll
   for (int st = 0; st < DNSTAGE; ++st) {
 #pragma unroll
-    for (int q = 0; q < NA; ++q) opa.dma(st, q, kbytes_a, smem + st * DSTAGE);
+    for (int q = 0; q < NA; ++q) opa.dma(st, q, kbytes, smem + st * DSTAGE);
     if (st < DNSTAGE - 1) {
 #pragma unroll
       for (int q = 0; q < NB; ++q) opb.dma(st, q, kbytes, smem + st * DSTAGE + DSLICE);
@@ -289,11 +229,10 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(NPS * (DNSTAGE - 2) + NA));  // stage 0 landed
   __builtin_amdgcn_s_barrier();
 
-  i32x4 fa[2][4], fb[2][4], ra[4];  // ra: an fp8 A operand's raw fragments (both sub-steps)
+  i32x4 fa[2][4], fb[2][4];
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    if constexpr (OA::FP8) ra[b] = opa.frag(smem, 0, b);
-    else fa[0][b] = opa.frag(smem, 0, b);
+    fa[0][b] = opa.frag(smem, 0, b);
     fb[0][b] = opb.frag(smem + DSLICE, 0, b);
   }
   int slot = 0;                 // k % DNSTAGE
@@ -303,22 +242,13 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
     const lds_char *cur = smem + slot * DSTAGE;
     __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // this sub-step's fragments (read under the previous one) are in
     OCTO_FENCE();
-    if constexpr (OA::FP8) {
-      fa[0][0] = OA::widen(ra[0], 0);
-      OCTO_FENCE();
-    }
-    // sub-step 0: read sub-step 1's fragments under the first 8 MFMAs (fp8 A: widen them instead); the B slice
-    // of stage k + DNSTAGE - 1 (into the slot stage k - 1 left) under the last 8
+    // sub-step 0: read sub-step 1's fragments under the first 8 MFMAs; the B slice of stage k + DNSTAGE - 1 (into
+    // the slot stage k - 1 left) under the last 8
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       Mfma<DT>::run(fa[0][q >> 2], fb[0][q & 3], acc[q >> 2][q & 3]);
       OCTO_FENCE();
-      if constexpr (OA::FP8) {
-        if ((q & 3) == 0 && q < 12) fa[0][(q >> 2) + 1] = OA::widen(ra[(q >> 2) + 1], 0);
-        if ((q & 3) == 2) fa[1][q >> 2] = OA::widen(ra[q >> 2], 1);
-        if (q < 4) fb[1][q] = opb.frag(cur + DSLICE, 1, q);
-        OCTO_FENCE();
-      } else if (q < 8) {
+      if (q < 8) {
         if (q < 4) fa[1][q] = opa.frag(cur, 1, q);
         else fb[1][q - 4] = opb.frag(cur + DSLICE, 1, q - 4);
         OCTO_FENCE();
@@ -341,16 +271,12 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
       Mfma<DT>::run(fa[1][q >> 2], fb[1][q & 3], acc[q >> 2][q & 3]);
       OCTO_FENCE();
       if (q < 8) {
-        if (q < 4) {
-          if constexpr (OA::FP8) ra[q] = opa.frag(nxt, 0, q);
-          else fa[0][q] = opa.frag(nxt, 0, q);
-        } else {
-          fb[0][q - 4] = opb.frag(nxt + DSLICE, 0, q - 4);
-        }
+        if (q < 4) fa[0][q] = opa.frag(nxt, 0, q);
+        else fb[0][q - 4] = opb.frag(nxt + DSLICE, 0, q - 4);
         OCTO_FENCE();
       }
       if (q >= 8 && (q - 8) % SPA == SPA - 1) {
-        opa.dma(k + DNSTAGE, (q - 8) / SPA, kbytes_a, refill);
+        opa.dma(k + DNSTAGE, (q - 8) / SPA, kbytes, refill);
         OCTO_FENCE();
       }
     }
@@ -368,13 +294,12 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
 // twice, once per half, which doubles the L1 -> L2 requests and stalls the address unit on the L1.
 //
 // A stage is two 32 KB slices (A, B). The LDS holds five slices, 2.5 stages: stage j's A slice sits in slot
-// 2 j mod 5, its B slice in slot 2 j + 1 mod 5. One s_barrier per stage, B_k, placed before the last of stage
-// k's four sub-steps, means "every wave has read stage k" (its last fragments are read under sub-step 2) and
-// "stage k + 1 has landed in every wave". It frees stage k's two slots; stage k + 2's B slice goes into the
-// first (issued under sub-step 3), and stage k + 3's A slice into the second (issued under sub-steps 0 and 1 of
-// stage k + 1, i.e. under the iteration that issues all of stage k + 3... see the loop). So iteration k issues
-// stage k + 2 whole: its A slice under sub-steps 0 and 1 (slot freed at B_(k-1)), its B slice under sub-step 3
-// (slot freed at B_k). At B_k only stage k + 2's A slice may still be in flight: vmcnt(8).
+// 2 j mod 5, its B slice in slot 2 j + 1 mod 5. One s_barrier per stage, B_k, placed between stage k's two K-steps,
+// means "every wave has read stage k" (its last fragments are read under its first K-step) and "stage k + 1 has
+// landed in every wave". It frees stage k's two slots: slot 2 k (mod 5) takes stage k + 2's B slice, slot 2 k + 1
+// stage k + 3's A slice. So iteration k issues stage k + 2 whole: its A slice under K-step 0 (into the slot freed at
+// B_(k-1)), its B slice under K-step 1 (the slot freed at B_k). At B_k only stage k + 2's A slice may still be in
+// flight: vmcnt(8).
 //
 //   OpRows128 (K-contiguous rows): a slice is 256 rows x 128 bytes. Chunk c (0..7) of row r sits at physical
 //     chunk c ^ ((r >> 1) & 7), so a 16-lane pass of fragment reads (rows r0..r0+15, r0 a multiple of 16, of
@@ -391,7 +316,6 @@ static_assert(SMEM_RING5 <= 160 * 1024, "LDS budget");
 
 struct OpRows128 {
   static constexpr int NI = ENI;
-  static constexpr bool FP8 = false;
   __amdgpu_buffer_rsrc_t rs;
   uint32_t off[ENI];
   uint32_t coff;
@@ -417,17 +341,6 @@ struct OpRows128 {
     const int row = wsub * 128 + (lane & 15);
     fo = row * EKB + ((((lane >> 4) ^ ((lane >> 1) & 7))) << 4);
   }
-  // A plain operand (no row map) whose first `valid` rows from row0 exist: no memory reads, so a persistent loop can
-  // re-point the DMA at its next tile without waiting on loads.
-  __device__ __forceinline__ void init_plain(const Operand &op, int64_t row0, int64_t valid) {
-    const int w = threadIdx.x >> 6, i = threadIdx.x & 63;
-#pragma unroll
-    for (int q = 0; q < ENI; ++q) {
-      const int r = (4 * q + w) * 8 + (i >> 3);
-      off[q] = (r < valid ? (uint32_t)(r * op.ld) : 0x80000000u) + coff;
-    }
-    rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
-  }
   // K chunks at or past kbytes (bytes per row) read zero
   __device__ __forceinline__ void dma(int k, int q, uint32_t kbytes, lds_char *slice) const {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -440,8 +353,9 @@ struct OpRows128 {
   }
 };
 
-// The 16-bit GEMMs (bf16 / f16 operands, no fp8 widening) run the ring loop; fp32 and fp8 the 4-stage one.
-__host__ __device__ constexpr bool ring5_ok(int dt, bool fp8) { return (dt == OCTO_BF16 || dt == OCTO_F16) && !fp8; }
+// The 16-bit GEMMs (bf16 / f16 operands; fp8 weights are widened to bf16 before the GEMM) run the ring loop, fp32
+// the 4-stage one.
+__host__ __device__ constexpr bool ring5_ok(int dt) { return dt == OCTO_BF16 || dt == OCTO_F16; }
 
 template <int DT> struct Mfma16;
 template <> struct Mfma16<OCTO_BF16> {
@@ -567,119 +481,6 @@ __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &
   __builtin_amdgcn_s_barrier();
 }
 
-// ---- persistent tile stream (short-K GEMMs: the forward and the dz recompute, K = d) --------------------
-//
-// One workgroup per CU. Workgroup b walks the tiles of the one-shot grid b, b + G, b + 2 G, ... (G = grid size, a
-// multiple of 8, so every tile it visits belongs to its own XCD's share, as in tile_of), skipping tiles with no
-// valid row. The K-stages of its tiles form one continuous ring-5 stream: the stage two ahead is always in flight,
-// across tile boundaries, so a tile's first stages land while the previous tile finishes and its epilogue runs,
-// and no workgroup launch or pipeline fill sits between tiles. Both operands are plain (no row map) and the row
-// count is read once, so re-pointing the DMA at the next tile reads no memory inside the loop. Past the last tile
-// the DMA keeps running with every row out of range: it writes zeros into slots nobody reads again, and every
-// stage keeps the same instruction stream and the same vmcnt accounting.
-//
-// After a tile's last stage, epi(acc, mt, nt, nvalid, red) runs (nvalid: the tile's valid N rows); `red` is the
-// one 32 KB ring slot that is free at that point (the last stage's B slot: the stream's next DMA into it is issued
-// after the epilogue). A barrier follows the epilogue, so every wave is done with `red` before that DMA.
-__device__ __forceinline__ bool tile_at32(int mtiles, int ntiles, int group_m, int vb, int &mt, int &nt) {
-  const int x = vb & 7;
-  const int k = vb >> 3;
-  const int mx = (mtiles - x + 7) >> 3;
-  if (k >= mx * ntiles) return false;
-  const int span = group_m * ntiles;
-  const int gid = k / span;
-  const int first = gid * group_m;
-  const int gsize = (mx - first) < group_m ? (mx - first) : group_m;
-  const int local = k - gid * span;
-  mt = x + 8 * (first + local % gsize);
-  nt = local / gsize;
-  return true;
-}
-
-// s.count (if any) bounds N (count_on == 2). Requires K > 64 (two or more stages per tile).
-template <int DT, typename Epi>
-__device__ __forceinline__ void persistent_ring5(const Operand &A, const Operand &B, const GemmShape &s, lds_char *smem,
-                                                 Epi &&epi) {
-  static_assert(DT == OCTO_BF16 || DT == OCTO_F16, "16-bit operands");
-  const int w = threadIdx.x >> 6;
-  const int wm = w >> 1, wn = w & 1;
-  const int64_t ntot = dev_count(s.count, s.count_off, s.N);  // valid N rows, read once
-  const int mtiles = s.mtiles, ntiles = (int)cdiv(ntot, TN), gm = s.group_m;
-  const int nvb = (int)tile_grid(mtiles, ntiles);
-  const int G = (int)gridDim.x;
-  const uint32_t kbytes = (uint32_t)(s.K * 2);
-  const int nk = (int)((kbytes + EKB - 1) / EKB);
-
-  int cvb = (int)blockIdx.x, cmt = 0, cnt = 0;  // compute tile
-  while (cvb < nvb && !tile_at32(mtiles, ntiles, gm, cvb, cmt, cnt)) cvb += G;
-  if (cvb >= nvb) return;
-
-  OpRows128 opa, opb;
-  opa.init(A, (int64_t)cmt * TM, wm, (uint32_t)s.K);  // swizzle and fragment offsets; rows re-pointed per tile
-  opb.init(B, (int64_t)cnt * TN, wn, (uint32_t)s.K);
-  int fvb = cvb, fk = 2;  // fetch cursor: tile, next stage
-  int ahead = 0;          // tiles the fetch cursor is past the compute tile
-  auto point = [&](int mt, int nt, bool live) {
-    const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
-    opa.init_plain(A, m0, live ? A.rows - m0 : 0);
-    opb.init_plain(B, n0, live ? ntot - n0 : 0);
-  };
-  auto advance = [&]() {  // after a stage of the fetch tile was issued
-    if (fk < nk || fvb >= nvb) return;
-    int mt = 0, nt = 0, v = fvb + G;
-    while (v < nvb && !tile_at32(mtiles, ntiles, gm, v, mt, nt)) v += G;
-    fvb = v;
-    fk = 0;
-    if (v < nvb) ++ahead;
-    point(mt, nt, v < nvb);
-  };
-  point(cmt, cnt, true);
-
-#pragma unroll
-  for (int q = 0; q < ENI; ++q) opa.dma(0, q, kbytes, smem);
-#pragma unroll
-  for (int q = 0; q < ENI; ++q) opb.dma(0, q, kbytes, smem + ESLICE);
-#pragma unroll
-  for (int q = 0; q < ENI; ++q) opa.dma(1, q, kbytes, smem + 2 * ESLICE);
-#pragma unroll
-  for (int q = 0; q < ENI; ++q) opb.dma(1, q, kbytes, smem + 3 * ESLICE);
-  advance();
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * ENI));  // stage 0 landed
-  __builtin_amdgcn_s_barrier();
-
-  f32x4 acc[8][8];
-  i32x4 fa[2][8], fb[2][8];
-#pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    fa[0][b] = opa.frag(smem, 0, b);
-    fb[0][b] = opb.frag(smem + ESLICE, 0, b);
-  }
-  int sa = 0;
-  while (true) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
-    for (int k = 0; k < nk; ++k) {
-      ring5_stage<DT, OpRows128, OpRows128, true, true>(opa, opb, fk, sa, kbytes, smem, fa, fb, acc);
-      ++fk;
-      advance();
-      sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
-    }
-    const int64_t n0 = (int64_t)cnt * TN;
-    epi(acc, cmt, cnt, (ntot - n0) < TN ? (ntot - n0) : (int64_t)TN, smem + (sa == 0 ? ENSLOT - 1 : sa - 1) * ESLICE);
-    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
-    __builtin_amdgcn_s_barrier();  // every wave is done with the epilogue's slot
-    if (ahead == 0) break;
-    --ahead;
-    cvb += G;
-    while (!tile_at32(mtiles, ntiles, gm, cvb, cmt, cnt)) cvb += G;
-  }
-  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
-}
-
 // ---- accumulator layouts of a wave's 128 x 128 sub-tile --------------------------------------------
 //
 // Row (M) and column (N), relative to the tile origin, of element v of block (i, j) of wave (wm, wn). In both
@@ -713,7 +514,7 @@ struct Acc16 {  // 8 x 8 blocks of v_mfma_f32_16x16x*: column l & 15, rows 4 (l 
   }
   static __device__ __forceinline__ bool col_lane(int lane) { return lane < 16; }
 };
-// The fp32 / fp8-weight paths' layout.
+// The fp32 path's layout.
 __device__ __forceinline__ int acc_row(int wm, int i, int v, int lane) { return Acc32::row(wm, i, v, lane); }
 __device__ __forceinline__ int acc_col(int wn, int j, int lane) { return Acc32::col(wn, j, lane); }
 

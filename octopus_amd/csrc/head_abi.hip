@@ -83,19 +83,20 @@ int staged_dtype(int w_dtype) { return w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_d
 
 struct FwdLayout {
   int64_t mtiles;
-  size_t part, rows, total;
+  size_t part, wide, total;
 };
-// part: (m, S, U) per (row, vocab tile). rows: the compacted hidden rows [n_max, d] when the forward GEMM is the
-// persistent one (16-bit operands), which takes plain operands.
+// part: (m, S, U) per (row, vocab tile). wide: fp8 weights widened to bf16 [V, d].
 FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
   FwdLayout L;
   L.mtiles = cdiv(V, TM);
   L.part = 0;
-  L.rows = align_up((size_t)n_max * L.mtiles * sizeof(f32x4));
-  L.total = L.rows;
-  if (ring5_ok(w_dtype, false)) L.total += align_up((size_t)n_max * d * elem_bytes(w_dtype));
+  size_t off = align_up((size_t)n_max * L.mtiles * sizeof(f32x4));
+  L.wide = off;
+  if (w_dtype == OCTO_FP8E4M3) off += align_up((size_t)V * d * 2);
+  L.total = off;
   return L;
 }
+
 
 // The backward stages every gradient GEMM operand K-contiguous, so each row fetch of the GEMM mainloop is one
 // whole cache line: W^T [d, V_pad] for grad_h = dz . W, the pass's hidden rows transposed to h^T [d, P] for
@@ -103,7 +104,7 @@ FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
 struct BwdLayout {
   int64_t P, V_pad, passes;
   int esz;
-  size_t wt, ht, dza, dzb, hit, gacc, total;
+  size_t wt, ht, dza, dzb, hit, wide, gacc, total;
 };
 BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw) {
   BwdLayout L;
@@ -122,6 +123,8 @@ BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, boo
   if (need_gw) off += align_up((size_t)L.V_pad * L.P * L.esz);
   L.hit = off;  // dz at each row's label [P] fp32 (16-bit dz epilogue)
   if (L.esz == 2) off += align_up((size_t)L.P * sizeof(float));
+  L.wide = off;  // fp8 weights widened to bf16 [V, d] (the dz recompute's operand)
+  if (w_dtype == OCTO_FP8E4M3) off += align_up((size_t)V * d * 2);
   L.gacc = off;  // fp32 grad_W partial sums across passes, for a 16-bit grad_W
   if (need_gw && L.passes > 1 && w_dtype != OCTO_F32) off += align_up((size_t)V * d * sizeof(float));
   L.total = off;
@@ -195,6 +198,16 @@ Operand weight_operand(const void *w, int64_t ldw, const Common &cm, int V) {
   A.count = nullptr;
   A.count_off = 0;
   A.extent = 0;
+  return A;
+}
+
+// The GEMMs' weight operand: W as stored, or for fp8 weights its bf16 widening in the workspace.
+Operand gemm_weight(const void *w, int64_t ldw, const Common &cm, int V, int d, void *wide, hipStream_t st, int &rc) {
+  rc = OCTO_OK;
+  if (!cm.fp8) return weight_operand(w, ldw, cm, V);
+  rc = launch_widen_fp8(w, ldw, V, d, wide, st);
+  Operand A = weight_operand(wide, d, cm, V);
+  A.ld = (int64_t)d * 2;
   return A;
 }
 
@@ -309,15 +322,9 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     return octo_fail(OCTO_EWORKSPACE, "head_fwd: workspace %zu < %zu bytes", ws_bytes, L.total);
   hipStream_t st = (hipStream_t)stream;
 
-  const Operand A = weight_operand(w, ldw, cm, V);
-  Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
-  if (idx && ring5_ok(cm.dt, cm.fp8)) {  // the persistent GEMM reads the compacted rows as one block
-    void *rows = (char *)ws + L.rows;
-    rc = launch_gather_rows(h, h_rows, ldh * cm.hesz, idx, count, n_max, (int64_t)d * cm.hesz, rows,
-                            (int64_t)d * cm.hesz, st);
-    if (rc) return rc;
-    B = plain_operand(rows, (int64_t)d * cm.hesz, n_max, count, 0);
-  }
+  const Operand A = gemm_weight(w, ldw, cm, V, d, (char *)ws + L.wide, st, rc);
+  if (rc) return rc;
+  const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
   const GemmShape s = shape(V, n_max, d, kGroupM, 2, count, 0);
   StatsArgs e;
   e.part = (f32x4 *)((char *)ws + L.part);
@@ -398,7 +405,8 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     rc = launch_transpose(w, ldw, w_dtype, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt, L.V_pad, cm.dt, st);
     if (rc) return rc;
   }
-  const Operand Aw = weight_operand(w, ldw, cm, V);
+  const Operand Aw = gemm_weight(w, ldw, cm, V, d, wsb + L.wide, st, rc);
+  if (rc) return rc;
 
   for (int64_t p = 0; p < L.passes; ++p) {
     const int64_t r0 = p * L.P;

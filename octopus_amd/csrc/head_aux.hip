@@ -2,7 +2,7 @@
 //   merge          per-row merge of the vocab-tile softmax partials + target logit -> logp, entropy, lse
 //   hit            per-row dz value at the label (the backward's dz epilogue writes it over the dense entry)
 //   transpose      K-contiguous copies (W^T, gathered h^T) feeding the backward's gradient GEMMs
-//   gather_rows    the compacted hidden rows as one contiguous block (the persistent forward GEMM's operand)
+//   widen_fp8      e4m3 weights to bf16 (exact), the GEMMs' operand for fp8 weights
 //   compact_rows   masked-row compaction, ascending (torch.nonzero order), count left on the device
 //   columns fwd/bwd  _head_columns over materialised logits
 //   pairs expand/grad, rows scatter, gather   the index plumbing of tree_head_output / _scored_rows
@@ -153,35 +153,33 @@ int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float
   return OCTO_OK;
 }
 
-// ---- row gather --------------------------------------------------------------------------------------
-// dst[r] = src[map[r]] for the rows below the device count (one workgroup per row, 16-byte chunks); a map entry
-// outside [0, src_rows) gives a zero row; rows at or past the count are left untouched (the GEMMs that read dst
-// treat them as absent).
-__global__ __launch_bounds__(256) void gather_rows_kernel(const char *src, int64_t src_rows, int64_t ld_src,
-                                                          const int64_t *map, const int32_t *count, int64_t rows,
-                                                          int64_t row_bytes, char *dst, int64_t ld_dst) {
-  const int64_t r = blockIdx.x;
-  if (r >= dev_count(count, 0, rows)) return;
-  const int64_t p = map[r];
-  const bool ok = p >= 0 && p < src_rows;
-  const char *s = src + (ok ? p : 0) * ld_src;
-  char *d = dst + r * ld_dst;
-  for (int64_t c = (int64_t)threadIdx.x * 16; c < row_bytes; c += 256 * 16) {
-    i32x4 v = {0, 0, 0, 0};
-    if (ok) v = *(const i32x4 *)(s + c);
-    *(i32x4 *)(d + c) = v;
+// ---- fp8 weight widening -----------------------------------------------------------------------------
+// dst[V, d] bf16 = the e4m3 weight values, exactly (no row scale: the GEMM epilogues apply it in fp32). One thread per
+// 16 weights.
+__global__ __launch_bounds__(256) void widen_fp8_kernel(const uint8_t *w, int64_t ldw, int64_t V, int64_t chunks,
+                                                        char *dst) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= V * chunks) return;
+  const int64_t r = i / chunks, c = i - r * chunks;
+  const i32x4 raw = *(const i32x4 *)(w + r * ldw + c * 16);
+  i32x4 o[2];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    o[h >> 1][2 * (h & 1)] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[h], 1.0f, false));
+    o[h >> 1][2 * (h & 1) + 1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw[h], 1.0f, true));
   }
+  i32x4 *d = (i32x4 *)(dst + (r * chunks + c) * 32);
+  d[0] = o[0];
+  d[1] = o[1];
 }
 
-int launch_gather_rows(const void *src, int64_t src_rows, int64_t ld_src_bytes, const int64_t *map,
-                       const int32_t *count, int64_t rows, int64_t row_bytes, void *dst, int64_t ld_dst_bytes,
-                       hipStream_t st) {
-  if (rows == 0 || row_bytes == 0) return OCTO_OK;
-  if (row_bytes % 16 || ld_src_bytes % 16 || ld_dst_bytes % 16)
-    return octo_fail(OCTO_EINVAL, "gather_rows: rows must be whole 16-byte chunks");
-  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)rows), dim3(256), 0, st, (const char *)src, src_rows,
-                     ld_src_bytes, map, count, rows, row_bytes, (char *)dst, ld_dst_bytes);
-  OCTO_CHECK_LAUNCH("gather_rows");
+int launch_widen_fp8(const void *w, int64_t ldw, int64_t V, int d, void *dst, hipStream_t st) {
+  if (V == 0) return OCTO_OK;
+  if (d % 16 || ldw % 16) return octo_fail(OCTO_EINVAL, "widen_fp8: rows must be whole 16-byte chunks");
+  const int64_t chunks = d / 16;
+  hipLaunchKernelGGL(widen_fp8_kernel, dim3((unsigned)cdiv(V * chunks, 256)), dim3(256), 0, st, (const uint8_t *)w,
+                     ldw, V, chunks, (char *)dst);
+  OCTO_CHECK_LAUNCH("widen_fp8");
   return OCTO_OK;
 }
 

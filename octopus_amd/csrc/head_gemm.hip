@@ -101,7 +101,7 @@ __device__ __forceinline__ void stats_cols(typename L::V (&acc)[L::NI][L::NJ], i
 
 template <int DT, bool A_FP8, bool TANH>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stats_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
-  constexpr bool R5 = ring5_ok(DT, A_FP8);
+  constexpr bool R5 = ring5_ok(DT);
   __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
@@ -115,14 +115,13 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if constexpr (R5) {
     f32x4 acc[8][8];
     mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
-    pre_transform<Acc16, false, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+    pre_transform<Acc16, A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
     if (m0 + TM > e.V) stats_cols<Acc16, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
     else stats_cols<Acc16, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
   } else {
     f32x16 acc[4][4];
-    if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
-    else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
-    pre_transform<Acc32, A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+    mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
+    pre_transform<Acc32, false, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
     if (m0 + TM > e.V) stats_cols<Acc32, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
     else stats_cols<Acc32, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
   }
@@ -136,34 +135,6 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
     o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
     e.part[(n0 + t) * e.mtiles + mt] = o;
   }
-}
-
-// Persistent form (16-bit operands, both plain): the tiles' K-stages run as one stream (persistent_ring5) and the
-// epilogue reduces through the free ring slot with bare barriers (no memory fence, so the next tile's DMA keeps
-// flowing underneath).
-template <int DT, bool TANH>
-__global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stats_persistent_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
-  __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
-  lds_char *smem = (lds_char *)smem_;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
-  persistent_ring5<DT>(A, B, s, smem, [&](f32x4 (&acc)[8][8], int mt, int nt, int64_t nvalid, lds_char *slot) {
-    const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
-    pre_transform<Acc16, false, TANH>(acc, m0, wm, lane, nullptr, e.V, e.pre);
-    lds_f32x4 *red = (lds_f32x4 *)slot;
-    if (m0 + TM > e.V) stats_cols<Acc16, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
-    else stats_cols<Acc16, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
-    __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);
-    __builtin_amdgcn_s_barrier();
-    const int t = threadIdx.x;
-    if (t < nvalid) {
-      const f32x4 a = red[t], b = red[256 + t];
-      Stat3 sa{a[0], a[1], a[2]}, sb{b[0], b[1], b[2]};
-      Stat3 r = stat_merge(sa, sb);
-      f32x4 o;
-      o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
-      e.part[(n0 + t) * e.mtiles + mt] = o;
-    }
-  });
 }
 
 // ---- epilogue: dz recompute ------------------------------------------------------------------
@@ -414,7 +385,7 @@ __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0
 
 template <int DT, bool A_FP8, bool TANH>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_dz_kernel(Operand A, Operand B, GemmShape s, DzArgs e) {
-  constexpr bool R5 = ring5_ok(DT, A_FP8);
+  constexpr bool R5 = ring5_ok(DT);
   __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
@@ -428,22 +399,15 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if constexpr (R5) {
     f32x4 acc[8][8];
     mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
-    if (m0 + TM > e.V) dz_stage<Acc16, P2, false, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-    else dz_stage<Acc16, P2, false, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+    if constexpr (A_FP8) pre_transform<Acc16, true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+    if (m0 + TM > e.V) dz_stage<Acc16, P2, A_FP8, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+    else dz_stage<Acc16, P2, A_FP8, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
     dz_write<Acc16, P2>(e, m0, n0, nvalid, smem);
-  } else {
+  } else {  // fp32
     f32x16 acc[4][4];
-    if constexpr (A_FP8) mainloop_dma<DT, OpRowsF8, OpRowsT<true>>(A, B, m0, n0, s.K, smem, acc);
-    else mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
-    if constexpr (A_FP8) pre_transform<Acc32, true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-    if constexpr (DT == OCTO_F32) {
-      dz_in_place<A_FP8, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
-      dz_store_direct(acc, e, m0, n0, wm, wn, lane);
-    } else {
-      if (m0 + TM > e.V) dz_stage<Acc32, P2, A_FP8, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-      else dz_stage<Acc32, P2, A_FP8, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-      dz_write<Acc32, P2>(e, m0, n0, nvalid, smem);
-    }
+    mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
+    dz_in_place<false, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
+    dz_store_direct(acc, e, m0, n0, wm, wn, lane);
   }
 }
 
@@ -499,7 +463,7 @@ __device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::N
 
 template <int DT, int OT>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
-  constexpr bool R5 = ring5_ok(DT, false);
+  constexpr bool R5 = ring5_ok(DT);
   __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
@@ -525,40 +489,13 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
 static inline dim3 grid_of(const GemmShape &s) { return dim3((unsigned)tile_grid(s.mtiles, s.ntiles)); }
 
-// Workgroups of a persistent launch: one per CU, a multiple of 8 (the tile walk keeps each on its own XCD), at most
-// the one-shot grid.
-static unsigned persistent_grid(const GemmShape &s) {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (!cus[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 8;
-    cus[dev] = n / 8 * 8;
-  }
-  const int64_t one_shot = tile_grid(s.mtiles, s.ntiles);
-  return (unsigned)(one_shot < cus[dev] ? one_shot : cus[dev]);
-}
-
-// The persistent forward takes 16-bit plain operands with at least two K-stages.
-static bool persistent_ok(int dt, bool fp8, const Operand &A, const Operand &B, const GemmShape &s) {
-  return ring5_ok(dt, fp8) && !A.map && !B.map && s.K > EKB / 2 && s.count_on != 1 && s.count_on != 3;
-}
-
 template <int DT, bool F8, bool TH>
 static int go_stats(const Operand &A, const Operand &B, const GemmShape &s, const StatsArgs &e, hipStream_t st) {
-  if constexpr (ring5_ok(DT, F8)) {
-    if (persistent_ok(DT, F8, A, B, s)) {
-      hipLaunchKernelGGL((gemm_stats_persistent_kernel<DT, TH>), dim3(persistent_grid(s)), dim3(NTHREADS), 0, st, A,
-                         B, s, e);
-      OCTO_CHECK_LAUNCH("gemm_stats");
-      return OCTO_OK;
-    }
-  }
   hipLaunchKernelGGL((gemm_stats_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
   OCTO_CHECK_LAUNCH("gemm_stats");
   return OCTO_OK;
 }
+
 template <int DT, bool F8, bool TH>
 static int go_dz(const Operand &A, const Operand &B, const GemmShape &s, const DzArgs &e, hipStream_t st) {
   hipLaunchKernelGGL((gemm_dz_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);

@@ -102,9 +102,7 @@ int launch_merge(const MergeArgs &a, hipStream_t st);
 // Source row r is row map[r] (or r) of src; dst holds the staged MFMA type (bf16/f16/f32).
 // dst[r, c] = src row map[r] (or r), element c, for r < rows_pad, c < cols; rows r at or past the valid count read 0.
 // Same dtype on both sides (a byte copy of 16-bit or 32-bit elements).
-int launch_gather_rows(const void *src, int64_t src_rows, int64_t ld_src_bytes, const int64_t *map,
-                       const int32_t *count, int64_t rows, int64_t row_bytes, void *dst, int64_t ld_dst_bytes,
-                       hipStream_t st);
+int launch_widen_fp8(const void *w, int64_t ldw, int64_t V, int d, void *dst, hipStream_t st);
 int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *src_scale,
                      const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
                      int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st);
