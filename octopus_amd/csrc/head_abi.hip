@@ -400,13 +400,15 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
   const int esz = L.esz;
   const bool gw_staged = need_gw && L.passes > 1 && gw_dtype != OCTO_F32;  // fp32 partials in gacc
 
-  // W^T [d, V_pad] in the staged type (fp8 weights: their exact bf16 values; the row scale is in dz)
-  if (need_gh) {
-    rc = launch_transpose(w, ldw, w_dtype, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt, L.V_pad, cm.dt, st);
-    if (rc) return rc;
-  }
   const Operand Aw = gemm_weight(w, ldw, cm, V, d, wsb + L.wide, st, rc);
   if (rc) return rc;
+  // W^T [d, V_pad] in the staged type (fp8 weights: from their exact bf16 widening; the row scale is in dz)
+  if (need_gh) {
+    if (cm.fp8) rc = launch_transpose(wsb + L.wide, d, OCTO_BF16, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt,
+                                      L.V_pad, cm.dt, st);
+    else rc = launch_transpose(w, ldw, w_dtype, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt, L.V_pad, cm.dt, st);
+    if (rc) return rc;
+  }
 
   for (int64_t p = 0; p < L.passes; ++p) {
     const int64_t r0 = p * L.P;

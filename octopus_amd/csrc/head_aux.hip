@@ -12,6 +12,57 @@
 
 namespace octo {
 
+// 8 consecutive 16-bit values (one 16-byte chunk) as fp32, and back (round to nearest even).
+__device__ __forceinline__ void unpack8(const i32x4 v, bool f16, float (&x)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t b = ((uint32_t)v[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+    x[e] = f16 ? (float)__builtin_bit_cast(_Float16, (uint16_t)b) : __uint_as_float(b << 16);
+  }
+}
+__device__ __forceinline__ i32x4 pack8(const float (&x)[8], bool f16) {
+  i32x4 v;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    uint32_t lo, hi;
+    if (f16) {
+      lo = __builtin_bit_cast(uint16_t, (_Float16)x[2 * h]);
+      hi = __builtin_bit_cast(uint16_t, (_Float16)x[2 * h + 1]);
+    } else {
+      lo = __builtin_bit_cast(uint16_t, (__bf16)x[2 * h]);
+      hi = __builtin_bit_cast(uint16_t, (__bf16)x[2 * h + 1]);
+    }
+    v[h] = (int)(lo | (hi << 16));
+  }
+  return v;
+}
+
+// This lane's part of the fp32 dot product of hidden row hrow and weight row y (the target logit before any scale):
+// 16-byte chunks when both are the same 16-bit type, element by element otherwise.
+__device__ __forceinline__ float row_dot(const void *h, int h_dtype, int64_t hoff, const void *w, int w_dtype,
+                                         int64_t woff, int d, int lane) {
+  float dot = 0.f;
+  if (h_dtype == w_dtype && (h_dtype == OCTO_BF16 || h_dtype == OCTO_F16) && d % 8 == 0) {
+    const bool f16 = h_dtype == OCTO_F16;
+    const char *hp = (const char *)h + hoff * 2, *wp = (const char *)w + woff * 2;
+    for (int k = lane; k < d / 8; k += 64) {
+      float a[8], b[8];
+      unpack8(*(const i32x4 *)(hp + k * 16), f16, a);
+      unpack8(*(const i32x4 *)(wp + k * 16), f16, b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(a[e], b[e], dot);
+    }
+    return dot;
+  }
+  for (int k = lane; k < d; k += 64) {
+    const float hv = load_as_f32(h, h_dtype, hoff + k);
+    const float wv = w_dtype == OCTO_FP8E4M3 ? e4m3_to_f32(((const uint8_t *)w)[woff + k])
+                                             : load_as_f32(w, w_dtype, woff + k);
+    dot = __builtin_fmaf(hv, wv, dot);
+  }
+  return dot;
+}
+
 // ---- merge: vocab-tile partials -> per-row outputs ----------------------------------------------
 // One wave per compact row: lanes merge the row's partials (m, S, U) strided by 64, then a wave
 // butterfly; the target logit h_r . W_y is a wave dot product in fp32.
@@ -33,15 +84,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
 
   float dot = 0.f;
   const bool y_ok = y >= 0 && y < a.V;
-  if (y_ok) {
-    for (int k = lane; k < a.d; k += 64) {
-      const float hv = load_as_f32(a.h, a.h_dtype, hrow * a.ldh + k);
-      float wv;
-      if (a.w_dtype == OCTO_FP8E4M3) wv = e4m3_to_f32(((const uint8_t *)a.w)[y * a.ldw + k]);
-      else wv = load_as_f32(a.w, a.w_dtype, y * a.ldw + k);
-      dot = __builtin_fmaf(hv, wv, dot);
-    }
-  }
+  if (y_ok) dot = row_dot(a.h, a.h_dtype, hrow * a.ldh, a.w, a.w_dtype, y * a.ldw, a.d, lane);
   dot = wave_sum(dot);
   if (lane != 0) return;
   if (a.w_dtype == OCTO_FP8E4M3 && y_ok) dot *= a.wscale[y];
@@ -83,14 +126,7 @@ __global__ __launch_bounds__(256) void hit_kernel(HitArgs a) {
     const int64_t hrow = a.idx ? a.idx[r] : r;
     const int64_t y = a.labels[a.label_idx ? a.label_idx[r] : r];
     if (y >= 0 && y < a.V) {
-      float dot = 0.f;
-      for (int k = lane; k < a.d; k += 64) {
-        const float hv = load_as_f32(a.h, a.h_dtype, hrow * a.ldh + k);
-        float wv;
-        if (a.w_dtype == OCTO_FP8E4M3) wv = e4m3_to_f32(((const uint8_t *)a.w)[y * a.ldw + k]);
-        else wv = load_as_f32(a.w, a.w_dtype, y * a.ldw + k);
-        dot = __builtin_fmaf(hv, wv, dot);
-      }
+      float dot = row_dot(a.h, a.h_dtype, hrow * a.ldh, a.w, a.w_dtype, y * a.ldw, a.d, lane);
       dot = wave_sum(dot);
       const bool f8 = a.w_dtype == OCTO_FP8E4M3;
       const float x = f8 ? dot * a.wscale[y] : dot;
@@ -142,11 +178,58 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *src, int64_t
   }
 }
 
+// The 16-bit form: 16-byte loads and stores. In the LDS tile, element (column c, row r) sits at
+// c * 128 + ((r >> 3) ^ ((c >> 3) & 7)) * 16 + (r & 7) * 2: a wave's 2-byte writes (8 rows x 8 column chunks, one
+// element of each) and its 16-byte reads (whole 128-byte column rows) both hit distinct banks.
+typedef __attribute__((address_space(3))) short lds_short16;
+typedef __attribute__((address_space(3))) i32x4 lds_i32x4_t;
+__global__ __launch_bounds__(256) void transpose16_kernel(const char *src, int64_t ld_src, const int64_t *map,
+                                                          const int32_t *count, int64_t count_off, int64_t rows,
+                                                          int64_t rows_pad, int64_t cols, char *dst, int64_t ld_dst) {
+  __shared__ __attribute__((aligned(16))) char tile_[64 * 128];
+  __attribute__((address_space(3))) char *tile = (__attribute__((address_space(3))) char *)tile_;
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
+  const int64_t valid = dev_count(count, count_off, rows);
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int c = t + 256 * k;  // 16-byte chunk of the source tile: row c >> 3, columns 8 (c & 7) ..
+    const int row = c >> 3, cc = c & 7;
+    const int64_t r = r0 + row, col = c0 + 8 * cc;
+    i32x4 v = {0, 0, 0, 0};
+    if (r < valid && col < cols) v = *(const i32x4 *)(src + (map ? map[r] : r) * ld_src + col * 2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const short x = (short)((uint32_t)v[e >> 1] >> (16 * (e & 1)));
+      *(lds_short16 *)(tile + (8 * cc + e) * 128 + (((row >> 3) ^ cc) << 4) + (row & 7) * 2) = x;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int c = t + 256 * k;  // destination row c0 + (c >> 3), source rows r0 + 8 (c & 7) ..
+    const int drow = c >> 3, rc = c & 7;
+    const int64_t col = c0 + drow, r = r0 + 8 * rc;
+    if (col < cols && r < rows_pad) {
+      const i32x4 v = *(const lds_i32x4_t *)(tile + drow * 128 + ((rc ^ ((drow >> 3) & 7)) << 4));
+      *(i32x4 *)(dst + (col * ld_dst + r) * 2) = v;
+    }
+  }
+}
+
 int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *,
                      const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
                      int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st) {
   if (rows_pad == 0 || cols == 0) return OCTO_OK;
   dim3 grid((unsigned)cdiv(rows_pad, 64), (unsigned)cdiv(cols, 64));
+  const bool b16 = (src_dtype == OCTO_BF16 || src_dtype == OCTO_F16) && dst_dtype == src_dtype;
+  if (b16 && cols % 8 == 0 && rows_pad % 64 == 0 && ld_src % 8 == 0 && ld_dst % 8 == 0 &&
+      ((uintptr_t)src) % 16 == 0 && ((uintptr_t)dst) % 16 == 0) {
+    hipLaunchKernelGGL(transpose16_kernel, grid, dim3(256), 0, st, (const char *)src, ld_src * 2, map, count,
+                       count_off, rows, rows_pad, cols, (char *)dst, ld_dst);
+    OCTO_CHECK_LAUNCH("transpose");
+    return OCTO_OK;
+  }
   hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, st, src, ld_src, src_dtype, map, count, count_off, rows,
                      rows_pad, cols, dst, ld_dst, dst_dtype);
   OCTO_CHECK_LAUNCH("transpose");
@@ -299,6 +382,24 @@ __global__ __launch_bounds__(256) void rows_scatter_kernel(const void *src, int6
   if (r > 0 && idx[r - 1] == row) return;
   int64_t e = r + 1;
   while (e < cnt && idx[e] == row) ++e;
+  if (src_dtype == dst_dtype && (src_dtype == OCTO_BF16 || src_dtype == OCTO_F16) && d % 8 == 0 && ld_src % 8 == 0 &&
+      ld_dst % 8 == 0 && (uintptr_t)src % 16 == 0 && (uintptr_t)dst % 16 == 0) {  // 16-byte chunks
+    const bool f16 = src_dtype == OCTO_F16;
+    for (int k = threadIdx.x; k < d / 8; k += 256) {
+      float s[8], x[8];
+      if (accumulate) unpack8(*(const i32x4 *)((const char *)dst + (row * ld_dst + 8 * k) * 2), f16, s);
+      else
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s[u] = 0.f;
+      for (int64_t q = r; q < e; ++q) {
+        unpack8(*(const i32x4 *)((const char *)src + (q * ld_src + 8 * k) * 2), f16, x);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s[u] += x[u];
+      }
+      *(i32x4 *)((char *)dst + (row * ld_dst + 8 * k) * 2) = pack8(s, f16);
+    }
+    return;
+  }
   for (int k = threadIdx.x; k < d; k += 256) {
     float s = accumulate ? load_as_f32(dst, dst_dtype, row * ld_dst + k) : 0.f;
     for (int64_t q = r; q < e; ++q) s += load_as_f32(src, src_dtype, q * ld_src + k);
