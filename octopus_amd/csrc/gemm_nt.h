@@ -57,10 +57,13 @@ struct GemmShape {
 };
 
 // Block -> (mt, nt). Blocks run on XCD b % 8. M-tiles are dealt to the XCDs round-robin (XCD x owns
-// mt = x, x + 8, ...), so a device-side count that idles a suffix of M-tiles idles them evenly on every
-// XCD; each XCD walks its own M-tiles in groups of group_m across all N-tiles, so the ~32 workgroups
-// resident on an XCD share a few A and B K-slices in its L2. The grid is 8 * (tiles of the largest
-// XCD); blocks past their XCD's tiles return false.
+// mt = x, x + 8, ...); each XCD walks its own M-tiles in groups of group_m across all N-tiles, so the ~32
+// workgroups resident on an XCD share a few A and B K-slices in its L2. A device-side row count that bounds M
+// or N shrinks the tile grid the blocks are dealt over (read once per block), so the idle blocks all come after
+// the working ones instead of between them: interleaved idle blocks retire instantly and stagger the working
+// workgroups at every group start, which breaks their L2 sharing (the forward GEMM fetched 3.4 x its
+// shared-slice traffic that way at 65,536 packed tokens of which 42,312 scored). The grid is 8 * (tiles of the
+// largest XCD) of the bound-free grid; blocks past their XCD's tiles return false.
 __host__ __device__ inline int64_t tile_grid(int mtiles, int ntiles) {
   return 8 * ((int64_t)((mtiles + 7) / 8) * ntiles);
 }
@@ -68,9 +71,12 @@ __device__ __forceinline__ bool tile_of(const GemmShape &s, int &mt, int &nt) {
   const int64_t b = blockIdx.x;
   const int x = (int)(b & 7);
   const int64_t k = b >> 3;
-  const int64_t mx = (s.mtiles - x + 7) / 8;  // M-tiles owned by XCD x
-  if (k >= mx * s.ntiles) return false;
-  const int64_t span = (int64_t)s.group_m * s.ntiles;
+  int64_t mtiles = s.mtiles, ntiles = s.ntiles;
+  if (s.count_on == 1) mtiles = min(mtiles, cdiv(dev_count(s.count, s.count_off, s.M), (int64_t)TM));
+  if (s.count_on == 2) ntiles = min(ntiles, cdiv(dev_count(s.count, s.count_off, s.N), (int64_t)TN));
+  const int64_t mx = (mtiles - x + 7) / 8;  // M-tiles owned by XCD x
+  if (k >= mx * ntiles) return false;
+  const int64_t span = (int64_t)s.group_m * ntiles;
   const int64_t gid = k / span;
   const int64_t first = gid * s.group_m;
   const int64_t gsize = (mx - first) < s.group_m ? (mx - first) : s.group_m;

@@ -68,7 +68,10 @@ struct TimedLaunch {
   ~TimedLaunch() { done(); }
 };
 
-constexpr int64_t kPassRows = 32768;  // backward rows per pass (bounds the dz staging buffers)
+// Backward rows per pass: bounds the dz staging buffers (both layouts: 4 V_pad bytes per row, 33.6 GB at 65,536 rows
+// and V = 128,256, 12% of a 288 GB MI355X). A pass runs each gradient GEMM once; a later pass with few rows runs them
+// at low occupancy and makes grad_W round-trip fp32 partials, so the cap is set to take 65,536 packed tokens whole.
+constexpr int64_t kPassRows = 65536;
 constexpr size_t kAlign = 256;
 #ifndef OCTO_GROUP_M
 #define OCTO_GROUP_M 4

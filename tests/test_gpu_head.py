@@ -68,6 +68,26 @@ def test_backward_matches_oracle(dtype, shape):
         assert _rel(hd.grad.cpu(), gh) <= bar and _rel(Wd.grad.cpu(), gw) <= bar, (T, post)
 
 
+def test_backward_over_two_passes_matches_fp32_reference():
+    """More rows than one backward pass takes (65,536): each pass recomputes its dz, grad_h rows come from their own
+    pass, and a 16-bit grad_W is the fp32 sum of both passes' partials, rounded once."""
+    from tests.gpu_reference import head_fp32
+    n, d, V = 65536 + 4096 + 3, 128, 1000
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    h = torch.randn(n, d, device=DEV, generator=gen).to(torch.bfloat16)
+    W = (torch.randn(V, d, device=DEV, generator=gen) * 0.05).to(torch.bfloat16)
+    y = torch.randint(0, V, (n,), device=DEV, generator=gen)
+    g = torch.randn(n, device=DEV, generator=gen)
+    hd, Wd = h.clone().requires_grad_(True), W.clone().requires_grad_(True)
+    out = fused_head(hd, Wd, y, 0.7)
+    (out[:, 0] * g).sum().backward()
+    lp, ent, gr, gw = head_fp32(h, W.float(), y, 0.7, g=g)
+    assert (out[:, 0] - lp).abs().max().item() <= 2e-3 and (out[:, 1] - ent).abs().max().item() <= 2e-3
+    assert _rel(hd.grad, gr) <= 1e-2 and _rel(Wd.grad, gw) <= 1e-2
+    # the rows of the second pass on their own
+    assert _rel(hd.grad[65536:], gr[65536:]) <= 1e-2
+
+
 FP8_SHAPES = [(1, 64, 100), (300, 64, 1000), (513, 256, 5000), (256, 48, 777), (70, 2560, 3000)]
 
 
