@@ -87,16 +87,6 @@ __device__ __forceinline__ bool tile_of(const GemmShape &s, int &mt, int &nt) {
 }
 
 template <int DT> struct Mfma;
-template <> struct Mfma<OCTO_BF16> {
-  static __device__ __forceinline__ void run(const i32x4 a, const i32x4 b, f32x16 &c) {
-    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-};
-template <> struct Mfma<OCTO_F16> {
-  static __device__ __forceinline__ void run(const i32x4 a, const i32x4 b, f32x16 &c) {
-    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-};
 template <> struct Mfma<OCTO_F32> {
   // a 16-byte fragment holds 4 fp32 K values: four 32x32x2 steps, lane half h supplies k = 4h + e
   static __device__ __forceinline__ void run(const i32x4 a, const i32x4 b, f32x16 &c) {

@@ -268,18 +268,15 @@ __device__ __forceinline__ void dz_store_direct(const f32x16 (&acc)[4][4], const
 
 // 16-bit dz through one LDS staging tile T (the ring, free after the mainloop): T[t] holds dz of token t (tile
 // column) over the tile's 256 vocabulary rows, as 64 slots of 8 bytes (4 consecutive rows); logical slot s of token t
-// sits at physical slot s ^ swz(t), the swizzle chosen per accumulator layout so that all three accesses are free of
-// bank conflicts:
-//   - the accumulator writes (Acc32: a half-wave = 32 tokens, one slot; Acc16: 16 tokens x 2 adjacent slots);
+// sits at physical slot s ^ swz(t), the swizzle chosen for the accumulator layout so that all three accesses are free
+// of bank conflicts:
+//   - the accumulator writes (Acc16: a half-wave = 16 tokens x 2 adjacent slots);
 //   - the token-major read-back (16 lanes: one token, 16 consecutive 16-byte pairs);
 //   - the vocab-major read-back by transposing reads (16 lanes: 16 tokens t & 31 in {8k + e}, one slot; the two
 //     16-lane groups of a 32-lane pass differ in bit 5 of t, which moves their slots to disjoint sets).
 // The dense pass writes -g p / T x post' (x fp8 row scale) everywhere; after a barrier one thread per token writes the
 // label entry (launch_hit's value) over it, so no element is compared against the label.
 template <class L> struct DzSwz;
-template <> struct DzSwz<Acc32> {
-  static __device__ __forceinline__ int at(int t) { return (t & 31) ^ (((t >> 5) & 1) << 2); }
-};
 template <> struct DzSwz<Acc16> {
   static __device__ __forceinline__ int at(int t) { return (((t & 15) << 1) | ((t >> 4) & 1)) ^ (((t >> 5) & 1) << 3); }
 };
