@@ -52,7 +52,7 @@ def test_forward_matches_oracle(dtype, shape):
         assert (out[:, 1].double() - ent).abs().max() <= tol, (T, post)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("shape", [(300, 64, 1000), (513, 256, 5000), (256, 40, 777)], ids=str)
 def test_backward_matches_oracle(dtype, shape):
     n, d, V = shape
