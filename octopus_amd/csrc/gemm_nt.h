@@ -312,6 +312,8 @@ static_assert(SMEM_RING5 <= 160 * 1024, "LDS budget");
 
 struct OpRows128 {
   static constexpr int NI = ENI;
+  typedef i32x4 F;  // fragment as held between its read and its MFMAs
+  static __device__ __forceinline__ i32x4 op(const F &f) { return f; }
   __amdgpu_buffer_rsrc_t rs;
   uint32_t off[ENI];
   uint32_t coff;
@@ -349,6 +351,70 @@ struct OpRows128 {
   }
 };
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16 through a restrict pointer: inlining gives the read alias-scope information, without which
+// the compiler waits for every LDS DMA in flight (vmcnt(0)) before it, as for a read it cannot tell apart from them.
+__device__ __forceinline__ s16x4 lds_read_tr16(lds_s16x4 *__restrict__ p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(p);
+}
+
+// K-major operand: the GEMM's K runs down the matrix rows and M along them, element (k, m) at base + k ld + 2 m
+// (grad_W = dz^T h reads dz token-major this way, so dz needs no vocab-major copy). A stage slice is 64 K-rows of
+// the tile's 256 M values (512 bytes). The 32-byte segment s (M values 16 s .. 16 s + 15) of slice row r sits at
+// physical segment s ^ f(r), f(r) = (r & 3) | ((r >> 3) & 3) << 2.
+// A fragment is two ds_read_b64_tr_b16. In a 16-lane group the instruction returns to lane i, element e, element
+// i & 3 of what lane 4 e + (i >> 2) addressed; so lane s of group G addresses K-row 8 G + (s >> 2) (+ 4 for the
+// second read) and M values 4 (s & 3) .. + 3 of the block, and lane l receives M value l & 15 at K values
+// 8 (l >> 4) + 0..7: the K-contiguous fragment layout of OpRows128. The 16 rows one read touches have distinct
+// f(r), so its 64 lanes cover 512 consecutive bank bytes.
+// DMA instruction q of wave w fills rows r0 = 2 (q & 1) + 4 ((q >> 1) & 1) + 8 w + 32 (q >> 2) and r0 + 1, lane i
+// row r0 + (i >> 5) and physical 16-byte chunk i & 31: f(r) then depends on the lane and q & 1 only, so two
+// lane offsets serve all eight instructions, the row offset riding in the instruction's scalar offset.
+// Nothing is bounds-checked: the caller guarantees K-rows up to the next multiple of 64 exist and read zero past K.
+struct OpCols128 {
+  static constexpr int NI = ENI;
+  // A fragment is carried as its two 8-byte halves and joined at each MFMA: a joined 16-byte value carried across
+  // the loop makes the register allocator keep the halves and the join apart (64 more VGPRs, spilled accumulators).
+  struct F {
+    i32x2 lo, hi;
+  };
+  static __device__ __forceinline__ i32x4 op(const F &f) { return __builtin_shufflevector(f.lo, f.hi, 0, 1, 2, 3); }
+  const char *base;  // K-row 0, M value col0
+  uint32_t ld;       // K-row stride, bytes
+  uint32_t lo[2];    // lane offset (row 8 w + (i >> 5)) of the DMA instructions with q & 1 = 0, 1
+  int fo, fx;        // fragment byte offset of K-step 0, read 0; segment XOR of block 0
+
+  __device__ __forceinline__ void init(const Operand &op, int64_t col0, int wsub, uint32_t /*krows*/) {
+    const int w = threadIdx.x >> 6, i = threadIdx.x & 63, c = i & 31;
+    base = uniform_ptr(op.base + col0 * 2);
+    ld = (uint32_t)op.ld;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int f = (i >> 5) | (b << 1) | (w << 2);
+      lo[b] = (uint32_t)((i >> 5) + 8 * w) * ld + (uint32_t)((((c >> 1) ^ f) << 5) | ((c & 1) << 4));
+    }
+    const int g = (i >> 4) & 3, s = i & 15;
+    fo = (8 * g + (s >> 2)) * 512 + 8 * (s & 3);
+    fx = (8 * wsub) ^ ((s >> 2) | (g << 2));
+  }
+  __device__ __forceinline__ void dma(int k, int q, uint32_t /*kbytes*/, lds_char *slice) const {
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r0 = 2 * (q & 1) + 4 * ((q >> 1) & 1) + 32 * (q >> 2);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(base + (int64_t)k * 64 * ld, 64u * ld),
+                                             (__attribute__((address_space(3))) void *)(slice + (r0 + 8 * w) * 512),
+                                             16, lo[q & 1], (uint32_t)r0 * ld, 0, 0);
+  }
+  __device__ __forceinline__ F frag(const lds_char *slice, int ks, int blk) const {
+    const lds_char *p = slice + fo + ks * 32 * 512 + ((fx ^ blk) << 5);
+    F f;
+    f.lo = __builtin_bit_cast(i32x2, lds_read_tr16((lds_s16x4 *)p));
+    f.hi = __builtin_bit_cast(i32x2, lds_read_tr16((lds_s16x4 *)(p + 4 * 512)));
+    return f;
+  }
+};
+
 // The 16-bit GEMMs (bf16 / f16 operands; fp8 weights are widened to bf16 before the GEMM) run the ring loop, fp32
 // the 4-stage one.
 __host__ __device__ constexpr bool ring5_ok(int dt) { return dt == OCTO_BF16 || dt == OCTO_F16; }
@@ -373,7 +439,7 @@ template <> struct Mfma16<OCTO_F16> {
 // XFRAG: its first fragments are read under K-step 1 (else the caller reads them).
 template <int DT, typename OA, typename OB, bool DMA, bool NEXT, bool XFRAG = NEXT>
 __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd, int sa, uint32_t kbytes,
-                                            lds_char *smem, i32x4 (&fa)[2][8], i32x4 (&fb)[2][8],
+                                            lds_char *smem, typename OA::F (&fa)[2][8], typename OB::F (&fb)[2][8],
                                             f32x4 (&acc)[8][8]) {
   // slots: stage k at (sa, sa + 1), stage k + 1 at (sa + 2, sa + 3), stage k + 2's A at sa + 4, its B at sa
   auto slot = [&](int d) -> lds_char * { const int x = sa + d; return smem + (x >= ENSLOT ? x - ENSLOT : x) * ESLICE; };
@@ -393,7 +459,7 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd
     OCTO_FENCE();
 #pragma unroll
     for (int q = 0; q < 64; ++q) {
-      Mfma16<DT>::run(fa[ks][q >> 3], fb[ks][q & 7], acc[q >> 3][q & 7]);
+      Mfma16<DT>::run(OA::op(fa[ks][q >> 3]), OB::op(fb[ks][q & 7]), acc[q >> 3][q & 7]);
       OCTO_FENCE();
       if (q < 16) {
         if (ks == 0) {
@@ -455,7 +521,8 @@ __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &
   }
   __builtin_amdgcn_s_barrier();
 
-  i32x4 fa[2][8], fb[2][8];
+  typename OA::F fa[2][8];
+  typename OB::F fb[2][8];
 #pragma unroll
   for (int b = 0; b < 8; ++b) {
     fa[0][b] = opa.frag(smem, 0, b);

@@ -68,8 +68,8 @@ struct TimedLaunch {
   ~TimedLaunch() { done(); }
 };
 
-// Backward rows per pass: bounds the dz staging buffers (both layouts: 4 V_pad bytes per row, 33.6 GB at 65,536 rows
-// and V = 128,256, 12% of a 288 GB MI355X). A pass runs each gradient GEMM once; a later pass with few rows runs them
+// Backward rows per pass: bounds the dz staging buffer (16-bit, token-major: 2 V_pad bytes per row, 16.8 GB at 65,536
+// rows and V = 128,256, 6% of a 288 GB MI355X). A pass runs each gradient GEMM once; a later pass with few rows runs them
 // at low occupancy and makes grad_W round-trip fp32 partials, so the cap is set to take 65,536 packed tokens whole.
 constexpr int64_t kPassRows = 65536;
 constexpr size_t kAlign = 256;
@@ -101,9 +101,10 @@ FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
 }
 
 
-// The backward stages every gradient GEMM operand K-contiguous, so each row fetch of the GEMM mainloop is one
-// whole cache line: W^T [d, V_pad] for grad_h = dz . W, the pass's hidden rows transposed to h^T [d, P] for
-// grad_W = dz^T . h, and dz in both layouts (token-major for grad_h, vocab-major for grad_W).
+// The backward stages the gradient GEMMs' operands so each mainloop row fetch is whole cache lines: W^T [d, V_pad]
+// for grad_h = dz . W, the pass's hidden rows transposed to h^T [d, P] for grad_W = dz^T . h, and dz token-major
+// [P, V_pad], which grad_h reads K-contiguous and 16-bit grad_W K-major (transposing LDS reads). fp32 dz is also
+// written vocab-major [V_pad, P] for the fp32 loop, which reads K-contiguous operands only.
 struct BwdLayout {
   int64_t P, V_pad, passes;
   int esz;
@@ -120,10 +121,10 @@ BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, boo
   if (need_gh) off += align_up((size_t)d * L.V_pad * L.esz);
   L.ht = off;  // h^T [d, P] of the pass's rows (grad_W)
   if (need_gw) off += align_up((size_t)d * L.P * L.esz);
-  L.dza = off;  // dz [P, V_pad], token-major (grad_h)
-  if (need_gh) off += align_up((size_t)L.P * L.V_pad * L.esz);
-  L.dzb = off;  // dz [V_pad, P], vocab-major (grad_W)
-  if (need_gw) off += align_up((size_t)L.V_pad * L.P * L.esz);
+  L.dza = off;  // dz [P, V_pad], token-major (grad_h; 16-bit grad_W)
+  if (need_gh || (need_gw && L.esz == 2)) off += align_up((size_t)L.P * L.V_pad * L.esz);
+  L.dzb = off;  // dz [V_pad, P], vocab-major (fp32 grad_W)
+  if (need_gw && L.esz == 4) off += align_up((size_t)L.V_pad * L.P * L.esz);
   L.hit = off;  // dz at each row's label [P] fp32 (16-bit dz epilogue)
   if (L.esz == 2) off += align_up((size_t)L.P * sizeof(float));
   L.wide = off;  // fp8 weights widened to bf16 [V, d] (the dz recompute's operand)
@@ -422,9 +423,9 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm);
     const GemmShape s1 = shape(V, rows, d, kGroupM, 2, count, r0);
     DzArgs e;
-    e.dzA = need_gh ? dza : nullptr;
+    e.dzA = (need_gh || (need_gw && esz == 2)) ? dza : nullptr;
     e.ldA = L.V_pad;
-    e.dzB = need_gw ? dzb : nullptr;
+    e.dzB = (need_gw && esz == 4) ? dzb : nullptr;
     e.ldB = L.P;
     e.lse = lse;
     e.g = g;
@@ -493,7 +494,9 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, nullptr,
                             idx ? idx + r0 : nullptr, count, r0, rows, rows_pad, d, ht, L.P, cm.dt, st);
       if (rc) return rc;
-      const Operand A3 = plain_operand(dzb, L.P * esz, L.V_pad, nullptr, 0);
+      const bool kmajor = esz == 2;  // dz token-major read K-major, else the fp32 vocab-major copy
+      const Operand A3 = kmajor ? plain_operand(dza, L.V_pad * esz, L.P, nullptr, 0)
+                                : plain_operand(dzb, L.P * esz, L.V_pad, nullptr, 0);
       const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
       const GemmShape s3 = shape(V, d, rows, kGroupM, 3, count, r0);
       StoreArgs o;
@@ -512,7 +515,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       o.ldc = d;
       {
         TimedLaunch t("gemm_store_grad_w", st);
-        rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st);
+        rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st, kmajor);
       }
       if (rc) return rc;
     }

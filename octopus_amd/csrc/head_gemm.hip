@@ -139,10 +139,10 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
 // ---- epilogue: dz recompute ------------------------------------------------------------------
 //
-// dz = g (onehot - p) / T x post'(z) of the 256 (vocab) x 256 (token) tile, written in both global layouts
-// (dzA [token][vocab] for grad_h, dzB [vocab][token] for grad_W). 16-bit types go through one LDS staging tile as
-// whole 512-byte and 256-byte row segments (dz_stage / dz_write below); fp32 is computed in place in the
-// accumulators and stored directly.
+// dz = g (onehot - p) / T x post'(z) of the 256 (vocab) x 256 (token) tile. 16-bit types write it token-major
+// only (dzA [token][vocab]: grad_h reads it K-contiguous, grad_W K-major), through one LDS staging tile as whole
+// 512-byte rows (dz_stage / dz_write below). fp32 is computed in place in the accumulators and stored directly in
+// both layouts (dzB [vocab][token] for grad_W's K-contiguous fp32 loop).
 
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -282,8 +282,6 @@ template <> struct DzSwz<Acc16> {
 };
 
 typedef __attribute__((address_space(3))) short lds_short;
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 template <class L, typename P2, bool A_FP8, bool TANH, bool EDGE>
 __device__ __forceinline__ void dz_stage(const typename L::V (&acc)[L::NI][L::NJ], const DzArgs &e, int64_t m0,
@@ -359,25 +357,6 @@ __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0
   __syncthreads();
   if (e.dzA)  // [token][vocab]: 512-byte rows
     lds_tile_to_global(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return DzSwz<L>::at(row); });
-  if (e.dzB) {  // [vocab][token] by transposing reads: a 16-lane group gives 4 vocab rows x 32 tokens, 8 per lane
-    const int w = t >> 6, l = t & 63, G = l >> 4, i = l & 15;
-    const int src = 8 * (i & 3) + (i >> 2);  // this lane's source token as a transposing-read source, 0..31
-#pragma unroll 4
-    for (int p = 0; p < 32; ++p) {
-      const int u = p * 4 + w;              // unit: 4 vocab rows (quad q) x 128 tokens (half)
-      const int q = u >> 1, tb = 128 * (u & 1) + 32 * G;
-      const int t1 = tb + src, t2 = t1 + 4;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + t1 * 512 + ((q ^ DzSwz<L>::at(t1)) << 3)));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(tile + t2 * 512 + ((q ^ DzSwz<L>::at(t2)) << 3)));
-      i32x4 v;
-      v[0] = __builtin_bit_cast(i32x2, lo)[0];
-      v[1] = __builtin_bit_cast(i32x2, lo)[1];
-      v[2] = __builtin_bit_cast(i32x2, hi)[0];
-      v[3] = __builtin_bit_cast(i32x2, hi)[1];
-      const int vr = 4 * q + (i & 3);
-      *(i32x4 *)((char *)e.dzB + ((m0 + vr) * e.ldB + n0 + tb + 8 * (i >> 2)) * 2) = v;
-    }
-  }
 }
 
 template <int DT, bool A_FP8, bool TANH>
@@ -458,7 +437,8 @@ __device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::N
   }
 }
 
-template <int DT, int OT>
+// AK: A is K-major (OpCols128; 16-bit types only).
+template <int DT, int OT, bool AK>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
   constexpr bool R5 = ring5_ok(DT);
   __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
@@ -473,9 +453,11 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
   if constexpr (R5) {
     f32x4 acc[8][8];
-    mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, K_eff, smem, acc);
+    typedef typename std::conditional<AK, OpCols128, OpRows128>::type OA;
+    mainloop_ring5<DT, OA, OpRows128>(A, B, m0, n0, K_eff, smem, acc);
     store_any<Acc16, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
   } else {
+    static_assert(!AK, "K-major A: 16-bit types only");
     f32x16 acc[4][4];
     mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
     store_any<Acc32, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
@@ -528,12 +510,12 @@ int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operan
   return octo_fail(OCTO_EUNSUPPORTED, "gemm_dz: dtype %d", dt);
 }
 
-template <int DT>
+template <int DT, bool AK>
 static int go_store(const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e, hipStream_t st) {
   switch (e.dtype) {
-    case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16, AK>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16, AK>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+    case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32, AK>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
     default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
   }
   OCTO_CHECK_LAUNCH("gemm_store");
@@ -541,11 +523,21 @@ static int go_store(const Operand &A, const Operand &B, const GemmShape &s, cons
 }
 
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
-                      hipStream_t st) {
+                      hipStream_t st, bool a_kmajor) {
+  if (a_kmajor) {
+    // OpCols128 reads whole 512-byte rows of the tile's 256 columns from a plain (unmapped) matrix
+    if (A.map || (A.ld & 15) || A.ld < 512 || A.ld > 0xffffffffLL / 64 || (uintptr_t)A.base % 16)
+      return octo_fail(OCTO_EINVAL, "gemm_store: K-major operand layout");
+    switch (dt) {
+      case OCTO_BF16: return go_store<OCTO_BF16, true>(A, B, s, e, st);
+      case OCTO_F16: return go_store<OCTO_F16, true>(A, B, s, e, st);
+    }
+    return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: K-major operand of dtype %d", dt);
+  }
   switch (dt) {
-    case OCTO_BF16: return go_store<OCTO_BF16>(A, B, s, e, st);
-    case OCTO_F16: return go_store<OCTO_F16>(A, B, s, e, st);
-    case OCTO_F32: return go_store<OCTO_F32>(A, B, s, e, st);
+    case OCTO_BF16: return go_store<OCTO_BF16, false>(A, B, s, e, st);
+    case OCTO_F16: return go_store<OCTO_F16, false>(A, B, s, e, st);
+    case OCTO_F32: return go_store<OCTO_F32, false>(A, B, s, e, st);
   }
   return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: dtype %d", dt);
 }

@@ -22,7 +22,7 @@ struct StatsArgs {
 struct DzArgs {
   void *dzA;  // [tokens, ldA] vocabulary contiguous, staged MFMA type, or NULL
   int64_t ldA;
-  void *dzB;  // [V_pad, ldB] tokens contiguous, staged MFMA type, or NULL
+  void *dzB;  // [V_pad, ldB] tokens contiguous, fp32 only, or NULL
   int64_t ldB;
   const float *lse;
   const float *g;
@@ -70,8 +70,9 @@ int launch_gemm_stats(int dt, bool a_fp8, bool tanh, const Operand &A, const Ope
                       const StatsArgs &e, hipStream_t st);
 int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
                    const DzArgs &e, hipStream_t st);
+// a_kmajor: A is a plain K-major matrix (element (k, m) at base + k ld + 2 m), 16-bit types
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
-                      hipStream_t st);
+                      hipStream_t st, bool a_kmajor = false);
 
 // ---- small kernels (head_aux.hip) ---------------------------------------------------------------
 struct MergeArgs {
