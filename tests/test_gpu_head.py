@@ -53,7 +53,8 @@ def test_forward_matches_oracle(dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
-@pytest.mark.parametrize("shape", [(300, 64, 1000), (513, 256, 5000), (256, 40, 777)], ids=str)
+@pytest.mark.parametrize("shape", [(1, 64, 100), (300, 64, 1000), (513, 256, 5000), (256, 40, 777), (70, 2560, 3000)],
+                         ids=str)
 def test_backward_matches_oracle(dtype, shape):
     n, d, V = shape
     h, W, y = _inputs(n, d, V, dtype, seed=1)
