@@ -295,38 +295,42 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
 // landed in every wave". It frees stage k's two slots: slot 2 k (mod 5) takes stage k + 2's B slice, slot 2 k + 1
 // stage k + 3's A slice. So iteration k issues stage k + 2 whole: its A slice under K-step 0 (into the slot freed at
 // B_(k-1)), its B slice under K-step 1 (the slot freed at B_k). At B_k only stage k + 2's A slice may still be in
-// flight: vmcnt(8).
+// flight: vmcnt(32 / NW).
 //
 //   OpRows128 (K-contiguous rows): a slice is 256 rows x 128 bytes. Chunk c (0..7) of row r sits at physical
 //     chunk c ^ ((r >> 1) & 7), so a 16-lane pass of fragment reads (rows r0..r0+15, r0 a multiple of 16, of
-//     one logical chunk) covers all 64 banks once. DMA instruction q of wave w fills slice rows (4 q + w) * 8 ..
+//     one logical chunk) covers all 64 banks once. DMA instruction q of wave w fills slice rows (NW q + w) * 8 ..
 //     + 8; lane i takes row + (i >> 3) and physical chunk i & 7, so the 8 lanes of a row fetch its 128 bytes.
 //     A fragment is one ds_read_b128: lane l holds row l & 15 of a 16-row block, K chunk 4 ks + (l >> 4) of the
 //     stage's K-step ks (the v_mfma_f32_16x16x32 operand layout).
 constexpr int EKB = 128;              // K bytes per stage and row
 constexpr int ESLICE = 256 * EKB;     // one operand's stage slice (32 KB)
 constexpr int ENSLOT = 5;             // ring slots
-constexpr int ENI = 8;                // DMA instructions per wave, operand and stage
 constexpr int SMEM_RING5 = ENSLOT * ESLICE;
 static_assert(SMEM_RING5 <= 160 * 1024, "LDS budget");
 
-struct OpRows128 {
-  static constexpr int NI = ENI;
+// The loop runs with NW = 4 waves (2 x 2, each 128 x 128 of the tile) or NW = 8 (2 x 4, each 128 x 64: two waves
+// per SIMD, so one issues MFMAs while the other waits on a stage or runs its epilogue). An operand's SUB is the
+// wave's rows of it (128; 64 for the B operand of the 8-wave loop). A slice takes 32 DMA instructions, 32 / NW per
+// wave.
+template <int NW, int SUB>
+struct OpRowsN {
+  static constexpr int NI = 32 / NW;   // DMA instructions per wave and stage
+  static constexpr int NB = SUB / 16;  // the wave's 16-row fragment blocks
   typedef i32x4 F;  // fragment as held between its read and its MFMAs
   static __device__ __forceinline__ i32x4 op(const F &f) { return f; }
   __amdgpu_buffer_rsrc_t rs;
-  uint32_t off[ENI];
+  uint32_t off[NI];
   uint32_t coff;
   int fo;  // fragment byte offset of K-step 0, block 0 (K-step 1: fo ^ 64)
-
   __device__ __forceinline__ void init(const Operand &op, int64_t row0, int wsub, uint32_t /*krows*/) {
     const int w = threadIdx.x >> 6, i = threadIdx.x & 63, lane = i;
     const int64_t valid = dev_count(op.count, op.count_off + row0, op.rows - row0);
-    // row (4 q + w) * 8 + (i >> 3): its swizzle ((row >> 1) & 7) = (4 (w & 1) + (i >> 4)) & 7 for every q
+    // row (NW q + w) * 8 + (i >> 3): its swizzle ((row >> 1) & 7) = (4 (w & 1) + (i >> 4)) & 7 for every q
     coff = (uint32_t)(((i & 7) ^ ((4 * (w & 1) + (i >> 4)) & 7)) << 4);
 #pragma unroll
-    for (int q = 0; q < ENI; ++q) {
-      const int r = (4 * q + w) * 8 + (i >> 3);
+    for (int q = 0; q < NI; ++q) {
+      const int r = (NW * q + w) * 8 + (i >> 3);
       uint32_t rowoff;
       if (r < valid) rowoff = op.map ? (uint32_t)(op.map[row0 + r] * op.ld) : (uint32_t)(r * op.ld);
       else rowoff = 0x80000000u;
@@ -336,20 +340,22 @@ struct OpRows128 {
     else rs = make_rsrc(uniform_ptr(op.base + row0 * op.ld), (uint32_t)(256 * op.ld));
     // lane l holds row l & 15 of a 16-row block and chunk 4 ks + (l >> 4) of K-step ks; (row >> 1) & 7 depends on
     // l & 15 alone, and 4 ks + g = (4 ks) ^ g for g < 4, so K-step 1's offset is K-step 0's with chunk bit 2 flipped
-    const int row = wsub * 128 + (lane & 15);
+    const int row = wsub * SUB + (lane & 15);
     fo = row * EKB + ((((lane >> 4) ^ ((lane >> 1) & 7))) << 4);
   }
   // K chunks at or past kbytes (bytes per row) read zero
   __device__ __forceinline__ void dma(int k, int q, uint32_t kbytes, lds_char *slice) const {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t kb = (uint32_t)k * EKB;
-    lds_dma16(rs, (kb + coff < kbytes) ? off[q] + kb : 0x80000000u, slice + (4 * q + w) * 1024);
+    lds_dma16(rs, (kb + coff < kbytes) ? off[q] + kb : 0x80000000u, slice + (NW * q + w) * 1024);
   }
   // the 16 K values (chunk 4 ks + (l >> 4)) of row l & 15 of 16-row block blk, K-step ks (0, 1) of the stage
   __device__ __forceinline__ i32x4 frag(const lds_char *slice, int ks, int blk) const {
     return *(const lds_i32x4 *)(slice + (fo ^ (ks << 6)) + blk * 16 * EKB);
   }
 };
+
+typedef OpRowsN<4, 128> OpRows128;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -367,14 +373,16 @@ __device__ __forceinline__ s16x4 lds_read_tr16(lds_s16x4 *__restrict__ p) {
 // A fragment is two ds_read_b64_tr_b16. In a 16-lane group the instruction returns to lane i, element e, element
 // i & 3 of what lane 4 e + (i >> 2) addressed; so lane s of group G addresses K-row 8 G + (s >> 2) (+ 4 for the
 // second read) and M values 4 (s & 3) .. + 3 of the block, and lane l receives M value l & 15 at K values
-// 8 (l >> 4) + 0..7: the K-contiguous fragment layout of OpRows128. The 16 rows one read touches have distinct
+// 8 (l >> 4) + 0..7: the K-contiguous fragment layout of OpRowsN. The 16 rows one read touches have distinct
 // f(r), so its 64 lanes cover 512 consecutive bank bytes.
-// DMA instruction q of wave w fills rows r0 = 2 (q & 1) + 4 ((q >> 1) & 1) + 8 w + 32 (q >> 2) and r0 + 1, lane i
+// DMA instruction q of wave w fills rows r0 = 2 (q & 1) + 4 ((q >> 1) & 1) + 8 w + 8 NW (q >> 2) and r0 + 1, lane i
 // row r0 + (i >> 5) and physical 16-byte chunk i & 31: f(r) then depends on the lane and q & 1 only, so two
-// lane offsets serve all eight instructions, the row offset riding in the instruction's scalar offset.
+// lane offsets serve all of a wave's instructions, the row offset riding in the instruction's scalar offset.
 // Nothing is bounds-checked: the caller guarantees K-rows up to the next multiple of 64 exist and read zero past K.
-struct OpCols128 {
-  static constexpr int NI = ENI;
+template <int NW, int SUB>
+struct OpColsN {
+  static constexpr int NI = 32 / NW;
+  static constexpr int NB = SUB / 16;
   // A fragment is carried as its two 8-byte halves and joined at each MFMA: a joined 16-byte value carried across
   // the loop makes the register allocator keep the halves and the join apart (64 more VGPRs, spilled accumulators).
   struct F {
@@ -392,16 +400,16 @@ struct OpCols128 {
     ld = (uint32_t)op.ld;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int f = (i >> 5) | (b << 1) | (w << 2);
+      const int f = (i >> 5) | (b << 1) | ((w & 3) << 2);
       lo[b] = (uint32_t)((i >> 5) + 8 * w) * ld + (uint32_t)((((c >> 1) ^ f) << 5) | ((c & 1) << 4));
     }
     const int g = (i >> 4) & 3, s = i & 15;
     fo = (8 * g + (s >> 2)) * 512 + 8 * (s & 3);
-    fx = (8 * wsub) ^ ((s >> 2) | (g << 2));
+    fx = (NB * wsub) ^ ((s >> 2) | (g << 2));
   }
   __device__ __forceinline__ void dma(int k, int q, uint32_t /*kbytes*/, lds_char *slice) const {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r0 = 2 * (q & 1) + 4 * ((q >> 1) & 1) + 32 * (q >> 2);
+    const int r0 = 2 * (q & 1) + 4 * ((q >> 1) & 1) + 8 * NW * (q >> 2);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(base + (int64_t)k * 64 * ld, 64u * ld),
                                              (__attribute__((address_space(3))) void *)(slice + (r0 + 8 * w) * 512),
                                              16, lo[q & 1], (uint32_t)r0 * ld, 0, 0);
@@ -439,8 +447,10 @@ template <> struct Mfma16<OCTO_F16> {
 // XFRAG: its first fragments are read under K-step 1 (else the caller reads them).
 template <int DT, typename OA, typename OB, bool DMA, bool NEXT, bool XFRAG = NEXT>
 __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd, int sa, uint32_t kbytes,
-                                            lds_char *smem, typename OA::F (&fa)[2][8], typename OB::F (&fb)[2][8],
-                                            f32x4 (&acc)[8][8]) {
+                                            lds_char *smem, typename OA::F (&fa)[2][OA::NB],
+                                            typename OB::F (&fb)[2][OB::NB], f32x4 (&acc)[OA::NB][OB::NB]) {
+  constexpr int NA = OA::NB, NBB = OB::NB, NQ = NA * NBB, NR = NA + NBB, NI = OA::NI;
+  constexpr int D0 = NR + 1, DS = (NQ - D0 + NI - 1) / NI;  // DMA issues: MFMA D0, D0 + DS, ... (4 waves: 17 + 6 j)
   // slots: stage k at (sa, sa + 1), stage k + 1 at (sa + 2, sa + 3), stage k + 2's A at sa + 4, its B at sa
   auto slot = [&](int d) -> lds_char * { const int x = sa + d; return smem + (x >= ENSLOT ? x - ENSLOT : x) * ESLICE; };
   const lds_char *cA = slot(0), *cB = slot(1);
@@ -450,7 +460,7 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd
   for (int ks = 0; ks < 2; ++ks) {
     if (ks == 1 && NEXT) {
       __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // this wave's reads of stage k are done
-      if (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(ENI));  // stage k + 1 landed (k + 2's A may be in flight)
+      if (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NI));  // stage k + 1 landed (k + 2's A may be in flight)
       else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
       __builtin_amdgcn_s_barrier();  // ... in every wave; stage k's slots are free
     } else {
@@ -458,23 +468,23 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd
     }
     OCTO_FENCE();
 #pragma unroll
-    for (int q = 0; q < 64; ++q) {
-      Mfma16<DT>::run(OA::op(fa[ks][q >> 3]), OB::op(fb[ks][q & 7]), acc[q >> 3][q & 7]);
+    for (int q = 0; q < NQ; ++q) {
+      Mfma16<DT>::run(OA::op(fa[ks][q / NBB]), OB::op(fb[ks][q % NBB]), acc[q / NBB][q % NBB]);
       OCTO_FENCE();
-      if (q < 16) {
+      if (q < NR) {
         if (ks == 0) {
-          if (q < 8) fa[1][q] = opa.frag(cA, 1, q);
-          else fb[1][q - 8] = opb.frag(cB, 1, q - 8);
+          if (q < NA) fa[1][q] = opa.frag(cA, 1, q);
+          else fb[1][q - NA] = opb.frag(cB, 1, q - NA);
           OCTO_FENCE();
         } else if (NEXT && XFRAG) {
-          if (q < 8) fa[0][q] = opa.frag(nA, 0, q);
-          else fb[0][q - 8] = opb.frag(nB, 0, q - 8);
+          if (q < NA) fa[0][q] = opa.frag(nA, 0, q);
+          else fb[0][q - NA] = opb.frag(nB, 0, q - NA);
           OCTO_FENCE();
         }
       }
-      if (DMA && q >= 17 && (q - 17) % 6 == 0) {  // q = 17, 23, ..., 59
-        if (ks == 0) opa.dma(kd, (q - 17) / 6, kbytes, dA);
-        else opb.dma(kd, (q - 17) / 6, kbytes, dB);
+      if (DMA && q >= D0 && (q - D0) % DS == 0 && (q - D0) / DS < NI) {
+        if (ks == 0) opa.dma(kd, (q - D0) / DS, kbytes, dA);
+        else opb.dma(kd, (q - D0) / DS, kbytes, dB);
         OCTO_FENCE();
       }
     }
@@ -484,15 +494,16 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd
 // smem: SMEM_RING5 bytes. 16-bit types only.
 template <int DT, typename OA, typename OB>
 __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &B, int64_t m0, int64_t n0,
-                                               int64_t K_eff, lds_char *smem, f32x4 (&acc)[8][8]) {
+                                               int64_t K_eff, lds_char *smem, f32x4 (&acc)[OA::NB][OB::NB]) {
   static_assert(DT == OCTO_BF16 || DT == OCTO_F16, "16-bit operands");
-  static_assert(OA::NI == ENI && OB::NI == ENI, "8 DMA instructions per wave and slice");
+  static_assert(OA::NI == OB::NI, "one workgroup shape");
+  constexpr int NI = OA::NI, NWN = TN / (16 * OB::NB);  // waves along N
   const int w = threadIdx.x >> 6;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w / NWN, wn = w % NWN;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < OA::NB; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < OB::NB; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
 
@@ -507,27 +518,26 @@ __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &
 
   // prologue: stages 0 and 1 into slots 0..3
 #pragma unroll
-  for (int q = 0; q < ENI; ++q) opa.dma(0, q, kbytes, smem);
+  for (int q = 0; q < NI; ++q) opa.dma(0, q, kbytes, smem);
 #pragma unroll
-  for (int q = 0; q < ENI; ++q) opb.dma(0, q, kbytes, smem + ESLICE);
+  for (int q = 0; q < NI; ++q) opb.dma(0, q, kbytes, smem + ESLICE);
   if (nk > 1) {
 #pragma unroll
-    for (int q = 0; q < ENI; ++q) opa.dma(1, q, kbytes, smem + 2 * ESLICE);
+    for (int q = 0; q < NI; ++q) opa.dma(1, q, kbytes, smem + 2 * ESLICE);
 #pragma unroll
-    for (int q = 0; q < ENI; ++q) opb.dma(1, q, kbytes, smem + 3 * ESLICE);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * ENI));  // stage 0 landed
+    for (int q = 0; q < NI; ++q) opb.dma(1, q, kbytes, smem + 3 * ESLICE);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NI));  // stage 0 landed
   } else {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   }
   __builtin_amdgcn_s_barrier();
 
-  typename OA::F fa[2][8];
-  typename OB::F fb[2][8];
+  typename OA::F fa[2][OA::NB];
+  typename OB::F fb[2][OB::NB];
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    fa[0][b] = opa.frag(smem, 0, b);
-    fb[0][b] = opb.frag(smem + ESLICE, 0, b);
-  }
+  for (int b = 0; b < OA::NB; ++b) fa[0][b] = opa.frag(smem, 0, b);
+#pragma unroll
+  for (int b = 0; b < OB::NB; ++b) fb[0][b] = opb.frag(smem + ESLICE, 0, b);
   int sa = 0;  // slot of stage k's A slice: 2 k mod 5
   int k = 0;
   for (; k + 2 < nk; ++k) {
@@ -552,6 +562,8 @@ __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &
 struct Acc32 {  // 4 x 4 blocks of v_mfma_f32_32x32x*: column l & 31, rows 8 (v >> 2) + 4 (l >> 5) + (v & 3)
   static constexpr int NI = 4, NJ = 4, NV = 16;
   typedef f32x16 V;
+  static __device__ __forceinline__ int wm(int w) { return w >> 1; }  // 2 x 2 waves
+  static __device__ __forceinline__ int wn(int w) { return w & 1; }
   static __device__ __forceinline__ int row(int wm, int i, int v, int lane) {
     return wm * 128 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
   }
@@ -560,13 +572,19 @@ struct Acc32 {  // 4 x 4 blocks of v_mfma_f32_32x32x*: column l & 31, rows 8 (v 
   static __device__ __forceinline__ float col_sum(float x) { return x + __shfl_xor(x, 32, 64); }
   static __device__ __forceinline__ bool col_lane(int lane) { return lane < 32; }  // one lane per column
 };
-struct Acc16 {  // 8 x 8 blocks of v_mfma_f32_16x16x*: column l & 15, rows 4 (l >> 4) + v
-  static constexpr int NI = 8, NJ = 8, NV = 4;
+// 8 x NJ blocks of v_mfma_f32_16x16x*: column l & 15, rows 4 (l >> 4) + v; NJ = 8 for 2 x 2 waves of 128 x 128,
+// NJ = 4 for the 8-wave loop's 2 x 4 waves of 128 x 64.
+template <int NJ_>
+struct Acc16N {
+  static constexpr int NI = 8, NJ = NJ_, NV = 4;
   typedef f32x4 V;
+  static constexpr int NWN = 256 / (16 * NJ);  // waves along N
+  static __device__ __forceinline__ int wm(int w) { return w / NWN; }
+  static __device__ __forceinline__ int wn(int w) { return w % NWN; }
   static __device__ __forceinline__ int row(int wm, int i, int v, int lane) {
     return wm * 128 + i * 16 + 4 * (lane >> 4) + v;
   }
-  static __device__ __forceinline__ int col(int wn, int j, int lane) { return wn * 128 + j * 16 + (lane & 15); }
+  static __device__ __forceinline__ int col(int wn, int j, int lane) { return wn * 16 * NJ + j * 16 + (lane & 15); }
   static __device__ __forceinline__ float col_max(float x) {
     x = fmaxf(x, __shfl_xor(x, 16, 64));
     return fmaxf(x, __shfl_xor(x, 32, 64));
@@ -577,6 +595,7 @@ struct Acc16 {  // 8 x 8 blocks of v_mfma_f32_16x16x*: column l & 15, rows 4 (l 
   }
   static __device__ __forceinline__ bool col_lane(int lane) { return lane < 16; }
 };
+typedef Acc16N<8> Acc16;
 // The fp32 path's layout.
 __device__ __forceinline__ int acc_row(int wm, int i, int v, int lane) { return Acc32::row(wm, i, v, lane); }
 __device__ __forceinline__ int acc_col(int wn, int j, int lane) { return Acc32::col(wn, j, lane); }

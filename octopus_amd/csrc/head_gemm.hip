@@ -426,7 +426,7 @@ template <class L, typename OT>
 __device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::NJ], void *C, const float *addend,
                                           int64_t ldc, int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid,
                                           int accumulate) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = L::wm(w), wn = L::wn(w);
   OT *c = (OT *)C;
   if (accumulate) {
     if (addend) store_edge<L, OT, true, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
@@ -437,8 +437,7 @@ __device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::N
   }
 }
 
-// AK: A is K-major (OpCols128; 16-bit types only).
-template <int DT, int OT, bool AK>
+template <int DT, int OT>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
   constexpr bool R5 = ring5_ok(DT);
   __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
@@ -453,15 +452,33 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
   if constexpr (R5) {
     f32x4 acc[8][8];
-    typedef typename std::conditional<AK, OpCols128, OpRows128>::type OA;
-    mainloop_ring5<DT, OA, OpRows128>(A, B, m0, n0, K_eff, smem, acc);
+    mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, K_eff, smem, acc);
     store_any<Acc16, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
   } else {
-    static_assert(!AK, "K-major A: 16-bit types only");
     f32x16 acc[4][4];
     mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
     store_any<Acc32, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
   }
+}
+
+// grad_W's 8-wave form: 512 threads, two waves per SIMD, each 128 x 64 of the tile, A (dz) K-major. A K-major
+// fragment is two transposing LDS reads, and the second wave on each SIMD issues MFMAs while one waits on them
+// (same box: 13.6 against 14.1 ms for the 4-wave form at cfg3; grad_h, K-contiguous, is 0.5 ms slower in it).
+template <int DT, int OT>
+__global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_store8_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
+  static_assert(ring5_ok(DT), "16-bit operands");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
+  lds_char *smem = (lds_char *)smem_;
+  int mt, nt;
+  if (!tile_of(s, mt, nt)) return;
+  const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
+  int64_t mvalid = s.M - m0, nvalid = s.N - n0, K_eff = s.K;
+  if (s.count_on == 1) mvalid = dev_count(s.count, s.count_off + m0, mvalid);
+  if (s.count_on == 3) K_eff = round_up(dev_count(s.count, s.count_off, s.K), 64);
+  if (mvalid <= 0 || nvalid <= 0) return;
+  f32x4 acc[8][4];
+  mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
+  store_any<Acc16N<4>, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
 }
 
 // ---- host launchers ----------------------------------------------------------------------------
@@ -512,11 +529,20 @@ int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operan
 
 template <int DT, bool AK>
 static int go_store(const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e, hipStream_t st) {
-  switch (e.dtype) {
-    case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16, AK>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16, AK>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32, AK>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
-    default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
+  if constexpr (AK) {
+    switch (e.dtype) {
+      case OCTO_BF16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_BF16>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_F16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F16>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_F32: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F32>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
+    }
+  } else {
+    switch (e.dtype) {
+      case OCTO_BF16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_BF16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_F16: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F16>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_F32: hipLaunchKernelGGL((gemm_store_kernel<DT, OCTO_F32>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e); break;
+      default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
+    }
   }
   OCTO_CHECK_LAUNCH("gemm_store");
   return OCTO_OK;
@@ -525,7 +551,7 @@ static int go_store(const Operand &A, const Operand &B, const GemmShape &s, cons
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
                       hipStream_t st, bool a_kmajor) {
   if (a_kmajor) {
-    // OpCols128 reads whole 512-byte rows of the tile's 256 columns from a plain (unmapped) matrix
+    // the K-major loader (OpColsN) reads whole 512-byte rows of the tile's 256 columns of a plain (unmapped) matrix
     if (A.map || (A.ld & 15) || A.ld < 512 || A.ld > 0xffffffffLL / 64 || (uintptr_t)A.base % 16)
       return octo_fail(OCTO_EINVAL, "gemm_store: K-major operand layout");
     switch (dt) {
