@@ -3,9 +3,9 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3] [--no-cpu-baseline]
 
 A step is one pass of the path over one packed micro-batch, inputs resident in HBM:
-  compaction of the scored rows -> fused forward (MFMA GEMM + softmax epilogue, merge, target gather)
-  -> GRPO weight g per flat token -> fused backward (recompute dz, grad_hidden and grad_W GEMMs, row
-  scatter, grad_W to bf16).
+  compaction of the scored rows -> fused forward (MFMA GEMM + softmax epilogue; merge with target gather and the
+  GRPO weight g of each compact row) -> fused backward (recompute dz, grad_hidden and grad_W GEMMs, row scatter,
+  grad_W to bf16).
 Default workload cfg3: N = 32,768 packed tree tokens (an 8,192-token root shared by 12 branches of 2,048,
 root masked: 24,576 scored rows), d = 2560, V = 151,936, bf16, T = 1.0 (octopus_amd.workloads).
 Prints one JSON line: packed tokens/s; per GEMM kernel, its average launch time from HIP events recorded around
@@ -277,22 +277,23 @@ def main() -> int:
         out, lse = head_op.head_fwd(h, W, b.w_scale, y, idx, count, inv_T, 1.0, 1.0, False, True, True)
         return idx, count, out, lse
 
-    def loss_grad(out):
-        return head_op.grpo_loss(out[:, 0], old, None, b.adv, mask_f, 0.2, 0.28, 5.0)
+    def forward_grpo():
+        # the forward with the GRPO weight dL/dlogprob of each compact row computed in its last kernel (ratio
+        # against the rollout's logprobs, eps 0.2 / 0.28, rejection 5.0), ready for the backward
+        idx, count = head_op.compact_rows(b.scored)
+        out, lse, g, loss = head_op.head_fwd_grpo(h, W, b.w_scale, y, idx, count, inv_T, 1.0, 1.0, False, True,
+                                                  True, old, None, b.adv, mask_f, 0.2, 0.28, 5.0)
+        return idx, count, out, lse, g
 
-    def backward(idx, count, lse, g_flat):
-        g = torch.empty(idx.numel(), dtype=torch.float32, device=dev)
-        _lib.call("octo_gather_f32", head_op._p(g_flat), 1, head_op._p(idx), head_op._p(count), idx.numel(),
-                  head_op._p(g), head_op._stream(g))
+    def backward(idx, count, lse, g):
         return head_op.head_bwd(h, W, b.w_scale, y, idx, count, lse, g, inv_T, 1.0, 1.0, False, True, True,
                                 need_w)
 
     def step():
-        idx, count, out, lse = forward()
         if cfg.backward == "none":  # a forward-only workload: logprob and entropy of every scored row
-            return out
-        loss, g_flat = loss_grad(out)
-        return backward(idx, count, lse, g_flat)
+            return forward()[2]
+        idx, count, out, lse, g = forward_grpo()
+        return backward(idx, count, lse, g)
 
     for _ in range(args.warmup):
         step()
@@ -318,13 +319,14 @@ def main() -> int:
     fwd_ms, bwd_ms, reps = [], [], 3
     for _ in range(reps):
         ev[0].record()
-        idx, count, out, lse = forward()
+        if cfg.backward == "none":
+            forward()
+        else:
+            idx, count, out, lse, g = forward_grpo()
         ev[1].record()
-        if cfg.backward != "none":
-            loss, g_flat = loss_grad(out)
         ev[2].record()
         if cfg.backward != "none":
-            backward(idx, count, lse, g_flat)
+            backward(idx, count, lse, g)
         ev[3].record()
         torch.cuda.synchronize()
         fwd_ms.append(ev[0].elapsed_time(ev[1]))

@@ -30,7 +30,8 @@
  *   octopus/rl/prefix_tree.py:156-166 build_tree, label-pair section (np.unique over packed
  *                                     (position, label)) -> octo_label_pairs
  *   AReaL grpo_loss_fn (cited by docs/rl-plan-episodes.md:496-497, constants grpo.yaml:103-118)
- *                                                  -> octo_grpo_grad
+ *                                                  -> octo_grpo_grad, or fused into the forward's
+ *                                                     last step: octo_head_fwd_grpo
  */
 #ifndef OCTO_HEAD_H
 #define OCTO_HEAD_H
@@ -173,6 +174,32 @@ int octo_gather_f32(const float *src, int64_t ld_src, const int64_t *idx, const 
  * weight format of its fp8-weight configuration (per-row scale = absmax / 448) on the device. */
 int octo_quantise_fp8_rows(const void *w, int64_t ldw, int w_dtype, int64_t V, int d,
                            uint8_t *q, int64_t ldq, float *scale, void *stream);
+
+/* octo_head_fwd followed, in its last kernel, by the GRPO weight of each compact row: what octo_grpo_grad computes
+ * for the row's flat token t = (idx ? idx[r] : r) from the row's logprob (the same per-token formula), written in
+ * compact order, so octo_head_bwd can take g directly. Replaces lm_head.py:102-112 (_head_chunk + _head_columns,
+ * as octo_head_fwd) plus the consumer of the head's column 0, AReaL's grpo_loss_fn (docs/rl-plan-episodes.md:
+ * 496-497, grpo.yaml:103-118): dL/dlogprob without a second pass over the tokens.
+ *   grpo->prox, old      : [n_tokens] or NULL (as octo_grpo_grad); adv, mask: [n_tokens]
+ *   Z                    : max(1, count of mask[t] != 0 over all n_tokens) (not only the compact rows)
+ *   grpo->g              : [n_max] fp32, g[r] = dL/dlogp of row r's token (0 when mask[t] == 0 or t >= n_tokens);
+ *                          rows at and after *count are left untouched
+ *   grpo->loss           : NULL or one float, L over the compact rows (the tokens with mask != 0 must be among
+ *                          them for L to be the whole objective); summed with atomics, so its last bits may vary
+ * Workspace as octo_head_fwd. */
+typedef struct octo_grpo_tail {
+  const float *prox, *old, *adv, *mask;
+  int64_t n_tokens;
+  float eps_lo, eps_hi, reject_upper;
+  float *g, *loss;
+} octo_grpo_tail;
+int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
+                       const void *w, int64_t ldw, int w_dtype, const float *w_scale,
+                       const int64_t *labels, const int64_t *idx, const int32_t *count,
+                       int64_t n_max, int d, int V, int flags,
+                       float inv_T, float pre, float post, int use_tanh,
+                       float *logp, float *ent, float *lse, float *out2, int64_t ld_out2,
+                       const octo_grpo_tail *grpo, void *ws, size_t ws_bytes, void *stream);
 
 /* GRPO/PPO policy-gradient weight per token (AReaL grpo_loss_fn semantics):
  *   ratio r = exp(logp - prox)          (prox == NULL: prox = logp, i.e. reuse_train_logp)

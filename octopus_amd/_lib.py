@@ -27,6 +27,14 @@ _i32 = ctypes.c_int
 _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
 
+
+
+class GrpoTail(ctypes.Structure):
+    """octo_grpo_tail: the GRPO weight octo_head_fwd_grpo computes per compact row."""
+    _fields_ = [("prox", _p), ("old", _p), ("adv", _p), ("mask", _p), ("n_tokens", _i64),
+                ("eps_lo", _f32), ("eps_hi", _f32), ("reject_upper", _f32), ("g", _p), ("loss", _p)]
+
+
 # name -> argument types (restype is int unless listed in _RESTYPES)
 SIGNATURES = {
     "octo_version": [],
@@ -37,6 +45,8 @@ SIGNATURES = {
     "octo_compact_rows": [_p, _i64, _p, _p, _p],
     "octo_head_fwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                       _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, _p, _sz, _p],
+    "octo_head_fwd_grpo": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                           _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, ctypes.POINTER(GrpoTail), _p, _sz, _p],
     "octo_head_bwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                       _f32, _f32, _f32, _i32, _p, _p, _p, _i64, _i32, _p, _i32, _p, _sz, _p],
     "octo_columns_fwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p],

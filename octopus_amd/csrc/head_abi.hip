@@ -86,9 +86,9 @@ int staged_dtype(int w_dtype) { return w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_d
 
 struct FwdLayout {
   int64_t mtiles;
-  size_t part, wide, total;
+  size_t part, wide, z, total;
 };
-// part: (m, S, U) per (row, vocab tile). wide: fp8 weights widened to bf16 [V, d].
+// part: (m, S, U) per (row, vocab tile). wide: fp8 weights widened to bf16 [V, d]. z: the GRPO tail's token count.
 FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
   FwdLayout L;
   L.mtiles = cdiv(V, TM);
@@ -96,6 +96,8 @@ FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
   size_t off = align_up((size_t)n_max * L.mtiles * sizeof(f32x4));
   L.wide = off;
   if (w_dtype == OCTO_FP8E4M3) off += align_up((size_t)V * d * 2);
+  L.z = off;
+  off += kAlign;
   L.total = off;
   return L;
 }
@@ -261,6 +263,88 @@ GemmShape shape(int64_t M, int64_t N, int64_t K, int group_m, int count_on, cons
   return s;
 }
 
+int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
+             const float *w_scale, const int64_t *labels, const int64_t *idx, const int32_t *count, int64_t n_max,
+             int d, int V, int flags, float inv_T, float pre, float post, int use_tanh, float *logp, float *ent,
+             float *lse, float *out2, int64_t ld_out2, const octo_grpo_tail *gt, void *ws, size_t ws_bytes,
+             void *stream) {
+  Common cm;
+  int rc = check_common(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, n_max, d, V, flags, inv_T,
+                        pre, post, use_tanh, cm);
+  if (rc) return rc;
+  OCTO_CHECK_ARG(!out2 || ld_out2 >= 2, "head_fwd: ld_out2 < 2");
+  if (gt) {
+    OCTO_CHECK_ARG(gt->n_tokens >= 0, "head_fwd_grpo: n_tokens < 0");
+    OCTO_CHECK_ARG(gt->g && gt->adv && gt->mask, "head_fwd_grpo: null g, adv or mask");
+  }
+  if (n_max == 0) return OCTO_OK;
+  const FwdLayout L = fwd_layout(n_max, d, V, w_dtype);
+  if (!ws || ws_bytes < L.total)
+    return octo_fail(OCTO_EWORKSPACE, "head_fwd: workspace %zu < %zu bytes", ws_bytes, L.total);
+  hipStream_t st = (hipStream_t)stream;
+  float *z = (float *)((char *)ws + L.z);
+  if (gt) {  // Z (and the loss zeroed) ahead of the merge
+    rc = launch_grpo_count(gt->mask, gt->n_tokens, z, gt->loss, st);
+    if (rc) return rc;
+  }
+
+  const Operand A = gemm_weight(w, ldw, cm, V, d, (char *)ws + L.wide, st, rc);
+  if (rc) return rc;
+  const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
+  const GemmShape s = shape(V, n_max, d, kGroupM, 2, count, 0);
+  StatsArgs e;
+  e.part = (f32x4 *)((char *)ws + L.part);
+  e.mtiles = L.mtiles;
+  e.V = V;
+  e.wscale = w_scale;
+  e.c = cm.c;
+  e.pre = cm.pre;
+  {
+    TimedLaunch t("gemm_stats", st);
+    rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, A, B, s, e, st);
+  }
+  if (rc) return rc;
+
+  MergeArgs m;
+  m.part = e.part;
+  m.mtiles = L.mtiles;
+  m.h = h;
+  m.ldh = ldh;
+  m.h_dtype = h_dtype;
+  m.w = w;
+  m.ldw = ldw;
+  m.w_dtype = w_dtype;
+  m.wscale = w_scale;
+  m.labels = labels;
+  m.idx = idx;
+  m.count = count;
+  m.n_max = n_max;
+  m.d = d;
+  m.V = V;
+  m.flags = flags;
+  m.inv_T = inv_T;
+  m.pre = pre;
+  m.post = post;
+  m.use_tanh = use_tanh;
+  m.logp = logp;
+  m.ent = ent;
+  m.lse = lse;
+  m.out2 = out2;
+  m.ld_out2 = ld_out2;
+  m.gprox = gt ? gt->prox : nullptr;
+  m.gold = gt ? gt->old : nullptr;
+  m.gadv = gt ? gt->adv : nullptr;
+  m.gmask = gt ? gt->mask : nullptr;
+  m.n_tokens = gt ? gt->n_tokens : 0;
+  m.eps_lo = gt ? gt->eps_lo : 0.f;
+  m.eps_hi = gt ? gt->eps_hi : 0.f;
+  m.reject_upper = gt ? gt->reject_upper : 0.f;
+  m.z = z;
+  m.g = gt ? gt->g : nullptr;
+  m.loss = gt ? gt->loss : nullptr;
+  return launch_merge(m, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -315,61 +399,18 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
                   int64_t n_max, int d, int V, int flags, float inv_T, float pre, float post, int use_tanh,
                   float *logp, float *ent, float *lse, float *out2, int64_t ld_out2, void *ws, size_t ws_bytes,
                   void *stream) {
-  Common cm;
-  int rc = check_common(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, n_max, d, V, flags, inv_T,
-                        pre, post, use_tanh, cm);
-  if (rc) return rc;
-  OCTO_CHECK_ARG(!out2 || ld_out2 >= 2, "head_fwd: ld_out2 < 2");
-  if (n_max == 0) return OCTO_OK;
-  const FwdLayout L = fwd_layout(n_max, d, V, w_dtype);
-  if (!ws || ws_bytes < L.total)
-    return octo_fail(OCTO_EWORKSPACE, "head_fwd: workspace %zu < %zu bytes", ws_bytes, L.total);
-  hipStream_t st = (hipStream_t)stream;
+  return head_fwd(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
+                  pre, post, use_tanh, logp, ent, lse, out2, ld_out2, nullptr, ws, ws_bytes, stream);
+}
 
-  const Operand A = gemm_weight(w, ldw, cm, V, d, (char *)ws + L.wide, st, rc);
-  if (rc) return rc;
-  const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
-  const GemmShape s = shape(V, n_max, d, kGroupM, 2, count, 0);
-  StatsArgs e;
-  e.part = (f32x4 *)((char *)ws + L.part);
-  e.mtiles = L.mtiles;
-  e.V = V;
-  e.wscale = w_scale;
-  e.c = cm.c;
-  e.pre = cm.pre;
-  {
-    TimedLaunch t("gemm_stats", st);
-    rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, A, B, s, e, st);
-  }
-  if (rc) return rc;
-
-  MergeArgs m;
-  m.part = e.part;
-  m.mtiles = L.mtiles;
-  m.h = h;
-  m.ldh = ldh;
-  m.h_dtype = h_dtype;
-  m.w = w;
-  m.ldw = ldw;
-  m.w_dtype = w_dtype;
-  m.wscale = w_scale;
-  m.labels = labels;
-  m.idx = idx;
-  m.count = count;
-  m.n_max = n_max;
-  m.d = d;
-  m.V = V;
-  m.flags = flags;
-  m.inv_T = inv_T;
-  m.pre = pre;
-  m.post = post;
-  m.use_tanh = use_tanh;
-  m.logp = logp;
-  m.ent = ent;
-  m.lse = lse;
-  m.out2 = out2;
-  m.ld_out2 = ld_out2;
-  return launch_merge(m, st);
+int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw,
+                       int w_dtype, const float *w_scale, const int64_t *labels, const int64_t *idx,
+                       const int32_t *count, int64_t n_max, int d, int V, int flags, float inv_T, float pre,
+                       float post, int use_tanh, float *logp, float *ent, float *lse, float *out2, int64_t ld_out2,
+                       const octo_grpo_tail *grpo, void *ws, size_t ws_bytes, void *stream) {
+  OCTO_CHECK_ARG(grpo != nullptr, "head_fwd_grpo: null grpo");
+  return head_fwd(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
+                  pre, post, use_tanh, logp, ent, lse, out2, ld_out2, grpo, ws, ws_bytes, stream);
 }
 
 int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,

@@ -63,6 +63,9 @@ __device__ __forceinline__ float row_dot(const void *h, int h_dtype, int64_t hof
   return dot;
 }
 
+__device__ __forceinline__ void grpo_token(float lp, const float *prox, const float *old, float A, float eps_lo,
+                                           float eps_hi, float reject_upper, float inv_z, float &gt, float &lt);
+
 // ---- merge: vocab-tile partials -> per-row outputs ----------------------------------------------
 // One wave per compact row: lanes merge the row's partials (m, S, U) strided by 64, then a wave
 // butterfly; the target logit h_r . W_y is a wave dot product in fp32.
@@ -101,6 +104,14 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     const int64_t orow = (a.flags & OCTO_OUT_SCATTER) ? hrow : r;
     a.out2[orow * a.ld_out2] = lp;
     a.out2[orow * a.ld_out2 + 1] = ent;
+  }
+  if (a.g) {  // the GRPO weight of the row's token, in compact order
+    float gt = 0.f, lt = 0.f;
+    if (hrow < a.n_tokens && a.gmask[hrow] != 0.f)
+      grpo_token(lp, a.gprox ? a.gprox + hrow : nullptr, a.gold ? a.gold + hrow : nullptr, a.gadv[hrow], a.eps_lo,
+                 a.eps_hi, a.reject_upper, 1.f / a.z[0], gt, lt);
+    a.g[r] = gt;
+    if (a.loss && lt != 0.f) atomicAdd(a.loss, lt);
   }
 }
 
@@ -432,6 +443,36 @@ __global__ __launch_bounds__(1024) void grpo_count_kernel(const float *mask, int
   }
 }
 
+int launch_grpo_count(const float *mask, int64_t n, float *z, float *loss, hipStream_t st) {
+  hipLaunchKernelGGL(grpo_count_kernel, dim3(1), dim3(1024), 0, st, mask, n, z, loss);
+  OCTO_CHECK_LAUNCH("grpo_count");
+  return OCTO_OK;
+}
+
+// The objective's term and dL/dlogp of one token with mask != 0 (logp lp; prox, old as pointers to its entries
+// or NULL), both already divided by Z.
+__device__ __forceinline__ void grpo_token(float lp, const float *prox, const float *old, float A, float eps_lo,
+                                           float eps_hi, float reject_upper, float inv_z, float &gt, float &lt) {
+  const float px = prox ? *prox : lp;
+  const float r = expf(lp - px);
+  float w = 1.f;
+  if (old) {
+    w = expf(px - *old);
+    if (reject_upper > 0.f && w > reject_upper) w = 0.f;
+  }
+  const float lo = 1.f - eps_lo, hi = 1.f + eps_hi;
+  const float cl = fminf(fmaxf(r, lo), hi);
+  const float a = -A * r, b = -A * cl;
+  const bool inside = (r >= lo) && (r <= hi);
+  float ga, gb;
+  if (a > b) { ga = 1.f; gb = 0.f; }
+  else if (a < b) { ga = 0.f; gb = 1.f; }
+  else { ga = 0.5f; gb = 0.5f; }
+  const float dmax_dr = ga * (-A) + gb * (-A) * (inside ? 1.f : 0.f);
+  gt = w * dmax_dr * r * inv_z;
+  lt = w * fmaxf(a, b) * inv_z;
+}
+
 __global__ __launch_bounds__(256) void grpo_grad_kernel(const float *logp, const float *prox, const float *old,
                                                         const float *adv, const float *mask, int64_t n,
                                                         float eps_lo, float eps_hi, float reject_upper,
@@ -440,29 +481,9 @@ __global__ __launch_bounds__(256) void grpo_grad_kernel(const float *logp, const
   float lt = 0.f;
   if (t < n) {
     float gt = 0.f;
-    if (mask[t] != 0.f) {
-      const float inv_z = 1.f / ws[0];
-      const float lp = logp[t];
-      const float px = prox ? prox[t] : lp;
-      const float r = expf(lp - px);
-      float w = 1.f;
-      if (old) {
-        w = expf(px - old[t]);
-        if (reject_upper > 0.f && w > reject_upper) w = 0.f;
-      }
-      const float A = adv[t];
-      const float lo = 1.f - eps_lo, hi = 1.f + eps_hi;
-      const float cl = fminf(fmaxf(r, lo), hi);
-      const float a = -A * r, b = -A * cl;
-      const bool inside = (r >= lo) && (r <= hi);
-      float ga, gb;
-      if (a > b) { ga = 1.f; gb = 0.f; }
-      else if (a < b) { ga = 0.f; gb = 1.f; }
-      else { ga = 0.5f; gb = 0.5f; }
-      const float dmax_dr = ga * (-A) + gb * (-A) * (inside ? 1.f : 0.f);
-      gt = w * dmax_dr * r * inv_z;
-      lt = w * fmaxf(a, b) * inv_z;
-    }
+    if (mask[t] != 0.f)
+      grpo_token(logp[t], prox ? prox + t : nullptr, old ? old + t : nullptr, adv[t], eps_lo, eps_hi, reject_upper,
+                 1.f / ws[0], gt, lt);
     g[t] = gt;
   }
   if (loss) {

@@ -96,14 +96,21 @@ struct MergeArgs {
   int use_tanh;
   float *logp, *ent, *lse, *out2;
   int64_t ld_out2;
+  // GRPO weight of each compact row (g != NULL): per-token arrays indexed by the row's flat token
+  const float *gprox, *gold, *gadv, *gmask;
+  int64_t n_tokens;
+  float eps_lo, eps_hi, reject_upper;
+  const float *z;  // max(1, masked-token count), from launch_grpo_count
+  float *g, *loss;
 };
 int launch_merge(const MergeArgs &a, hipStream_t st);
+// z[0] = max(1, count of mask[t] != 0, t < n); *loss = 0 when loss != NULL. One workgroup.
+int launch_grpo_count(const float *mask, int64_t n, float *z, float *loss, hipStream_t st);
 
-// dst[c * ld_dst + r] = src row r, element c, for r < rows_pad, c < cols; rows r >= valid read 0.
-// Source row r is row map[r] (or r) of src; dst holds the staged MFMA type (bf16/f16/f32).
-// dst[r, c] = src row map[r] (or r), element c, for r < rows_pad, c < cols; rows r at or past the valid count read 0.
-// Same dtype on both sides (a byte copy of 16-bit or 32-bit elements).
+// dst[r * d + c] = bf16(e4m3 w[r * ldw + c]) for r < V, c < d (exact).
 int launch_widen_fp8(const void *w, int64_t ldw, int64_t V, int d, void *dst, hipStream_t st);
+// dst[c * ld_dst + r] = src row map[r] (or r), element c, for r < rows_pad, c < cols; rows at or past the valid
+// count (count - count_off, capped at rows) read 0; dst holds the staged MFMA type (bf16/f16/f32).
 int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *src_scale,
                      const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
                      int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st);

@@ -96,6 +96,48 @@ def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, lab
     return out, rows.new_empty(n_max, dtype=torch.float32)
 
 
+@torch.library.custom_op("octohead::head_fwd_grpo", mutates_args=(), device_types="cuda")
+def head_fwd_grpo(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Tensor, idx: Optional[Tensor],
+                  count: Optional[Tensor], inv_T: float, pre: float, post: float, use_tanh: bool,
+                  labels_via_idx: bool, scatter: bool, prox: Optional[Tensor], old: Optional[Tensor], adv: Tensor,
+                  mask: Tensor, eps_lo: float, eps_hi: float,
+                  reject_upper: float) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """head_fwd plus the GRPO weight of each compact row (octo_head_fwd_grpo): (out, lse, g, loss) with
+    g [n] fp32 = dL/dlogprob of compact row r's token (idx[r], or r), in compact order, ready for head_bwd;
+    prox, old, adv, mask are per flat token, as grpo_loss takes them."""
+    rows, weight = _rows2d(rows), _rows2d(weight)
+    labels, idx = _index(labels), _index(idx)
+    n_max = idx.numel() if idx is not None else rows.shape[0]
+    V, d = weight.shape
+    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | (_lib.OUT_SCATTER if scatter else 0)
+    out = torch.zeros(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32, device=rows.device)
+    lse = torch.zeros(n_max, dtype=torch.float32, device=rows.device)
+    g = torch.zeros(n_max, dtype=torch.float32, device=rows.device)
+    loss = torch.zeros((), dtype=torch.float32, device=rows.device)
+    if n_max == 0:
+        return out, lse, g, loss
+    f = lambda t: None if t is None else t.float().contiguous().reshape(-1)  # noqa: E731
+    prox_, old_, adv_, mask_ = f(prox), f(old), f(adv), f(mask)
+    tail = _lib.GrpoTail(_p(prox_), _p(old_), _p(adv_), _p(mask_), adv_.numel(), eps_lo, eps_hi, reject_upper,
+                         _p(g), _p(loss))
+    w_code = _dtype_code(weight)
+    ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, 0), rows)
+    _lib.call("octo_head_fwd_grpo", _p(rows), rows.shape[0], rows.stride(0), _dtype_code(rows),
+              _p(weight), weight.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
+              n_max, d, V, flags, inv_T, pre, post, int(use_tanh),
+              None, None, _p(lse), _p(out), 2, ctypes.byref(tail), _p(ws), ws.numel(), _stream(rows))
+    return out, lse, g, loss
+
+
+@head_fwd_grpo.register_fake
+def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, labels_via_idx, scatter, prox, old, adv,
+      mask, eps_lo, eps_hi, reject_upper):
+    n_max = idx.shape[0] if idx is not None else rows.shape[0]
+    out = rows.new_empty(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32)
+    return (out, rows.new_empty(n_max, dtype=torch.float32), rows.new_empty(n_max, dtype=torch.float32),
+            rows.new_empty((), dtype=torch.float32))
+
+
 @torch.library.custom_op("octohead::head_bwd", mutates_args=(), device_types="cuda")
 def head_bwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Tensor, idx: Optional[Tensor],
              count: Optional[Tensor], lse: Tensor, g: Tensor, inv_T: float, pre: float, post: float,

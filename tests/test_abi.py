@@ -97,6 +97,13 @@ def test_small_entry_point_checks():
         _lib.call("octo_label_pairs", P, 7, P, 2, P, 5, None, P, P, P, P, 8, P, 1 << 20, None)
     with pytest.raises(ValueError):  # no workspace
         _lib.call("octo_label_pairs", P, 7, P, 2, P, 5, None, P, P, P, P, 0, None, 0, None)
+    fwd = (P, 10, 64, _lib.BF16, P, 64, _lib.BF16, None, P, None, None, 10, 64, 100, 0, 1.0, 1.0, 1.0, 0,
+           None, None, None, None, 2)
+    with pytest.raises(ValueError):  # no GRPO tail
+        _lib.call("octo_head_fwd_grpo", *fwd, None, P, 1 << 30, None)
+    tail = _lib.GrpoTail(None, None, None, P, 10, 0.2, 0.28, 5.0, P, None)
+    with pytest.raises(ValueError):  # no advantages
+        _lib.call("octo_head_fwd_grpo", *fwd, ctypes.byref(tail), P, 1 << 30, None)
 
 
 def test_timing_hook_without_launches():

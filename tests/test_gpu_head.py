@@ -353,3 +353,36 @@ def test_fp8_row_quantiser_at_full_size_feeds_the_head():
     a = fused_head(h, q, y, 1.0, w_scale=scale)
     b = fused_head(h, tq, y, 1.0, w_scale=ts)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("variant", ["prox", "old", "prox+old"])
+def test_forward_grpo_tail_matches_unfused(dtype, variant):
+    """octo_head_fwd_grpo: the forward's outputs as octo_head_fwd's; g per compact row as octo_grpo_grad's on the
+    forward's logprobs, gathered to compact order; the loss as its loss up to summation order; both against the
+    oracle's GRPO restatement. The loss mask is a strict subset of the scored rows, so Z and the zero rows matter."""
+    N, d, V = 1500, 64, 3000
+    h, W, y = _inputs(N, d, V, dtype, seed=11)
+    gen = torch.Generator().manual_seed(12)
+    scored = torch.rand(N, generator=gen) < 0.6
+    mask = (scored & (torch.rand(N, generator=gen) < 0.8)).float()
+    adv = torch.randn(N, generator=gen)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    idx, count = head_op.compact_rows(scored.to(DEV))
+    out, lse = head_op.head_fwd(hd, Wd, None, yd, idx, count, 1.0, 1.0, 1.0, False, True, True)
+    lp = out[:, 0].cpu()
+    prox = (lp + 0.3 * torch.randn(N, generator=gen)) if "prox" in variant else None
+    old = (lp + 0.5 * torch.randn(N, generator=gen)) if "old" in variant else None
+    dv = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    out2, lse2, g2, loss2 = head_op.head_fwd_grpo(hd, Wd, None, yd, idx, count, 1.0, 1.0, 1.0, False, True, True,
+                                                  dv(prox), dv(old), adv.to(DEV), mask.to(DEV), 0.2, 0.28, 5.0)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    loss1, g1 = head_op.grpo_loss(out[:, 0], dv(prox), dv(old), adv.to(DEV), mask.to(DEV), 0.2, 0.28, 5.0)
+    n = int(count.item())
+    assert n == int(scored.sum())
+    torch.testing.assert_close(g2[:n], g1[idx[:n]], rtol=1e-6, atol=0)
+    assert abs(loss2.item() - loss1.item()) <= 1e-5 * max(1.0, abs(loss1.item()))
+    lo, go = ogrpo.grpo(lp.numpy(), adv.numpy(), mask.numpy(), prox=None if prox is None else prox.numpy(),
+                        old=None if old is None else old.numpy())
+    assert np.abs(g2[:n].cpu().double().numpy() - go[idx[:n].cpu().numpy()]).max() <= 1e-6
+    assert abs(loss2.item() - lo) <= 1e-5 * max(1.0, abs(lo))
