@@ -445,12 +445,19 @@ template <> struct Mfma16<OCTO_F16> {
 // K-steps, after the last reads of stage k. DMA: issue stage kd of the operands' current tile (stage k + 2 of the
 // stream: A under K-step 0, B under K-step 1, one instruction per 6 MFMAs). NEXT: a stage k + 1 exists (barrier B_k);
 // XFRAG: its first fragments are read under K-step 1 (else the caller reads them).
-template <int DT, typename OA, typename OB, bool DMA, bool NEXT, bool XFRAG = NEXT>
+// SPLIT: B_k only frees stage k's slots; the wait for stage k + 1 (vmcnt, then a second barrier L_k) moves to the
+// middle of K-step 1, and stage k + 1's first fragments are read after L_k. The wait then covers DMA issued half a
+// K-step longer ago, for a second barrier per stage.
+template <int DT, typename OA, typename OB, bool DMA, bool NEXT, bool XFRAG, bool SPLIT>
 __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd, int sa, uint32_t kbytes,
                                             lds_char *smem, typename OA::F (&fa)[2][OA::NB],
                                             typename OB::F (&fb)[2][OB::NB], f32x4 (&acc)[OA::NB][OB::NB]) {
   constexpr int NA = OA::NB, NBB = OB::NB, NQ = NA * NBB, NR = NA + NBB, NI = OA::NI;
   constexpr int D0 = NR + 1, DS = (NQ - D0 + NI - 1) / NI;  // DMA issues: MFMA D0, D0 + DS, ... (4 waves: 17 + 6 j)
+  // SPLIT: L_k at MFMA QX; DQX DMA instructions of this K-step are issued before it
+  constexpr int QX = NQ / 2, DQX = QX <= D0 ? 0 : ((QX - 1 - D0) / DS + 1 < NI ? (QX - 1 - D0) / DS + 1 : NI);
+  static_assert(!SPLIT || QX + NR <= NQ, "next-stage fragment reads fit the K-step");
+  constexpr int XQ = SPLIT ? QX : 0;  // first MFMA under which stage k + 1's fragments are read
   // slots: stage k at (sa, sa + 1), stage k + 1 at (sa + 2, sa + 3), stage k + 2's A at sa + 4, its B at sa
   auto slot = [&](int d) -> lds_char * { const int x = sa + d; return smem + (x >= ENSLOT ? x - ENSLOT : x) * ESLICE; };
   const lds_char *cA = slot(0), *cB = slot(1);
@@ -460,8 +467,10 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd
   for (int ks = 0; ks < 2; ++ks) {
     if (ks == 1 && NEXT) {
       __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // this wave's reads of stage k are done
-      if (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NI));  // stage k + 1 landed (k + 2's A may be in flight)
-      else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      if (!SPLIT) {
+        if (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NI));  // stage k + 1 landed (k + 2's A may be in flight)
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      }
       __builtin_amdgcn_s_barrier();  // ... in every wave; stage k's slots are free
     } else {
       __builtin_amdgcn_s_waitcnt(WAIT_LGKM0);  // this K-step's fragments are in
@@ -469,18 +478,23 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd
     OCTO_FENCE();
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
+      if (SPLIT && ks == 1 && NEXT && q == QX) {
+        // L_k: stage k + 1 landed (stage k + 2's A and this K-step's first B issues may be in flight) ... everywhere
+        if (DMA) __builtin_amdgcn_s_waitcnt(waitcnt_vm(NI + DQX));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        __builtin_amdgcn_s_barrier();
+        OCTO_FENCE();
+      }
       Mfma16<DT>::run(OA::op(fa[ks][q / NBB]), OB::op(fb[ks][q % NBB]), acc[q / NBB][q % NBB]);
       OCTO_FENCE();
-      if (q < NR) {
-        if (ks == 0) {
-          if (q < NA) fa[1][q] = opa.frag(cA, 1, q);
-          else fb[1][q - NA] = opb.frag(cB, 1, q - NA);
-          OCTO_FENCE();
-        } else if (NEXT && XFRAG) {
-          if (q < NA) fa[0][q] = opa.frag(nA, 0, q);
-          else fb[0][q - NA] = opb.frag(nB, 0, q - NA);
-          OCTO_FENCE();
-        }
+      if (ks == 0 && q < NR) {
+        if (q < NA) fa[1][q] = opa.frag(cA, 1, q);
+        else fb[1][q - NA] = opb.frag(cB, 1, q - NA);
+        OCTO_FENCE();
+      } else if (ks == 1 && NEXT && XFRAG && q >= XQ && q < XQ + NR) {
+        if (q - XQ < NA) fa[0][q - XQ] = opa.frag(nA, 0, q - XQ);
+        else fb[0][q - XQ - NA] = opb.frag(nB, 0, q - XQ - NA);
+        OCTO_FENCE();
       }
       if (DMA && q >= D0 && (q - D0) % DS == 0 && (q - D0) / DS < NI) {
         if (ks == 0) opa.dma(kd, (q - D0) / DS, kbytes, dA);
@@ -492,7 +506,7 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd
 }
 
 // smem: SMEM_RING5 bytes. 16-bit types only.
-template <int DT, typename OA, typename OB>
+template <int DT, typename OA, typename OB, bool SPLIT = false>
 __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &B, int64_t m0, int64_t n0,
                                                int64_t K_eff, lds_char *smem, f32x4 (&acc)[OA::NB][OB::NB]) {
   static_assert(DT == OCTO_BF16 || DT == OCTO_F16, "16-bit operands");
@@ -541,15 +555,15 @@ __device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &
   int sa = 0;  // slot of stage k's A slice: 2 k mod 5
   int k = 0;
   for (; k + 2 < nk; ++k) {
-    ring5_stage<DT, OA, OB, true, true>(opa, opb, k + 2, sa, kbytes, smem, fa, fb, acc);
+    ring5_stage<DT, OA, OB, true, true, true, SPLIT>(opa, opb, k + 2, sa, kbytes, smem, fa, fb, acc);
     sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
   }
   if (k + 1 < nk) {
-    ring5_stage<DT, OA, OB, false, true>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
+    ring5_stage<DT, OA, OB, false, true, true, SPLIT>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
     sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
     ++k;
   }
-  ring5_stage<DT, OA, OB, false, false>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
+  ring5_stage<DT, OA, OB, false, false, false, SPLIT>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
   __builtin_amdgcn_s_barrier();
 }

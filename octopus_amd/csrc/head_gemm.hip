@@ -437,10 +437,11 @@ __device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::N
   }
 }
 
+// fp32 gradient GEMMs (4-stage loop, 32 x 32 MFMAs).
 template <int DT, int OT>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
-  constexpr bool R5 = ring5_ok(DT);
-  __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
+  static_assert(!ring5_ok(DT), "16-bit operands run gemm_store8_kernel");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
@@ -449,22 +450,16 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (s.count_on == 1) mvalid = dev_count(s.count, s.count_off + m0, mvalid);
   if (s.count_on == 3) K_eff = round_up(dev_count(s.count, s.count_off, s.K), 64);
   if (mvalid <= 0 || nvalid <= 0) return;
-
-  if constexpr (R5) {
-    f32x4 acc[8][8];
-    mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, K_eff, smem, acc);
-    store_any<Acc16, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
-  } else {
-    f32x16 acc[4][4];
-    mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
-    store_any<Acc32, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
-  }
+  f32x16 acc[4][4];
+  mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
+  store_any<Acc32, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
 }
 
-// grad_W's 8-wave form: 512 threads, two waves per SIMD, each 128 x 64 of the tile, A (dz) K-major. A K-major
-// fragment is two transposing LDS reads, and the second wave on each SIMD issues MFMAs while one waits on them
-// (same box: 13.6 against 14.1 ms for the 4-wave form at cfg3; grad_h, K-contiguous, is 0.5 ms slower in it).
-template <int DT, int OT>
+// The 16-bit gradient GEMMs' 8-wave form: 512 threads, two waves per SIMD, each 128 x 64 of the tile; the second
+// wave on each SIMD issues MFMAs while one waits. grad_W (AK: dz read K-major by transposing LDS reads) keeps one
+// barrier per stage; grad_h (K-contiguous) waits for the next stage half-way through the K-step (SPLIT). Same box,
+// cfg3: grad_W 13.6 against 14.1 ms and grad_h 13.9 against 14.4 ms for the 4-wave form.
+template <int DT, int OT, bool AK>
 __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_store8_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
   static_assert(ring5_ok(DT), "16-bit operands");
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
@@ -477,7 +472,8 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   if (s.count_on == 3) K_eff = round_up(dev_count(s.count, s.count_off, s.K), 64);
   if (mvalid <= 0 || nvalid <= 0) return;
   f32x4 acc[8][4];
-  mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
+  if constexpr (AK) mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
+  else mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
   store_any<Acc16N<4>, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
 }
 
@@ -529,11 +525,11 @@ int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operan
 
 template <int DT, bool AK>
 static int go_store(const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e, hipStream_t st) {
-  if constexpr (AK) {
+  if constexpr (ring5_ok(DT)) {
     switch (e.dtype) {
-      case OCTO_BF16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_BF16>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
-      case OCTO_F16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F16>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
-      case OCTO_F32: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F32>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_BF16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_BF16, AK>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_F16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F16, AK>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_F32: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F32, AK>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
       default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
     }
   } else {
