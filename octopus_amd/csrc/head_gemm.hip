@@ -107,7 +107,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
   const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
-  const int64_t nvalid = dev_count(s.count, s.count_off + n0, s.N - n0);
+  const int64_t nvalid = min(dev_count(s.count, s.count_off + n0, s.N - n0), (int64_t)TN);  // this tile's tokens
   if (nvalid <= 0) return;
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
@@ -162,13 +162,14 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi, f16x2_t *) {
 
 // Stream a 256 x 512-byte LDS tile (rows stored with slot swizzle `s(row)` on 8-byte slots) to global
 // rows dst + row * ld_bytes, 16 bytes per thread per row-eighth.
-template <typename SWZ>
+template <int NT = NTHREADS, typename SWZ>
 __device__ __forceinline__ void lds_tile_to_global(const lds_char *tile, char *dst, int64_t ld_bytes, SWZ swz) {
+  constexpr int RPP = NT / 32;  // rows per pass
   const int t = threadIdx.x;
   const int c16 = t & 31;
 #pragma unroll 4
-  for (int p = 0; p < 32; ++p) {
-    const int row = p * 8 + (t >> 5);
+  for (int p = 0; p < 256 / RPP; ++p) {
+    const int row = p * RPP + (t >> 5);
     const int s = swz(row);
     // logical slots 2c, 2c+1 sit at physical (2c ^ s, (2c+1) ^ s): one aligned 16-byte pair, its halves
     // swapped when s is odd
@@ -268,16 +269,14 @@ __device__ __forceinline__ void dz_store_direct(const f32x16 (&acc)[4][4], const
 
 // 16-bit dz through one LDS staging tile T (the ring, free after the mainloop): T[t] holds dz of token t (tile
 // column) over the tile's 256 vocabulary rows, as 64 slots of 8 bytes (4 consecutive rows); logical slot s of token t
-// sits at physical slot s ^ swz(t), the swizzle chosen for the accumulator layout so that all three accesses are free
+// sits at physical slot s ^ swz(t), the swizzle chosen for the accumulator layout so that both accesses are free
 // of bank conflicts:
-//   - the accumulator writes (Acc16: a half-wave = 16 tokens x 2 adjacent slots);
-//   - the token-major read-back (16 lanes: one token, 16 consecutive 16-byte pairs);
-//   - the vocab-major read-back by transposing reads (16 lanes: 16 tokens t & 31 in {8k + e}, one slot; the two
-//     16-lane groups of a 32-lane pass differ in bit 5 of t, which moves their slots to disjoint sets).
+//   - the accumulator writes (Acc16N: a half-wave = 16 consecutive tokens x 2 adjacent slots, for 4 and 8 waves);
+//   - the token-major read-back (16 lanes: one token, 16 consecutive 16-byte pairs).
 // The dense pass writes -g p / T x post' (x fp8 row scale) everywhere; after a barrier one thread per token writes the
 // label entry (launch_hit's value) over it, so no element is compared against the label.
 template <class L> struct DzSwz;
-template <> struct DzSwz<Acc16> {
+template <int NJ> struct DzSwz<Acc16N<NJ>> {
   static __device__ __forceinline__ int at(int t) { return (((t & 15) << 1) | ((t >> 4) & 1)) ^ (((t >> 5) & 1) << 3); }
 };
 
@@ -334,7 +333,7 @@ __device__ __forceinline__ void dz_stage(const typename L::V (&acc)[L::NI][L::NJ
   }
 }
 
-template <class L, typename P2>
+template <class L, typename P2, int NT = NTHREADS>
 __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0, int64_t nvalid, lds_char *tile) {
   typedef typename std::conditional<std::is_same<P2, bf16x2>::value, __bf16, _Float16>::type ET;
   const int t = threadIdx.x;
@@ -356,7 +355,7 @@ __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0
   }
   __syncthreads();
   if (e.dzA)  // [token][vocab]: 512-byte rows
-    lds_tile_to_global(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return DzSwz<L>::at(row); });
+    lds_tile_to_global<NT>(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return DzSwz<L>::at(row); });
 }
 
 template <int DT, bool A_FP8, bool TANH>
@@ -367,7 +366,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
   const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
-  const int64_t nvalid = dev_count(s.count, s.count_off + n0, s.N - n0);
+  const int64_t nvalid = min(dev_count(s.count, s.count_off + n0, s.N - n0), (int64_t)TN);  // this tile's tokens
   if (nvalid <= 0) return;
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
@@ -477,20 +476,80 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   store_any<Acc16N<4>, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
 }
 
+// The logits-shaped GEMMs on the 8-wave loop (16-bit operands): 512 threads, two waves per SIMD, each 128 x 64, with
+// the split stage barrier. Same box, cfg3 (against the 4-wave loop): gemm_stats 14.3 against 15.1 ms, gemm_dz 15.3
+// against 16.5 ms; without the split barrier gemm_dz was 0.4 ms slower than the 4-wave loop.
+template <int DT, bool A_FP8, bool TANH>
+__global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_stats8_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
+  static_assert(ring5_ok(DT), "16-bit operands");
+  typedef Acc16N<4> L;
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
+  lds_char *smem = (lds_char *)smem_;
+  int mt, nt;
+  if (!tile_of(s, mt, nt)) return;
+  const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
+  const int64_t nvalid = min(dev_count(s.count, s.count_off + n0, s.N - n0), (int64_t)TN);  // this tile's tokens
+  if (nvalid <= 0) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = L::wm(w), wn = L::wn(w);
+  lds_f32x4 *red = (lds_f32x4 *)smem;
+  f32x4 acc[8][4];
+  mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, s.K, smem, acc);
+  pre_transform<L, A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+  if (m0 + TM > e.V) stats_cols<L, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  else stats_cols<L, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < nvalid) {
+    const f32x4 a = red[t], b = red[256 + t];
+    Stat3 sa{a[0], a[1], a[2]}, sb{b[0], b[1], b[2]};
+    Stat3 r = stat_merge(sa, sb);
+    f32x4 o;
+    o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
+    e.part[(n0 + t) * e.mtiles + mt] = o;
+  }
+}
+
+template <int DT, bool A_FP8, bool TANH>
+__global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_dz8_kernel(Operand A, Operand B, GemmShape s, DzArgs e) {
+  static_assert(ring5_ok(DT), "16-bit operands");
+  typedef Acc16N<4> L;
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
+  lds_char *smem = (lds_char *)smem_;
+  int mt, nt;
+  if (!tile_of(s, mt, nt)) return;
+  const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
+  const int64_t nvalid = min(dev_count(s.count, s.count_off + n0, s.N - n0), (int64_t)TN);  // this tile's tokens
+  if (nvalid <= 0) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = L::wm(w), wn = L::wn(w);
+  typedef typename std::conditional<DT == OCTO_BF16, bf16x2, f16x2_t>::type P2;
+  f32x4 acc[8][4];
+  mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, s.K, smem, acc);
+  if constexpr (A_FP8) pre_transform<L, true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+  if (m0 + TM > e.V) dz_stage<L, P2, A_FP8, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+  else dz_stage<L, P2, A_FP8, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+  dz_write<L, P2, 2 * NTHREADS>(e, m0, n0, nvalid, smem);
+}
+
 // ---- host launchers ----------------------------------------------------------------------------
 
 static inline dim3 grid_of(const GemmShape &s) { return dim3((unsigned)tile_grid(s.mtiles, s.ntiles)); }
 
 template <int DT, bool F8, bool TH>
 static int go_stats(const Operand &A, const Operand &B, const GemmShape &s, const StatsArgs &e, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_stats_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
+  if constexpr (ring5_ok(DT))
+    hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
+  else
+    hipLaunchKernelGGL((gemm_stats_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
   OCTO_CHECK_LAUNCH("gemm_stats");
   return OCTO_OK;
 }
 
 template <int DT, bool F8, bool TH>
 static int go_dz(const Operand &A, const Operand &B, const GemmShape &s, const DzArgs &e, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_dz_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
+  if constexpr (ring5_ok(DT))
+    hipLaunchKernelGGL((gemm_dz8_kernel<DT, F8, TH>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
+  else
+    hipLaunchKernelGGL((gemm_dz_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
   OCTO_CHECK_LAUNCH("gemm_dz");
   return OCTO_OK;
 }
