@@ -103,10 +103,15 @@ FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
 }
 
 
-// The backward stages the gradient GEMMs' operands so each mainloop row fetch is whole cache lines: W^T [d, V_pad]
-// for grad_h = dz . W, the pass's hidden rows transposed to h^T [d, P] for grad_W = dz^T . h, and dz token-major
-// [P, V_pad], which grad_h reads K-contiguous and 16-bit grad_W K-major (transposing LDS reads). fp32 dz is also
-// written vocab-major [V_pad, P] for the fp32 loop, which reads K-contiguous operands only.
+// The backward stages the gradient GEMMs' operands so each mainloop row fetch is whole cache lines: the pass's
+// hidden rows transposed to h^T [d, P] for grad_W = dz^T . h, and dz token-major [P, V_pad], which grad_h reads
+// K-contiguous and 16-bit grad_W K-major (transposing LDS reads). 16-bit grad_h = dz . W reads W K-major as stored
+// when V is a multiple of 64 (the loader's K-row granule) and d of 256 (its column granule); otherwise, and for
+// fp32, W^T [d, V_pad] is staged. fp32 dz is also written vocab-major [V_pad, P] for the fp32 loop, which reads
+// K-contiguous operands only.
+bool gh_reads_w(int d, int V, int w_dtype) {
+  return elem_bytes(staged_dtype(w_dtype)) == 2 && V % 64 == 0 && d % 256 == 0;
+}
 struct BwdLayout {
   int64_t P, V_pad, passes;
   int esz;
@@ -119,8 +124,8 @@ BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, boo
   L.P = n_max == 0 ? 0 : (round_up(n_max, TN) < kPassRows ? round_up(n_max, TN) : kPassRows);
   L.passes = L.P == 0 ? 0 : cdiv(n_max, L.P);
   size_t off = 0;
-  L.wt = off;  // W^T [d, V_pad] (grad_h)
-  if (need_gh) off += align_up((size_t)d * L.V_pad * L.esz);
+  L.wt = off;  // W^T [d, V_pad] (grad_h, unless it reads W K-major)
+  if (need_gh && !gh_reads_w(d, V, w_dtype)) off += align_up((size_t)d * L.V_pad * L.esz);
   L.ht = off;  // h^T [d, P] of the pass's rows (grad_W)
   if (need_gw) off += align_up((size_t)d * L.P * L.esz);
   L.dza = off;  // dz [P, V_pad], token-major (grad_h; 16-bit grad_W)
@@ -447,8 +452,10 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
 
   const Operand Aw = gemm_weight(w, ldw, cm, V, d, wsb + L.wide, st, rc);
   if (rc) return rc;
-  // W^T [d, V_pad] in the staged type (fp8 weights: from their exact bf16 widening; the row scale is in dz)
-  if (need_gh) {
+  // W^T [d, V_pad] in the staged type (fp8 weights: from their exact bf16 widening; the row scale is in dz), unless
+  // grad_h reads W (or the widening) K-major
+  const bool wk = gh_reads_w(d, V, w_dtype);
+  if (need_gh && !wk) {
     if (cm.fp8) rc = launch_transpose(wsb + L.wide, d, OCTO_BF16, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt,
                                       L.V_pad, cm.dt, st);
     else rc = launch_transpose(w, ldw, w_dtype, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt, L.V_pad, cm.dt, st);
@@ -514,10 +521,10 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     }
     if (rc) return rc;
 
-    if (need_gh) {  // grad_h[rows] = dz . W   (K = V_pad)
+    if (need_gh) {  // grad_h[rows] = dz . W   (K = V, or V_pad through the staged W^T)
       const Operand A2 = plain_operand(dza, L.V_pad * esz, rows, count, r0);
-      const Operand B2 = plain_operand(wt, L.V_pad * esz, d, nullptr, 0);
-      const GemmShape s2 = shape(rows, d, L.V_pad, kGroupM, 1, count, r0);
+      const Operand B2 = wk ? plain_operand(Aw.base, Aw.ld, d, nullptr, 0) : plain_operand(wt, L.V_pad * esz, d, nullptr, 0);
+      const GemmShape s2 = shape(rows, d, wk ? V : L.V_pad, kGroupM, 1, count, r0);
       StoreArgs o;
       o.C = (char *)grad_h + r0 * ld_gh * elem_bytes(gh_dtype);
       o.addend = nullptr;
@@ -526,7 +533,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       o.accumulate = 0;
       {
         TimedLaunch t("gemm_store_grad_h", st);
-        rc = launch_gemm_store(cm.dt, A2, B2, s2, o, st);
+        rc = launch_gemm_store(cm.dt, A2, B2, s2, o, st, wk ? KM_B : KM_NONE);
       }
       if (rc) return rc;
     }
@@ -535,7 +542,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, nullptr,
                             idx ? idx + r0 : nullptr, count, r0, rows, rows_pad, d, ht, L.P, cm.dt, st);
       if (rc) return rc;
-      const bool kmajor = esz == 2;  // dz token-major read K-major, else the fp32 vocab-major copy
+      const int kmajor = esz == 2 ? KM_A : KM_NONE;  // dz token-major read K-major, else the fp32 vocab-major copy
       const Operand A3 = kmajor ? plain_operand(dza, L.V_pad * esz, L.P, nullptr, 0)
                                 : plain_operand(dzb, L.P * esz, L.V_pad, nullptr, 0);
       const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);

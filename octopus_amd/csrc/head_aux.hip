@@ -67,57 +67,73 @@ __device__ __forceinline__ void grpo_token(float lp, const float *prox, const fl
                                            float eps_hi, float reject_upper, float inv_z, float &gt, float &lt);
 
 // ---- merge: vocab-tile partials -> per-row outputs ----------------------------------------------
-// One wave per compact row: lanes merge the row's partials (m, S, U) strided by 64, then a wave
-// butterfly; the target logit h_r . W_y is a wave dot product in fp32.
-__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// One wave per compact row, kMergeRows rows per workgroup: lanes merge the row's partials (m, S, U) strided by 64,
+// then a wave butterfly; the target logit h_r . W_y is a wave dot product in fp32. With a GRPO tail the rows' loss
+// terms are summed in LDS and added with one atomic per workgroup (one per row serialises on the scalar).
+constexpr int kMergeRows = 16;
+
+__global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
+  __shared__ float loss_part[kMergeRows];
+  const int wave = threadIdx.x >> 6;
+  const int64_t r = (int64_t)blockIdx.x * kMergeRows + wave;
   const int lane = threadIdx.x & 63;
   const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
-  if (r >= cnt) return;
-  const int64_t hrow = a.idx ? a.idx[r] : r;
-  const int64_t y = a.labels[(a.flags & OCTO_ROWS_VIA_IDX) ? hrow : r];
+  float lt = 0.f;
+  if (r < cnt) {
+    const int64_t hrow = a.idx ? a.idx[r] : r;
+    const int64_t y = a.labels[(a.flags & OCTO_ROWS_VIA_IDX) ? hrow : r];
 
-  Stat3 st{-INFINITY, 0.f, 0.f};
-  const f32x4 *pr = a.part + r * a.mtiles;
-  for (int64_t mt = lane; mt < a.mtiles; mt += 64) {
-    const f32x4 p = pr[mt];
-    st = stat_merge(st, Stat3{p[0], p[1], p[2]});
-  }
-  st = wave_stat_merge(st);
+    Stat3 st{-INFINITY, 0.f, 0.f};
+    const f32x4 *pr = a.part + r * a.mtiles;
+    for (int64_t mt = lane; mt < a.mtiles; mt += 64) {
+      const f32x4 p = pr[mt];
+      st = stat_merge(st, Stat3{p[0], p[1], p[2]});
+    }
+    st = wave_stat_merge(st);
 
-  float dot = 0.f;
-  const bool y_ok = y >= 0 && y < a.V;
-  if (y_ok) dot = row_dot(a.h, a.h_dtype, hrow * a.ldh, a.w, a.w_dtype, y * a.ldw, a.d, lane);
-  dot = wave_sum(dot);
-  if (lane != 0) return;
-  if (a.w_dtype == OCTO_FP8E4M3 && y_ok) dot *= a.wscale[y];
-  const float zt = a.use_tanh ? a.post * tanhf(a.pre * dot) : a.post * a.pre * dot;
-  const float sy = zt * a.inv_T;
-  const float l2S = flog2(st.S);
-  const float lse = (st.m + l2S) * OCTO_LN2;
-  const float ent = (l2S - st.U / st.S) * OCTO_LN2;
-  const float lp = y_ok ? sy - lse : __builtin_nanf("");
-  if (a.logp) a.logp[r] = lp;
-  if (a.ent) a.ent[r] = ent;
-  if (a.lse) a.lse[r] = lse;
-  if (a.out2) {
-    const int64_t orow = (a.flags & OCTO_OUT_SCATTER) ? hrow : r;
-    a.out2[orow * a.ld_out2] = lp;
-    a.out2[orow * a.ld_out2 + 1] = ent;
+    float dot = 0.f;
+    const bool y_ok = y >= 0 && y < a.V;
+    if (y_ok) dot = row_dot(a.h, a.h_dtype, hrow * a.ldh, a.w, a.w_dtype, y * a.ldw, a.d, lane);
+    dot = wave_sum(dot);
+    if (lane == 0) {
+      if (a.w_dtype == OCTO_FP8E4M3 && y_ok) dot *= a.wscale[y];
+      const float zt = a.use_tanh ? a.post * tanhf(a.pre * dot) : a.post * a.pre * dot;
+      const float sy = zt * a.inv_T;
+      const float l2S = flog2(st.S);
+      const float lse = (st.m + l2S) * OCTO_LN2;
+      const float ent = (l2S - st.U / st.S) * OCTO_LN2;
+      const float lp = y_ok ? sy - lse : __builtin_nanf("");
+      if (a.logp) a.logp[r] = lp;
+      if (a.ent) a.ent[r] = ent;
+      if (a.lse) a.lse[r] = lse;
+      if (a.out2) {
+        const int64_t orow = (a.flags & OCTO_OUT_SCATTER) ? hrow : r;
+        a.out2[orow * a.ld_out2] = lp;
+        a.out2[orow * a.ld_out2 + 1] = ent;
+      }
+      if (a.g) {  // the GRPO weight of the row's token, in compact order
+        float gt = 0.f;
+        if (hrow < a.n_tokens && a.gmask[hrow] != 0.f)
+          grpo_token(lp, a.gprox ? a.gprox + hrow : nullptr, a.gold ? a.gold + hrow : nullptr, a.gadv[hrow],
+                     a.eps_lo, a.eps_hi, a.reject_upper, 1.f / a.z[0], gt, lt);
+        a.g[r] = gt;
+      }
+    }
   }
-  if (a.g) {  // the GRPO weight of the row's token, in compact order
-    float gt = 0.f, lt = 0.f;
-    if (hrow < a.n_tokens && a.gmask[hrow] != 0.f)
-      grpo_token(lp, a.gprox ? a.gprox + hrow : nullptr, a.gold ? a.gold + hrow : nullptr, a.gadv[hrow], a.eps_lo,
-                 a.eps_hi, a.reject_upper, 1.f / a.z[0], gt, lt);
-    a.g[r] = gt;
-    if (a.loss && lt != 0.f) atomicAdd(a.loss, lt);
+  if (!a.loss) return;  // uniform across the workgroup: no barrier below is skipped by part of it
+  if (lane == 0) loss_part[wave] = lt;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMergeRows; ++k) sum += loss_part[k];
+    if (sum != 0.f) atomicAdd(a.loss, sum);
   }
 }
 
 int launch_merge(const MergeArgs &a, hipStream_t st) {
   if (a.n_max == 0) return OCTO_OK;
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)cdiv(a.n_max, 4)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)cdiv(a.n_max, kMergeRows)), dim3(64 * kMergeRows), 0, st, a);
   OCTO_CHECK_LAUNCH("merge");
   return OCTO_OK;
 }

@@ -455,10 +455,11 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 }
 
 // The 16-bit gradient GEMMs' 8-wave form: 512 threads, two waves per SIMD, each 128 x 64 of the tile; the second
-// wave on each SIMD issues MFMAs while one waits. grad_W (AK: dz read K-major by transposing LDS reads) keeps one
-// barrier per stage; grad_h (K-contiguous) waits for the next stage half-way through the K-step (SPLIT). Same box,
-// cfg3: grad_W 13.6 against 14.1 ms and grad_h 13.9 against 14.4 ms for the 4-wave form.
-template <int DT, int OT, bool AK>
+// wave on each SIMD issues MFMAs while one waits. KM selects the operand layouts: KM_A, grad_W (dz read K-major by
+// transposing LDS reads), keeps one barrier per stage; KM_NONE (both K-contiguous) and KM_B, grad_h (W read K-major
+// as stored, so no W^T is staged), wait for the next stage half-way through the K-step (SPLIT). Same box, cfg3:
+// grad_W 13.6 against 14.1 ms and grad_h 13.9 against 14.4 ms for the 4-wave form.
+template <int DT, int OT, int KM>
 __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_store8_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
   static_assert(ring5_ok(DT), "16-bit operands");
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
@@ -471,7 +472,8 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   if (s.count_on == 3) K_eff = round_up(dev_count(s.count, s.count_off, s.K), 64);
   if (mvalid <= 0 || nvalid <= 0) return;
   f32x4 acc[8][4];
-  if constexpr (AK) mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
+  if constexpr (KM == KM_A) mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
+  else if constexpr (KM == KM_B) mainloop_ring5<DT, OpRowsN<8, 128>, OpColsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
   else mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
   store_any<Acc16N<4>, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
 }
@@ -582,13 +584,13 @@ int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operan
   return octo_fail(OCTO_EUNSUPPORTED, "gemm_dz: dtype %d", dt);
 }
 
-template <int DT, bool AK>
+template <int DT, int KM>
 static int go_store(const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e, hipStream_t st) {
   if constexpr (ring5_ok(DT)) {
     switch (e.dtype) {
-      case OCTO_BF16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_BF16, AK>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
-      case OCTO_F16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F16, AK>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
-      case OCTO_F32: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F32, AK>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_BF16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_BF16, KM>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_F16: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F16, KM>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
+      case OCTO_F32: hipLaunchKernelGGL((gemm_store8_kernel<DT, OCTO_F32, KM>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e); break;
       default: return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: output dtype %d", e.dtype);
     }
   } else {
@@ -603,22 +605,26 @@ static int go_store(const Operand &A, const Operand &B, const GemmShape &s, cons
   return OCTO_OK;
 }
 
+// The K-major loader (OpColsN) reads whole 512-byte rows of the tile's 256 columns of a plain (unmapped) matrix,
+// up to the next multiple of 64 K-rows: the caller guarantees those rows exist.
+static bool kmajor_layout_ok(const Operand &X) {
+  return !X.map && !(X.ld & 15) && X.ld >= 512 && X.ld <= 0xffffffffLL / 64 && (uintptr_t)X.base % 16 == 0;
+}
+
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
-                      hipStream_t st, bool a_kmajor) {
-  if (a_kmajor) {
-    // the K-major loader (OpColsN) reads whole 512-byte rows of the tile's 256 columns of a plain (unmapped) matrix
-    if (A.map || (A.ld & 15) || A.ld < 512 || A.ld > 0xffffffffLL / 64 || (uintptr_t)A.base % 16)
-      return octo_fail(OCTO_EINVAL, "gemm_store: K-major operand layout");
+                      hipStream_t st, int kmajor) {
+  if (kmajor != KM_NONE) {
+    if (!kmajor_layout_ok(kmajor == KM_A ? A : B)) return octo_fail(OCTO_EINVAL, "gemm_store: K-major operand layout");
     switch (dt) {
-      case OCTO_BF16: return go_store<OCTO_BF16, true>(A, B, s, e, st);
-      case OCTO_F16: return go_store<OCTO_F16, true>(A, B, s, e, st);
+      case OCTO_BF16: return kmajor == KM_A ? go_store<OCTO_BF16, KM_A>(A, B, s, e, st) : go_store<OCTO_BF16, KM_B>(A, B, s, e, st);
+      case OCTO_F16: return kmajor == KM_A ? go_store<OCTO_F16, KM_A>(A, B, s, e, st) : go_store<OCTO_F16, KM_B>(A, B, s, e, st);
     }
     return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: K-major operand of dtype %d", dt);
   }
   switch (dt) {
-    case OCTO_BF16: return go_store<OCTO_BF16, false>(A, B, s, e, st);
-    case OCTO_F16: return go_store<OCTO_F16, false>(A, B, s, e, st);
-    case OCTO_F32: return go_store<OCTO_F32, false>(A, B, s, e, st);
+    case OCTO_BF16: return go_store<OCTO_BF16, KM_NONE>(A, B, s, e, st);
+    case OCTO_F16: return go_store<OCTO_F16, KM_NONE>(A, B, s, e, st);
+    case OCTO_F32: return go_store<OCTO_F32, KM_NONE>(A, B, s, e, st);
   }
   return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: dtype %d", dt);
 }

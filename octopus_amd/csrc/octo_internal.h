@@ -70,9 +70,10 @@ int launch_gemm_stats(int dt, bool a_fp8, bool tanh, const Operand &A, const Ope
                       const StatsArgs &e, hipStream_t st);
 int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
                    const DzArgs &e, hipStream_t st);
-// a_kmajor: A is a plain K-major matrix (element (k, m) at base + k ld + 2 m), 16-bit types
+// kmajor: which operand, if any, is a plain K-major matrix (element (k, m) at base + k ld + 2 m; 16-bit types)
+enum { KM_NONE = 0, KM_A = 1, KM_B = 2 };
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
-                      hipStream_t st, bool a_kmajor = false);
+                      hipStream_t st, int kmajor = KM_NONE);
 
 // ---- small kernels (head_aux.hip) ---------------------------------------------------------------
 struct MergeArgs {

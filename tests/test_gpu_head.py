@@ -52,9 +52,14 @@ def test_forward_matches_oracle(dtype, shape):
         assert (out[:, 1].double() - ent).abs().max() <= tol, (T, post)
 
 
+# (1, 256, 64), (300, 256, 1024) and (513, 512, 4992): V a multiple of 64 and d of 256, so 16-bit grad_h reads W
+# K-major as stored (4992 is not a multiple of the 256-wide tile); the others go through the staged W^T
+BWD_SHAPES = [(1, 64, 100), (300, 64, 1000), (513, 256, 5000), (256, 40, 777), (70, 2560, 3000), (1, 256, 64),
+              (300, 256, 1024), (513, 512, 4992)]
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16], ids=["f32", "bf16", "f16"])
-@pytest.mark.parametrize("shape", [(1, 64, 100), (300, 64, 1000), (513, 256, 5000), (256, 40, 777), (70, 2560, 3000)],
-                         ids=str)
+@pytest.mark.parametrize("shape", BWD_SHAPES, ids=str)
 def test_backward_matches_oracle(dtype, shape):
     n, d, V = shape
     h, W, y = _inputs(n, d, V, dtype, seed=1)
@@ -89,7 +94,7 @@ def test_backward_over_two_passes_matches_fp32_reference():
     assert _rel(hd.grad[65536:], gr[65536:]) <= 1e-2
 
 
-FP8_SHAPES = [(1, 64, 100), (300, 64, 1000), (513, 256, 5000), (256, 48, 777), (70, 2560, 3000)]
+FP8_SHAPES = [(1, 64, 100), (300, 64, 1000), (513, 256, 5000), (256, 48, 777), (70, 2560, 3000), (513, 512, 4992)]
 
 
 @pytest.mark.parametrize("shape", FP8_SHAPES, ids=[f"{n}x{d}x{V}" for n, d, V in FP8_SHAPES])
