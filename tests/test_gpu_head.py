@@ -138,6 +138,39 @@ def test_compaction_is_bit_exact_nonzero():
         assert torch.equal(idx[:ref.numel()], ref)
 
 
+def test_no_scored_rows_every_scored_row_and_zero_rows():
+    """Edge cases of the compaction contract (the reference's `_scored_rows`, lm_head.py:124-130): a mask with no true
+    entry gives a device count of 0, all-zero outputs and all-zero gradients (no tile of any GEMM runs); an all-true
+    mask gives the unscored head bit for bit; zero rows give an empty [0, 2] output and empty gradients."""
+    n, d, V = 300, 256, 1024
+    h, W, y = _inputs(n, d, V, torch.bfloat16, seed=7)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    full = fused_head(hd, Wd, yd, 0.7)
+    for fill, expect_full in ((False, False), (True, True)):
+        mask = torch.full((n,), fill, dtype=torch.bool, device=DEV)
+        idx, count = head_op.compact_rows(mask)
+        assert int(count.item()) == (n if fill else 0)
+        a = hd.clone().requires_grad_(True)
+        b = Wd.clone().requires_grad_(True)
+        out = fused_head(a, b, yd, 0.7, idx=idx, count=count, labels_via_idx=True, scatter=True)
+        if expect_full:
+            assert torch.equal(out, full)
+        else:
+            assert (out == 0).all()
+        (out[:, 0] * torch.ones(n, device=DEV)).sum().backward()
+        if not expect_full:
+            assert (a.grad == 0).all() and (b.grad == 0).all()
+        else:
+            gh, gw = ohead.head_backward(h, W, y, 0.7, torch.ones(n))
+            assert _rel(a.grad.cpu(), gh) <= 1e-2 and _rel(b.grad.cpu(), gw) <= 1e-2
+    a = hd[:0].clone().requires_grad_(True)
+    b = Wd.clone().requires_grad_(True)
+    out = fused_head(a, b, yd[:0], 1.0)
+    assert out.shape == (0, 2)
+    out.sum().backward()
+    assert a.grad.shape == (0, d) and (b.grad == 0).all()
+
+
 def test_scored_rows_equal_the_unscored_rows_bitwise():
     n, d, V = 777, 128, 3000
     h, W, y = _inputs(n, d, V, torch.bfloat16, seed=2)
