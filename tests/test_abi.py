@@ -32,12 +32,19 @@ def test_workspace_query():
     fwd = _lib.workspace_bytes(32768, d, V, _lib.BF16, 0)
     assert fwd >= 32768 * ((V + 255) // 256) * 16
     Vp = (V + 255) // 256 * 256
-    # 16-bit: W^T [d, V_pad], h^T [d, P] and dz token-major [P, V_pad] (grad_W reads it K-major)
+    # 16-bit, V a multiple of 64 and d of 256: h^T [d, P] and dz token-major [P, V_pad] (grad_W reads it K-major,
+    # grad_h reads W K-major as stored)
     bwd = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_BACKWARD)
     no_gw = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_BACKWARD | _lib.WS_NO_GRADW)
-    assert bwd >= (d * Vp + 32768 * Vp + d * 32768) * 2 and bwd < (d * Vp + 32768 * Vp + d * 32768) * 2 + (1 << 20)
-    # without grad_W: W^T and dz
-    assert no_gw >= (d * Vp + 32768 * Vp) * 2 and no_gw < (d * Vp + 32768 * Vp) * 2 + (1 << 20)
+    assert bwd >= (32768 * Vp + d * 32768) * 2 and bwd < (32768 * Vp + d * 32768) * 2 + (1 << 20)
+    # without grad_W: dz only
+    assert no_gw >= 32768 * Vp * 2 and no_gw < 32768 * Vp * 2 + (1 << 20)
+    # other shapes stage W^T [d, V_pad] for grad_h as well
+    for V2, d2 in ((151937, 2560), (151936, 2304 + 64)):
+        Vp2 = (V2 + 255) // 256 * 256
+        bwd2 = _lib.workspace_bytes(32768, d2, V2, _lib.BF16, _lib.WS_BACKWARD)
+        full = (d2 * Vp2 + 32768 * Vp2 + d2 * 32768) * 2
+        assert full <= bwd2 < full + (1 << 20)
     # one pass takes 65,536 rows; two passes of a 16-bit grad_W keep fp32 partial sums
     one = _lib.workspace_bytes(65536, d, V, _lib.BF16, _lib.WS_BACKWARD)
     two = _lib.workspace_bytes(65536 + 256, d, V, _lib.BF16, _lib.WS_BACKWARD)
