@@ -99,10 +99,11 @@ __device__ __forceinline__ void stats_cols(typename L::V (&acc)[L::NI][L::NJ], i
   }
 }
 
+// fp32 forward statistics (4-stage loop, 32 x 32 MFMAs); 16-bit operands run gemm_stats8_kernel.
 template <int DT, bool A_FP8, bool TANH>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_stats_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
-  constexpr bool R5 = ring5_ok(DT);
-  __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
+  static_assert(!ring5_ok(DT) && !A_FP8, "16-bit operands run gemm_stats8_kernel");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
@@ -112,19 +113,11 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
   lds_f32x4 *red = (lds_f32x4 *)smem;
-  if constexpr (R5) {
-    f32x4 acc[8][8];
-    mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
-    pre_transform<Acc16, A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-    if (m0 + TM > e.V) stats_cols<Acc16, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
-    else stats_cols<Acc16, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
-  } else {
-    f32x16 acc[4][4];
-    mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
-    pre_transform<Acc32, false, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-    if (m0 + TM > e.V) stats_cols<Acc32, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
-    else stats_cols<Acc32, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
-  }
+  f32x16 acc[4][4];
+  mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
+  pre_transform<Acc32, false, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
+  if (m0 + TM > e.V) stats_cols<Acc32, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  else stats_cols<Acc32, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
   __syncthreads();
   const int t = threadIdx.x;
   if (t < nvalid) {
@@ -161,7 +154,9 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi, f16x2_t *) {
 }
 
 // Stream a 256 x 512-byte LDS tile (rows stored with slot swizzle `s(row)` on 8-byte slots) to global
-// rows dst + row * ld_bytes, 16 bytes per thread per row-eighth.
+// rows dst + row * ld_bytes, 16 bytes per thread per row-eighth. Non-temporal stores: dz is read back only by the
+// next kernels, after 7.5 GB more of it at 24,576 rows; same box, cfg3: gemm_dz 14.9 against 15.2 ms, grad_h 0.13 ms
+// slower, the step 0.15 ms faster.
 template <int NT = NTHREADS, typename SWZ>
 __device__ __forceinline__ void lds_tile_to_global(const lds_char *tile, char *dst, int64_t ld_bytes, SWZ swz) {
   constexpr int RPP = NT / 32;  // rows per pass
@@ -175,7 +170,7 @@ __device__ __forceinline__ void lds_tile_to_global(const lds_char *tile, char *d
     // swapped when s is odd
     i32x4 v = *(const lds_i32x4 *)(tile + row * 512 + ((2 * c16) ^ (s & ~1)) * 8);
     if (s & 1) v = __builtin_shufflevector(v, v, 2, 3, 0, 1);
-    *(i32x4 *)(dst + row * ld_bytes + c16 * 16) = v;
+    __builtin_nontemporal_store(v, (i32x4 *)(dst + row * ld_bytes + c16 * 16));
   }
 }
 
@@ -358,10 +353,11 @@ __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0
     lds_tile_to_global<NT>(tile, (char *)e.dzA + (n0 * e.ldA + m0) * 2, e.ldA * 2, [](int row) { return DzSwz<L>::at(row); });
 }
 
+// fp32 dz (4-stage loop, 32 x 32 MFMAs, both layouts stored directly); 16-bit operands run gemm_dz8_kernel.
 template <int DT, bool A_FP8, bool TANH>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_dz_kernel(Operand A, Operand B, GemmShape s, DzArgs e) {
-  constexpr bool R5 = ring5_ok(DT);
-  __shared__ __attribute__((aligned(16))) char smem_[R5 ? SMEM_RING5 : SMEM_BYTES];
+  static_assert(!ring5_ok(DT) && !A_FP8, "16-bit operands run gemm_dz8_kernel");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_BYTES];
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
@@ -370,20 +366,10 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (nvalid <= 0) return;
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
-  typedef typename std::conditional<DT == OCTO_BF16, bf16x2, f16x2_t>::type P2;
-  if constexpr (R5) {
-    f32x4 acc[8][8];
-    mainloop_ring5<DT, OpRows128, OpRows128>(A, B, m0, n0, s.K, smem, acc);
-    if constexpr (A_FP8) pre_transform<Acc16, true, false>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-    if (m0 + TM > e.V) dz_stage<Acc16, P2, A_FP8, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-    else dz_stage<Acc16, P2, A_FP8, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-    dz_write<Acc16, P2>(e, m0, n0, nvalid, smem);
-  } else {  // fp32
-    f32x16 acc[4][4];
-    mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
-    dz_in_place<false, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
-    dz_store_direct(acc, e, m0, n0, wm, wn, lane);
-  }
+  f32x16 acc[4][4];
+  mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
+  dz_in_place<false, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
+  dz_store_direct(acc, e, m0, n0, wm, wn, lane);
 }
 
 // ---- epilogue: plain store -------------------------------------------------------------------
