@@ -346,6 +346,17 @@ def main() -> int:
     for k in kernels.values():
         k["flop_per_launch"] = flop_step / k["launches_per_step"]
         k["tflops"] = k["flop_per_launch"] / (k["avg_ms"] / 1e3) / 1e12
+    for name, k in kernels.items():  # fabric (HBM side of L2) bytes per launch from the recorded rocprof counters
+        t = recorded_traffic(name, cfg.name)
+        k["traffic_GBps"] = t / (k["avg_ms"] / 1e3) / 1e9 if t else None
+    # the weight stream: the logits GEMM reads W (its MFMA operand: bf16, fp8 weights widened) once per launch
+    w_bytes = V * d * (4 if cfg.dtype == torch.float32 else 2)
+    weight_stream = None
+    if "gemm_stats" in kernels:
+        ks = kernels["gemm_stats"]
+        weight_stream = {"bytes_per_launch": w_bytes, "kernel": "gemm_stats",
+                         "GBps": w_bytes / (ks["avg_ms"] / 1e3) / 1e9,
+                         "fabric_GBps_all_operands": ks["traffic_GBps"]}
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
     flop_launch = kernels[dom]["flop_per_launch"]
     dom_achieved = flop_launch / (kernels[dom]["avg_ms"] / 1e3)
@@ -370,6 +381,7 @@ def main() -> int:
         "mfma_frac_executed": exe_flop / step_s / peak,
         "phase_ms": {"forward": fwd_ms, "backward": bwd_ms},
         "kernels": kernels,
+        "weight_stream": weight_stream,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": dom_achieved / 1e12, "peak": peak / 1e12,
                      "unit": "TFLOP/s", "frac": dom_achieved / peak,
                      "traffic": recorded_traffic(dom, cfg.name),
