@@ -62,6 +62,8 @@ extern "C" {
 #define OCTO_GRADW_ACCUMULATE 4  /* grad_w += contribution (else grad_w = contribution)               */
 #define OCTO_WS_BACKWARD      8  /* octo_head_workspace_bytes: size for octo_head_bwd                 */
 #define OCTO_WS_NO_GRADW     16  /* octo_head_workspace_bytes: backward without grad_w                */
+#define OCTO_WS_GATHER       32  /* octo_head_workspace_bytes: add a contiguous copy of the n_max rows  */
+                                 /* read through idx; needed when h_rows * ldh * element bytes >= 2^31  */
 #define OCTO_PAIRS_NONE_AS_COUNT 1 /* octo_label_pairs: positions without a pair get the pair count  */
 
 const char *octo_version(void);
@@ -76,7 +78,9 @@ int octo_timing_enable(int on);
 int octo_timing_read(const char *kernel, int *launches, double *total_ms);
 
 /* Workspace bytes for octo_head_fwd (flags without OCTO_WS_BACKWARD) or octo_head_bwd
- * (OCTO_WS_BACKWARD [| OCTO_WS_NO_GRADW]) at n_max rows, width d, vocabulary V. */
+ * (OCTO_WS_BACKWARD [| OCTO_WS_NO_GRADW]) at n_max rows, width d, vocabulary V. With idx, a hidden matrix of
+ * 2 GiB or more (h_rows * ldh * element bytes >= 2^31) is first gathered into the workspace (the GEMMs address
+ * mapped rows with 32-bit offsets): add OCTO_WS_GATHER for those calls. */
 int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes);
 
 /* Masked-row compaction (lm_head.py:128 `scored.nonzero()[:, 0]`): idx[0..count) = the positions

@@ -86,10 +86,14 @@ int staged_dtype(int w_dtype) { return w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_d
 
 struct FwdLayout {
   int64_t mtiles;
-  size_t part, wide, z, total;
+  size_t part, wide, z, rows, total;
 };
+// Bytes of the contiguous copy of the n_max gathered hidden rows [n_max, d] (OCTO_WS_GATHER).
+size_t gather_bytes(int64_t n_max, int d, int h_dtype) { return align_up((size_t)n_max * d * elem_bytes(h_dtype)); }
+
 // part: (m, S, U) per (row, vocab tile). wide: fp8 weights widened to bf16 [V, d]. z: the GRPO tail's token count.
-FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
+// rows: the gathered hidden rows, when asked for (last, so the other offsets do not depend on it).
+FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype, bool gather) {
   FwdLayout L;
   L.mtiles = cdiv(V, TM);
   L.part = 0;
@@ -98,6 +102,8 @@ FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype) {
   if (w_dtype == OCTO_FP8E4M3) off += align_up((size_t)V * d * 2);
   L.z = off;
   off += kAlign;
+  L.rows = off;
+  if (gather) off += gather_bytes(n_max, d, w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_dtype);
   L.total = off;
   return L;
 }
@@ -115,9 +121,9 @@ bool gh_reads_w(int d, int V, int w_dtype) {
 struct BwdLayout {
   int64_t P, V_pad, passes;
   int esz;
-  size_t wt, ht, dza, dzb, hit, wide, gacc, total;
+  size_t wt, ht, dza, dzb, hit, wide, gacc, rows, total;
 };
-BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw) {
+BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw, bool gather) {
   BwdLayout L;
   L.esz = elem_bytes(staged_dtype(w_dtype));
   L.V_pad = round_up(V, TM);
@@ -138,6 +144,8 @@ BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, boo
   if (w_dtype == OCTO_FP8E4M3) off += align_up((size_t)V * d * 2);
   L.gacc = off;  // fp32 grad_W partial sums across passes, for a 16-bit grad_W
   if (need_gw && L.passes > 1 && w_dtype != OCTO_F32) off += align_up((size_t)V * d * sizeof(float));
+  L.rows = off;  // the gathered hidden rows (OCTO_WS_GATHER), last
+  if (gather) off += gather_bytes(n_max, d, w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_dtype);
   L.total = off;
   return L;
 }
@@ -147,6 +155,7 @@ struct Common {
   bool fp8;
   float c, pre, gmul;
   uint32_t h_extent;
+  bool gather;  // idx over a hidden matrix of 2 GiB or more: the GEMMs read a contiguous copy of the rows
 };
 
 int check_common(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
@@ -180,11 +189,12 @@ int check_common(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const 
   if (idx) {
     OCTO_CHECK_ARG(h_rows > 0, "head: h_rows must be positive with idx");
     const int64_t ext = h_rows * ldh * cm.hesz;
-    if (ext >= (int64_t)0x7fffffff) return octo_fail(OCTO_EUNSUPPORTED, "head: gathered hidden exceeds 2 GiB");
-    cm.h_extent = (uint32_t)ext;
+    cm.gather = ext >= (int64_t)0x7fffffff;  // past the 32-bit offsets of a mapped GEMM operand
+    cm.h_extent = cm.gather ? 0 : (uint32_t)ext;
   } else {
     OCTO_CHECK_ARG(h_rows >= n_max, "head: h_rows %lld < n_max %lld", (long long)h_rows, (long long)n_max);
     cm.h_extent = 0;
+    cm.gather = false;
     OCTO_CHECK_ARG(!(flags & (OCTO_ROWS_VIA_IDX | OCTO_OUT_SCATTER)), "head: idx-based flags without idx");
   }
   OCTO_CHECK_ARG(inv_T > 0.f, "head: temperature must be positive");
@@ -223,11 +233,18 @@ Operand gemm_weight(const void *w, int64_t ldw, const Common &cm, int V, int d, 
 }
 
 // Hidden rows [r0, r0 + rows) of the compact order.
+// Hidden rows [r0, r0 + rows) of the compact order: through idx, or (gathered != NULL) from the contiguous copy
+// [n_max, d] of them that launch_rows_gather wrote.
 Operand hidden_operand(const void *h, int64_t ldh, const int64_t *idx, const int32_t *count, int64_t r0,
-                       int64_t rows, const Common &cm) {
+                       int64_t rows, const Common &cm, const void *gathered = nullptr, int d = 0) {
   Operand B;
   B.ld = ldh * cm.hesz;
-  if (idx) {
+  if (gathered) {
+    B.ld = (int64_t)d * cm.hesz;
+    B.base = (const char *)gathered + r0 * B.ld;
+    B.map = nullptr;
+    B.extent = 0;
+  } else if (idx) {
     B.base = (const char *)h;
     B.map = idx + r0;
     B.extent = cm.h_extent;
@@ -283,9 +300,10 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
     OCTO_CHECK_ARG(gt->g && gt->adv && gt->mask, "head_fwd_grpo: null g, adv or mask");
   }
   if (n_max == 0) return OCTO_OK;
-  const FwdLayout L = fwd_layout(n_max, d, V, w_dtype);
+  const FwdLayout L = fwd_layout(n_max, d, V, w_dtype, cm.gather);
   if (!ws || ws_bytes < L.total)
-    return octo_fail(OCTO_EWORKSPACE, "head_fwd: workspace %zu < %zu bytes", ws_bytes, L.total);
+    return octo_fail(OCTO_EWORKSPACE, "head_fwd: workspace %zu < %zu bytes%s", ws_bytes, L.total,
+                     cm.gather ? " (hidden of 2 GiB or more through idx: query with OCTO_WS_GATHER)" : "");
   hipStream_t st = (hipStream_t)stream;
   float *z = (float *)((char *)ws + L.z);
   if (gt) {  // Z (and the loss zeroed) ahead of the merge
@@ -295,7 +313,12 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
 
   const Operand A = gemm_weight(w, ldw, cm, V, d, (char *)ws + L.wide, st, rc);
   if (rc) return rc;
-  const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm);
+  void *gathered = cm.gather ? (char *)ws + L.rows : nullptr;
+  if (gathered) {
+    rc = launch_rows_gather(h, ldh * cm.hesz, idx, count, n_max, (int64_t)d * cm.hesz, gathered, st);
+    if (rc) return rc;
+  }
+  const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm, gathered, d);
   const GemmShape s = shape(V, n_max, d, kGroupM, 2, count, 0);
   StatsArgs e;
   e.part = (f32x4 *)((char *)ws + L.part);
@@ -392,9 +415,9 @@ int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flag
   OCTO_CHECK_ARG(n_max >= 0 && d > 0 && V > 0, "workspace_bytes: bad sizes");
   OCTO_CHECK_ARG(w_dtype >= OCTO_BF16 && w_dtype <= OCTO_FP8E4M3, "workspace_bytes: dtype %d", w_dtype);
   if (flags & OCTO_WS_BACKWARD) {
-    *bytes = bwd_layout(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW)).total;
+    *bytes = bwd_layout(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW), flags & OCTO_WS_GATHER).total;
   } else {
-    *bytes = fwd_layout(n_max, d, V, w_dtype).total;
+    *bytes = fwd_layout(n_max, d, V, w_dtype, flags & OCTO_WS_GATHER).total;
   }
   return OCTO_OK;
 }
@@ -438,9 +461,10 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
   }
   const bool need_gh = grad_h != nullptr, need_gw = grad_w != nullptr;
   if (n_max == 0 || (!need_gh && !need_gw)) return OCTO_OK;
-  const BwdLayout L = bwd_layout(n_max, d, V, w_dtype, need_gh, need_gw);
+  const BwdLayout L = bwd_layout(n_max, d, V, w_dtype, need_gh, need_gw, cm.gather);
   if (!ws || ws_bytes < L.total)
-    return octo_fail(OCTO_EWORKSPACE, "head_bwd: workspace %zu < %zu bytes", ws_bytes, L.total);
+    return octo_fail(OCTO_EWORKSPACE, "head_bwd: workspace %zu < %zu bytes%s", ws_bytes, L.total,
+                     cm.gather ? " (hidden of 2 GiB or more through idx: query with OCTO_WS_GATHER)" : "");
   if (need_gw && L.passes > 1 && gw_dtype != OCTO_F32 && w_dtype == OCTO_F32)
     return octo_fail(OCTO_EUNSUPPORTED, "head_bwd: 16-bit grad_w of fp32 weights over several passes");
   hipStream_t st = (hipStream_t)stream;
@@ -452,6 +476,11 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
 
   const Operand Aw = gemm_weight(w, ldw, cm, V, d, wsb + L.wide, st, rc);
   if (rc) return rc;
+  void *gathered = cm.gather ? wsb + L.rows : nullptr;
+  if (gathered) {
+    rc = launch_rows_gather(h, ldh * cm.hesz, idx, count, n_max, (int64_t)d * cm.hesz, gathered, st);
+    if (rc) return rc;
+  }
   // W^T [d, V_pad] in the staged type (fp8 weights: from their exact bf16 widening; the row scale is in dz), unless
   // grad_h reads W (or the widening) K-major
   const bool wk = gh_reads_w(d, V, w_dtype);
@@ -468,7 +497,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     const bool last = p + 1 == L.passes;
 
     // dz of this pass, recomputed tile by tile
-    const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm);
+    const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm, gathered, d);
     const GemmShape s1 = shape(V, rows, d, kGroupM, 2, count, r0);
     DzArgs e;
     e.dzA = (need_gh || (need_gw && esz == 2)) ? dza : nullptr;

@@ -398,6 +398,31 @@ __global__ void pairs_grad_kernel(const float *gf, int64_t T, int C, const int64
 }
 
 // One workgroup per compact row r that starts a run of equal idx; it sums the run in fp32.
+// dst row r = src row idx[r] for r < *count (rows at and after it untouched), 16-byte chunks; one workgroup per row.
+// The GEMMs address rows read through a row map with 32-bit offsets from the matrix base, so a hidden matrix of
+// 2 GiB or more is gathered into a contiguous copy first.
+__global__ __launch_bounds__(256) void rows_gather_kernel(const char *src, int64_t ld_src, const int64_t *idx,
+                                                          const int32_t *count, int64_t n_max, int64_t row_bytes,
+                                                          char *dst) {
+  const int64_t r = blockIdx.x;
+  const int64_t cnt = count ? min((int64_t)(*count), n_max) : n_max;
+  if (r >= cnt) return;
+  const char *s = src + idx[r] * ld_src;
+  char *o = dst + r * row_bytes;
+  for (int64_t c = threadIdx.x; c < row_bytes / 16; c += 256) *(i32x4 *)(o + 16 * c) = *(const i32x4 *)(s + 16 * c);
+}
+
+int launch_rows_gather(const void *src, int64_t ld_src_bytes, const int64_t *idx, const int32_t *count,
+                       int64_t n_max, int64_t row_bytes, void *dst, hipStream_t st) {
+  if (n_max == 0) return OCTO_OK;
+  if (row_bytes % 16 || ld_src_bytes % 16 || (uintptr_t)src % 16 || (uintptr_t)dst % 16)
+    return octo_fail(OCTO_EINVAL, "rows_gather: rows must be 16-byte aligned");
+  hipLaunchKernelGGL(rows_gather_kernel, dim3((unsigned)n_max), dim3(256), 0, st, (const char *)src, ld_src_bytes,
+                     idx, count, n_max, row_bytes, (char *)dst);
+  OCTO_CHECK_LAUNCH("rows_gather");
+  return OCTO_OK;
+}
+
 __global__ __launch_bounds__(256) void rows_scatter_kernel(const void *src, int64_t ld_src, int src_dtype,
                                                            const int64_t *idx, const int32_t *count, int64_t n_max,
                                                            int d, void *dst, int64_t ld_dst, int dst_dtype,

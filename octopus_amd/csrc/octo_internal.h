@@ -105,6 +105,9 @@ struct MergeArgs {
   float *g, *loss;
 };
 int launch_merge(const MergeArgs &a, hipStream_t st);
+// dst row r (row_bytes, contiguous) = src row idx[r] (ld_src_bytes apart) for r < *count; 16-byte aligned rows
+int launch_rows_gather(const void *src, int64_t ld_src_bytes, const int64_t *idx, const int32_t *count,
+                       int64_t n_max, int64_t row_bytes, void *dst, hipStream_t st);
 // z[0] = max(1, count of mask[t] != 0, t < n); *loss = 0 when loss != NULL. One workgroup.
 int launch_grpo_count(const float *mask, int64_t n, float *z, float *loss, hipStream_t st);
 

@@ -65,6 +65,14 @@ def _workspace(nbytes: int, like: Tensor) -> Tensor:
 
 # ---- fused head ---------------------------------------------------------------------------------
 
+def _gather_flag(rows: Tensor, idx: Optional[Tensor]) -> int:
+    """OCTO_WS_GATHER when rows are read through idx from a matrix of 2 GiB or more: the library then gathers the
+    compact rows into its workspace (its GEMMs address mapped rows with 32-bit offsets)."""
+    if idx is None:
+        return 0
+    return _lib.WS_GATHER if rows.shape[0] * rows.stride(0) * rows.element_size() >= 0x7fffffff else 0
+
+
 @torch.library.custom_op("octohead::head_fwd", mutates_args=(), device_types="cuda")
 def head_fwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Tensor, idx: Optional[Tensor],
              count: Optional[Tensor], inv_T: float, pre: float, post: float, use_tanh: bool,
@@ -81,7 +89,7 @@ def head_fwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
     if n_max == 0:
         return out, lse
     w_code = _dtype_code(weight)
-    ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, 0), rows)
+    ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, _gather_flag(rows, idx)), rows)
     _lib.call("octo_head_fwd", _p(rows), rows.shape[0], rows.stride(0), _dtype_code(rows),
               _p(weight), weight.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
               n_max, d, V, flags, inv_T, pre, post, int(use_tanh),
@@ -121,7 +129,7 @@ def head_fwd_grpo(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], label
     tail = _lib.GrpoTail(_p(prox_), _p(old_), _p(adv_), _p(mask_), adv_.numel(), eps_lo, eps_hi, reject_upper,
                          _p(g), _p(loss))
     w_code = _dtype_code(weight)
-    ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, 0), rows)
+    ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, _gather_flag(rows, idx)), rows)
     _lib.call("octo_head_fwd_grpo", _p(rows), rows.shape[0], rows.stride(0), _dtype_code(rows),
               _p(weight), weight.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
               n_max, d, V, flags, inv_T, pre, post, int(use_tanh),
@@ -156,7 +164,7 @@ def head_bwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
         return grad_rows, grad_w
     w_code = _dtype_code(weight2)
     flags = _lib.ROWS_VIA_IDX if labels_via_idx else 0
-    ws_flags = _lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW)
+    ws_flags = _lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, idx)
     ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, ws_flags), rows2)
     gh = None
     if need_rows:

@@ -45,6 +45,12 @@ def test_workspace_query():
         bwd2 = _lib.workspace_bytes(32768, d2, V2, _lib.BF16, _lib.WS_BACKWARD)
         full = (d2 * Vp2 + 32768 * Vp2 + d2 * 32768) * 2
         assert full <= bwd2 < full + (1 << 20)
+    # OCTO_WS_GATHER adds a contiguous copy of the n_max rows read through idx (hidden of 2 GiB or more)
+    for flags in (0, _lib.WS_BACKWARD):
+        plain = _lib.workspace_bytes(32768, d, V, _lib.BF16, flags)
+        assert _lib.workspace_bytes(32768, d, V, _lib.BF16, flags | _lib.WS_GATHER) >= plain + 32768 * d * 2
+    assert _lib.workspace_bytes(1000, 4096, V, _lib.FP8E4M3, _lib.WS_GATHER) >= \
+        _lib.workspace_bytes(1000, 4096, V, _lib.FP8E4M3, 0) + 1000 * 4096 * 2  # bf16 rows under fp8 weights
     # one pass takes 65,536 rows; two passes of a 16-bit grad_W keep fp32 partial sums
     one = _lib.workspace_bytes(65536, d, V, _lib.BF16, _lib.WS_BACKWARD)
     two = _lib.workspace_bytes(65536 + 256, d, V, _lib.BF16, _lib.WS_BACKWARD)

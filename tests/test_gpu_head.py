@@ -171,6 +171,38 @@ def test_no_scored_rows_every_scored_row_and_zero_rows():
     assert a.grad.shape == (0, d) and (b.grad == 0).all()
 
 
+def test_hidden_of_more_than_2_gib_through_idx():
+    """A hidden matrix of 2 GiB or more read through idx (the GEMMs address mapped rows with 32-bit offsets): the
+    library gathers the compact rows into its workspace first. Scored rows sit on both sides of the 2 GiB mark;
+    outputs scattered to their positions and gradients against the oracle on the same rows."""
+    rows_total, d, V = 270_000, 4096, 1024  # 2.21e9 bytes of bf16 hidden
+    gen = torch.Generator(device=DEV).manual_seed(31)
+    h = torch.randn(rows_total, d, device=DEV, generator=gen)
+    h = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    assert h.numel() * 2 >= 2**31
+    W = (torch.randn(V, d, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    y = torch.randint(0, V, (rows_total,), device=DEV, generator=gen)
+    sel = torch.randperm(rows_total, generator=torch.Generator().manual_seed(32))[:1500]
+    sel = torch.cat([sel, torch.tensor([0, rows_total - 1])]).unique()
+    mask = torch.zeros(rows_total, dtype=torch.bool)
+    mask[sel] = True
+    idx, count = head_op.compact_rows(mask.to(DEV))
+    g = torch.randn(sel.numel(), generator=torch.Generator().manual_seed(33))
+    gfull = torch.zeros(rows_total)
+    gfull[sel] = g
+    a = h.requires_grad_(True)
+    b = W.clone().requires_grad_(True)
+    out = fused_head(a, b, y, 0.7, idx=idx, count=count, labels_via_idx=True, scatter=True)
+    (out[:, 0] * gfull.to(DEV)).sum().backward()
+    hs, ys = h.detach()[sel].cpu(), y[sel].cpu()
+    lp, ent, _ = ohead.head_forward(hs, W.cpu(), ys, 0.7)
+    o = out.detach()[sel].cpu().double()
+    assert (o[:, 0] - lp).abs().max() <= 2e-3 and (o[:, 1] - ent).abs().max() <= 2e-3
+    assert int((out.detach() != 0).any(dim=1).sum().item()) <= sel.numel()
+    gh, gw = ohead.head_backward(hs, W.cpu(), ys, 0.7, g)
+    assert _rel(a.grad[sel].cpu(), gh) <= 1e-2 and _rel(b.grad.cpu(), gw) <= 1e-2
+
+
 def test_scored_rows_equal_the_unscored_rows_bitwise():
     n, d, V = 777, 128, 3000
     h, W, y = _inputs(n, d, V, torch.bfloat16, seed=2)
