@@ -155,8 +155,8 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi, f16x2_t *) {
 
 // Stream a 256 x 512-byte LDS tile (rows stored with slot swizzle `s(row)` on 8-byte slots) to global
 // rows dst + row * ld_bytes, 16 bytes per thread per row-eighth. Non-temporal stores: dz is read back only by the
-// next kernels, after 7.5 GB more of it at 24,576 rows; same box, cfg3: gemm_dz 14.9 against 15.2 ms, grad_h 0.13 ms
-// slower, the step 0.15 ms faster.
+// next kernels, after 7.5 GB more of it at 24,576 rows. Same box, 24,576 rows, d 2560, V 151,936: gemm_dz 14.9
+// against 15.2 ms, grad_h 0.13 ms slower, the fused fwd+bwd step 0.15 ms faster.
 template <int NT = NTHREADS, typename SWZ>
 __device__ __forceinline__ void lds_tile_to_global(const lds_char *tile, char *dst, int64_t ld_bytes, SWZ swz) {
   constexpr int RPP = NT / 32;  // rows per pass
@@ -443,8 +443,9 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 // The 16-bit gradient GEMMs' 8-wave form: 512 threads, two waves per SIMD, each 128 x 64 of the tile; the second
 // wave on each SIMD issues MFMAs while one waits. KM selects the operand layouts: KM_A, grad_W (dz read K-major by
 // transposing LDS reads), keeps one barrier per stage; KM_NONE (both K-contiguous) and KM_B, grad_h (W read K-major
-// as stored, so no W^T is staged), wait for the next stage half-way through the K-step (SPLIT). Same box, cfg3:
-// grad_W 13.6 against 14.1 ms and grad_h 13.9 against 14.4 ms for the 4-wave form.
+// as stored, so no W^T is staged), wait for the next stage half-way through the K-step (SPLIT). Same box, 24,576
+// rows, d 2560, V 151,936: grad_W 13.6 against 14.1 ms and grad_h 13.9 against 14.4 ms for the 4-wave form; grad_h
+// reading W K-major without SPLIT 15.0 against 14.15 ms.
 template <int DT, int OT, int KM>
 __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_store8_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
   static_assert(ring5_ok(DT), "16-bit operands");
@@ -465,8 +466,9 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
 }
 
 // The logits-shaped GEMMs on the 8-wave loop (16-bit operands): 512 threads, two waves per SIMD, each 128 x 64, with
-// the split stage barrier. Same box, cfg3 (against the 4-wave loop): gemm_stats 14.3 against 15.1 ms, gemm_dz 15.3
-// against 16.5 ms; without the split barrier gemm_dz was 0.4 ms slower than the 4-wave loop.
+// the split stage barrier. Same box, 24,576 rows, d 2560, V 151,936 (against the 4-wave loop): gemm_stats 14.3
+// against 15.1 ms, gemm_dz 15.3 against 16.5 ms; without the split barrier gemm_dz was 0.4 ms slower than the 4-wave
+// loop.
 template <int DT, bool A_FP8, bool TANH>
 __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_stats8_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
   static_assert(ring5_ok(DT), "16-bit operands");

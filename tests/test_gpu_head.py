@@ -1,7 +1,7 @@
 """Parity of the HIP path (through the C ABI, via octopus_amd.head_op) with the oracle.
 
 Small shapes: every output against the fp64 oracle on the same inputs (the bf16 inputs rounded first), at
-logprob / entropy 1e-5 abs (fp32) and 2e-3 abs (bf16/f16); gradients relative
+the required bars: logprob / entropy 1e-5 abs (fp32) and 2e-3 abs (bf16/f16); gradients relative
 Frobenius error 1e-2 (bf16), 1e-4 (fp32); compaction and target gathers bit-exact.
 Full-size configurations: all rows on the GPU, the oracle on a seeded subsample of rows, and a chunked
 fp32 torch reference on the GPU for the gradients (which depend on every row)."""
