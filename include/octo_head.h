@@ -64,6 +64,10 @@ extern "C" {
 #define OCTO_WS_NO_GRADW     16  /* octo_head_workspace_bytes: backward without grad_w                */
 #define OCTO_WS_GATHER       32  /* octo_head_workspace_bytes: add a contiguous copy of the n_max rows  */
                                  /* read through idx; needed when h_rows * ldh * element bytes >= 2^31  */
+#define OCTO_LSE_PAIR        64  /* head fwd/bwd: lse holds 2 floats per row, (m2, l2S): the row's       */
+                                 /* base-2 maximum of s log2(e) and log2 of the shifted sum, lse =       */
+                                 /* (m2 + l2S) ln 2; the backward then repeats the forward's rounding    */
+                                 /* (exact dz row sums when the logits sit far from zero)                */
 #define OCTO_PAIRS_NONE_AS_COUNT 1 /* octo_label_pairs: positions without a pair get the pair count  */
 
 const char *octo_version(void);
@@ -94,7 +98,8 @@ int octo_compact_rows(const uint8_t *mask, int64_t n, int64_t *idx, int32_t *cou
  *   weight           : w [V, ldw] (w_dtype = h_dtype, or FP8E4M3 with w_scale[V] and BF16 h)
  *   label of r       : labels[(flags & OCTO_ROWS_VIA_IDX) ? idx[r] : r], int64 in [0, V)
  *   post-head logits : z' = use_tanh ? post * tanh(pre * z) : post * pre * z;  s = z' * inv_T
- *   outputs          : logp[r], ent[r], lse[r] (any may be NULL) and, if out2 != NULL,
+ *   outputs          : logp[r], ent[r], lse[r] (any may be NULL; lse[2 r], lse[2 r + 1] under
+ *                      OCTO_LSE_PAIR) and, if out2 != NULL,
  *                      out2[row * ld_out2 + {0,1}] = {logp, entropy} with row = idx[r] under
  *                      OCTO_OUT_SCATTER, else r. Rows of out2 not written are left untouched.
  * Requires d % 8 == 0 (bf16/f16), d % 16 == 0 (fp8) or d % 4 == 0 (f32), inv_T > 0, pre * post > 0 when !use_tanh. */
@@ -108,7 +113,7 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
 
 /* Backward of octo_head_fwd's logprob column (the entropy column carries no gradient):
  *   g[r]   : dL/dlogprob of compact row r (fp32, compact order)
- *   lse[r] : from octo_head_fwd on the same inputs
+ *   lse[r] : from octo_head_fwd on the same inputs (the pair form under OCTO_LSE_PAIR, given to both calls)
  *   grad_h : NULL or [n_max, ld_gh] of gh_dtype (BF16, F16 or F32), compact order; rows at and
  *            after *count are left unspecified
  *   grad_w : NULL or [V, d] (row stride d) of gw_dtype (BF16, F16 or F32); = or += (OCTO_GRADW_ACCUMULATE),
@@ -125,10 +130,13 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                   void *ws, size_t ws_bytes, void *stream);
 
 /* _head_columns on materialised logits [n, ld] (dtype BF16, F16 or F32):
- * out2[r] = {log_softmax(s)[y_r], entropy}, s = logits * inv_T; lse[r] saved (may be NULL). */
+ * out2[r] = {log_softmax(s)[y_r], entropy}, s = logits * inv_T; the row state saved (may be NULL) as two floats
+ * per row, lse[2 r] = m2 (the row's maximum of s log2(e)) and lse[2 r + 1] = l2S (log2 of the shifted sum):
+ * lse = (m2 + l2S) ln 2, and octo_columns_bwd repeats the forward's rounding with it. */
 int octo_columns_fwd(const void *logits, int64_t ld, int dtype, const int64_t *labels,
                      int64_t n, int V, float inv_T, float *out2, float *lse, void *stream);
-/* dlogits[r, j] = g[r] * (1[j = y_r] - p_rj) * inv_T, written in dtype at stride ld_d. */
+/* dlogits[r, j] = g[r] * (1[j = y_r] - p_rj) * inv_T, written in dtype at stride ld_d; lse: octo_columns_fwd's
+ * row state (2 floats per row). */
 int octo_columns_bwd(const void *logits, int64_t ld, int dtype, const int64_t *labels,
                      int64_t n, int V, float inv_T, const float *lse, const float *g,
                      void *dlogits, int64_t ld_d, void *stream);

@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(HERE, "libocto_head.so")
 # status codes and enums (include/octo_head.h)
 OK, EINVAL, EWORKSPACE, EUNSUPPORTED, EHIP = 0, -1, -2, -3, -4
 BF16, F16, F32, FP8E4M3 = 0, 1, 2, 3
-ROWS_VIA_IDX, OUT_SCATTER, GRADW_ACCUMULATE, WS_BACKWARD, WS_NO_GRADW, WS_GATHER = 1, 2, 4, 8, 16, 32
+ROWS_VIA_IDX, OUT_SCATTER, GRADW_ACCUMULATE, WS_BACKWARD, WS_NO_GRADW, WS_GATHER, LSE_PAIR = 1, 2, 4, 8, 16, 32, 64
 PAIRS_NONE_AS_COUNT = 1
 
 _p = ctypes.c_void_p

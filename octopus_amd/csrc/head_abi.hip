@@ -357,6 +357,7 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
   m.logp = logp;
   m.ent = ent;
   m.lse = lse;
+  m.lse_pair = (flags & OCTO_LSE_PAIR) != 0;
   m.out2 = out2;
   m.ld_out2 = ld_out2;
   m.gprox = gt ? gt->prox : nullptr;
@@ -505,6 +506,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
     e.dzB = (need_gw && esz == 4) ? dzb : nullptr;
     e.ldB = L.P;
     e.lse = lse;
+    e.lse_pair = (flags & OCTO_LSE_PAIR) != 0;
     e.g = g;
     e.labels = labels;
     e.label_idx = (flags & OCTO_ROWS_VIA_IDX) ? idx : nullptr;
@@ -528,6 +530,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       ha.labels = labels;
       ha.label_idx = e.label_idx;
       ha.lse = lse;
+      ha.lse_pair = e.lse_pair;
       ha.g = g;
       ha.count = count;
       ha.r0 = r0;

@@ -105,7 +105,14 @@ __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
       const float lp = y_ok ? sy - lse : __builtin_nanf("");
       if (a.logp) a.logp[r] = lp;
       if (a.ent) a.ent[r] = ent;
-      if (a.lse) a.lse[r] = lse;
+      if (a.lse) {
+        if (a.lse_pair) {
+          a.lse[2 * r] = st.m;
+          a.lse[2 * r + 1] = l2S;
+        } else {
+          a.lse[r] = lse;
+        }
+      }
       if (a.out2) {
         const int64_t orow = (a.flags & OCTO_OUT_SCATTER) ? hrow : r;
         a.out2[orow * a.ld_out2] = lp;
@@ -157,13 +164,15 @@ __global__ __launch_bounds__(256) void hit_kernel(HitArgs a) {
       dot = wave_sum(dot);
       const bool f8 = a.w_dtype == OCTO_FP8E4M3;
       const float x = f8 ? dot * a.wscale[y] : dot;
-      const float lse2 = a.lse[r] * OCTO_LOG2E, gs = a.g[r] * a.gmul;
+      float m2, l2s;
+      row_state(a.lse, a.lse_pair, r, m2, l2s);
+      const float gs = a.g[r] * a.gmul;
       float v;
       if (a.use_tanh) {
         const float th = ftanh(a.pre * x);
-        v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(th, a.c, -lse2)), gs) * (1.f - th * th);
+        v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(th, a.c, -m2) - l2s), gs) * (1.f - th * th);
       } else {
-        v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(x, a.c, -lse2)), gs);
+        v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(x, a.c, -m2) - l2s), gs);
       }
       hv_out = f8 ? v * a.wscale[y] : v;
     }
@@ -359,7 +368,10 @@ __global__ __launch_bounds__(256) void columns_fwd_kernel(const void *logits, in
     const float sy = (y >= 0 && y < V) ? load_as_f32(logits, dtype, r * ld + y) * inv_T : __builtin_nanf("");
     out2[2 * r] = sy - lse;
     out2[2 * r + 1] = (l2S - U / S) * OCTO_LN2;
-    if (lse_out) lse_out[r] = lse;
+    if (lse_out) {  // the row state (m2, l2S) for columns_bwd, as row_state's paired form
+      lse_out[2 * r] = m2;
+      lse_out[2 * r + 1] = l2S;
+    }
   }
 }
 
@@ -370,7 +382,9 @@ __global__ __launch_bounds__(256) void columns_bwd_kernel(const void *logits, in
   const int64_t r = blockIdx.y;
   const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (j >= V) return;
-  const float p = fexp2((load_as_f32(logits, dtype, r * ld + j) * inv_T - lse[r]) * OCTO_LOG2E);
+  // the forward's own t = fma(x, c, -m2), so the row's p keep the forward's rounding (row_state)
+  const float p = fexp2(__builtin_fmaf(load_as_f32(logits, dtype, r * ld + j), inv_T * OCTO_LOG2E, -lse[2 * r]) -
+                        lse[2 * r + 1]);
   const float onehot = (labels[r] == j) ? 1.f : 0.f;
   store_from_f32(dl, dtype, r * ld_d + j, g[r] * inv_T * (onehot - p));
 }

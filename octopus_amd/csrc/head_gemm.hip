@@ -186,10 +186,10 @@ __device__ __forceinline__ void dz_in_place(f32x16 (&acc)[4][4], const DzArgs &e
     const int col = acc_col(wn, j, lane);
     const bool tok_ok = col < nvalid;
     const int64_t r = e.row_off + n0 + col;  // compact row
-    float lse2 = 0.f, gs = 0.f;
+    float m2 = 0.f, l2s = 0.f, gs = 0.f;
     int yrel = -1;
     if (tok_ok) {
-      lse2 = e.lse[r] * OCTO_LOG2E;
+      row_state(e.lse, e.lse_pair, r, m2, l2s);
       gs = e.g[r] * e.gmul;
       const int64_t y = e.labels[e.label_idx ? e.label_idx[r] : r] - lane_row0;
       yrel = (y >= 0 && y < 256) ? (int)y : -1;
@@ -203,10 +203,10 @@ __device__ __forceinline__ void dz_in_place(f32x16 (&acc)[4][4], const DzArgs &e
         const float x = acc[i][j][v];
         if constexpr (TANH) {
           const float th = ftanh(e.pre * x);
-          const float p = fexp2(__builtin_fmaf(th, e.c, -lse2));
+          const float p = fexp2(__builtin_fmaf(th, e.c, -m2) - l2s);
           acc[i][j][v] = __builtin_fmaf(-gs, p, hit) * (1.f - th * th);
         } else {
-          const float p = fexp2(__builtin_fmaf(x, e.c, -lse2));
+          const float p = fexp2(__builtin_fmaf(x, e.c, -m2) - l2s);
           acc[i][j][v] = __builtin_fmaf(-gs, p, hit);
         }
       }
@@ -283,10 +283,10 @@ __device__ __forceinline__ void dz_stage(const typename L::V (&acc)[L::NI][L::NJ
 #pragma unroll
   for (int j = 0; j < L::NJ; ++j) {
     const int tt = L::col(wn, j, lane);
-    float lse2 = 0.f, ngs = 0.f;  // -g / T (0 for tokens past the pass's count: dz 0, also in K-padding)
+    float m2 = 0.f, l2s = 0.f, ngs = 0.f;  // -g / T (0 for tokens past the pass's count: dz 0, also in K-padding)
     if (tt < nvalid) {
       const int64_t r = e.row_off + n0 + tt;
-      lse2 = e.lse[r] * OCTO_LOG2E;
+      row_state(e.lse, e.lse_pair, r, m2, l2s);
       ngs = -(e.g[r] * e.gmul);
     }
     const int sw = DzSwz<L>::at(tt);
@@ -313,9 +313,9 @@ __device__ __forceinline__ void dz_stage(const typename L::V (&acc)[L::NI][L::NJ
           const float x = acc[i][j][4 * g4 + u];
           if constexpr (TANH) {
             const float th = ftanh(e.pre * x);
-            d[u] = ngs * fexp2(__builtin_fmaf(th, e.c, -lse2)) * (1.f - th * th);
+            d[u] = ngs * fexp2(__builtin_fmaf(th, e.c, -m2) - l2s) * (1.f - th * th);
           } else {
-            d[u] = ngs * fexp2(__builtin_fmaf(x, e.c, -lse2));
+            d[u] = ngs * fexp2(__builtin_fmaf(x, e.c, -m2) - l2s);
           }
           if constexpr (A_FP8) d[u] *= sc[u];
           if constexpr (EDGE) d[u] = (m0 + rl + u < e.V) ? d[u] : 0.f;

@@ -18,6 +18,22 @@ struct StatsArgs {
   float pre;            // tanh argument scale (softcap)
 };
 
+// The backward's per-row softmax state. Paired (OCTO_LSE_PAIR): lse[2 r] = m2, the row's base-2 maximum exactly as
+// the statistics epilogue subtracts it (t = fma(x, c, -m2)), and lse[2 r + 1] = log2 of the shifted sum, so that
+// p = exp2(fma(x, c, -m2) - l2S) repeats the forward's rounding: a plain fp32 lse of a row whose logits sit far from
+// zero carries an absolute rounding error that scales every p of the row alike, and the row's dz then no longer sums
+// to zero (at logits near -1,400 nats, 3% off in grad_h when the weights share a large component). Plain: m2 =
+// lse[r] log2(e), l2S = 0.
+__device__ __forceinline__ void row_state(const float *lse, int pair, int64_t r, float &m2, float &l2s) {
+  if (pair) {
+    m2 = lse[2 * r];
+    l2s = lse[2 * r + 1];
+  } else {
+    m2 = lse[r] * OCTO_LOG2E;
+    l2s = 0.f;
+  }
+}
+
 // gemm_dz epilogue arguments (tokens are pass-local; compact row = row_off + token).
 struct DzArgs {
   void *dzA;  // [tokens, ldA] vocabulary contiguous, staged MFMA type, or NULL
@@ -33,6 +49,7 @@ struct DzArgs {
   const float *wscale;
   const float *hit;  // 16-bit dz: the pass's label entries, hit[token] (launch_hit), written over the dense values
   float c, pre, gmul;
+  int lse_pair;      // lse holds (m2, l2S) per row (row_state)
 };
 
 // The label entry of each row's dz, g (1 - p_y) / T x post'(z_y) (x the fp8 row scale), from an fp32 target logit:
@@ -55,6 +72,7 @@ struct HitArgs {
   float c, pre, gmul;
   int use_tanh;
   float *hit;
+  int lse_pair;  // lse holds (m2, l2S) per row (row_state)
 };
 int launch_hit(const HitArgs &a, hipStream_t st);
 
@@ -96,6 +114,7 @@ struct MergeArgs {
   float inv_T, pre, post;
   int use_tanh;
   float *logp, *ent, *lse, *out2;
+  int lse_pair;  // lse gets (m2, l2S) per row (row_state) instead of the natural-log lse
   int64_t ld_out2;
   // GRPO weight of each compact row (g != NULL): per-token arrays indexed by the row's flat token
   const float *gprox, *gold, *gadv, *gmask;

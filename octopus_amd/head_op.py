@@ -78,14 +78,15 @@ def head_fwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
              count: Optional[Tensor], inv_T: float, pre: float, post: float, use_tanh: bool,
              labels_via_idx: bool, scatter: bool) -> tuple[Tensor, Tensor]:
     """(out, lse): out [n, 2] fp32 = (logprob, entropy) per compact row (n = len(idx) or rows), or
-    [rows, 2] with each compact row written at idx[r] and zeros elsewhere (scatter); lse [n] fp32."""
+    [rows, 2] with each compact row written at idx[r] and zeros elsewhere (scatter); lse [n, 2] fp32, the
+    backward's row state (m2, l2S) with lse = (m2 + l2S) ln 2 (OCTO_LSE_PAIR)."""
     rows, weight = _rows2d(rows), _rows2d(weight)
     labels, idx = _index(labels), _index(idx)
     n_max = idx.numel() if idx is not None else rows.shape[0]
     V, d = weight.shape
-    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | (_lib.OUT_SCATTER if scatter else 0)
+    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | (_lib.OUT_SCATTER if scatter else 0) | _lib.LSE_PAIR
     out = torch.zeros(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32, device=rows.device)
-    lse = torch.zeros(n_max, dtype=torch.float32, device=rows.device)
+    lse = torch.zeros(n_max, 2, dtype=torch.float32, device=rows.device)
     if n_max == 0:
         return out, lse
     w_code = _dtype_code(weight)
@@ -101,7 +102,7 @@ def head_fwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
 def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, labels_via_idx, scatter):
     n_max = idx.shape[0] if idx is not None else rows.shape[0]
     out = rows.new_empty(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32)
-    return out, rows.new_empty(n_max, dtype=torch.float32)
+    return out, rows.new_empty(n_max, 2, dtype=torch.float32)
 
 
 @torch.library.custom_op("octohead::head_fwd_grpo", mutates_args=(), device_types="cuda")
@@ -117,9 +118,9 @@ def head_fwd_grpo(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], label
     labels, idx = _index(labels), _index(idx)
     n_max = idx.numel() if idx is not None else rows.shape[0]
     V, d = weight.shape
-    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | (_lib.OUT_SCATTER if scatter else 0)
+    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | (_lib.OUT_SCATTER if scatter else 0) | _lib.LSE_PAIR
     out = torch.zeros(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32, device=rows.device)
-    lse = torch.zeros(n_max, dtype=torch.float32, device=rows.device)
+    lse = torch.zeros(n_max, 2, dtype=torch.float32, device=rows.device)
     g = torch.zeros(n_max, dtype=torch.float32, device=rows.device)
     loss = torch.zeros((), dtype=torch.float32, device=rows.device)
     if n_max == 0:
@@ -142,7 +143,7 @@ def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, lab
       mask, eps_lo, eps_hi, reject_upper):
     n_max = idx.shape[0] if idx is not None else rows.shape[0]
     out = rows.new_empty(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32)
-    return (out, rows.new_empty(n_max, dtype=torch.float32), rows.new_empty(n_max, dtype=torch.float32),
+    return (out, rows.new_empty(n_max, 2, dtype=torch.float32), rows.new_empty(n_max, dtype=torch.float32),
             rows.new_empty((), dtype=torch.float32))
 
 
@@ -163,7 +164,7 @@ def head_bwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
             grad_w = torch.zeros_like(weight)
         return grad_rows, grad_w
     w_code = _dtype_code(weight2)
-    flags = _lib.ROWS_VIA_IDX if labels_via_idx else 0
+    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | _lib.LSE_PAIR
     ws_flags = _lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, idx)
     ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, ws_flags), rows2)
     gh = None
@@ -240,7 +241,7 @@ def columns_fwd(logits: Tensor, labels: Tensor, inv_T: float) -> tuple[Tensor, T
     labels = _index(labels)
     n, V = logits.shape
     out = torch.empty(n, 2, dtype=torch.float32, device=logits.device)
-    lse = torch.empty(n, dtype=torch.float32, device=logits.device)
+    lse = torch.empty(n, 2, dtype=torch.float32, device=logits.device)  # row state (m2, l2S)
     _lib.call("octo_columns_fwd", _p(logits), logits.stride(0), _dtype_code(logits), _p(labels), n, V, inv_T,
               _p(out), _p(lse), _stream(logits))
     return out, lse
@@ -248,7 +249,7 @@ def columns_fwd(logits: Tensor, labels: Tensor, inv_T: float) -> tuple[Tensor, T
 
 @columns_fwd.register_fake
 def _(logits, labels, inv_T):
-    return logits.new_empty(logits.shape[0], 2, dtype=torch.float32), logits.new_empty(logits.shape[0],
+    return logits.new_empty(logits.shape[0], 2, dtype=torch.float32), logits.new_empty(logits.shape[0], 2,
                                                                                         dtype=torch.float32)
 
 

@@ -203,6 +203,68 @@ def test_hidden_of_more_than_2_gib_through_idx():
     assert _rel(a.grad[sel].cpu(), gh) <= 1e-2 and _rel(b.grad.cpu(), gw) <= 1e-2
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_extreme_logits_are_stable(dtype):
+    """The online max / sum over vocabulary tiles at extreme logits. Every row's hidden vector is e_0, so logit j is
+    W[j, 0] exactly: all-zero weights give logprob = -log V and entropy = log V (closed form); a 600-nat peak in the
+    last vocabulary tile, with the other logits in [-50, 50], gives logprob 0 and entropy 0 at the peak's rows and
+    about -600 elsewhere; logits near -1000 at T = 0.7 check the shift by the row max. Against the fp64 oracle, the
+    absolute bar grows with the logits' magnitude (logprob = s_y - lse cancels two fp32 numbers of that size)."""
+    n, d, V = 300, 64, 1000
+    h = torch.zeros(n, d, dtype=dtype)
+    h[:, 0] = 1.0
+    gen = torch.Generator().manual_seed(41)
+    base = torch.randint(-50, 51, (V,), generator=gen).to(torch.float32)
+    y = torch.randint(0, V, (n,), generator=gen)
+    y[::2] = 777
+    tol0 = _tol(dtype)
+    # all-zero weights: uniform over V
+    W = torch.zeros(V, d, dtype=dtype)
+    out = fused_head(h.to(DEV), W.to(DEV), y.to(DEV), 1.0).cpu().double()
+    assert (out[:, 0] + np.log(V)).abs().max() <= tol0 and (out[:, 1] - np.log(V)).abs().max() <= tol0
+    for T, col, big in ((1.0, base.clone().index_fill_(0, torch.tensor([777]), 600.0), 650.0),
+                        (0.7, base / 10 - 1000.0, 1000.0 / 0.7)):
+        W = torch.zeros(V, d)
+        W[:, 0] = col
+        W = W.to(dtype)
+        hd = h.to(DEV).requires_grad_(True)
+        Wd = W.to(DEV).requires_grad_(True)
+        out = fused_head(hd, Wd, y.to(DEV), T)
+        g = torch.randn(n, generator=torch.Generator().manual_seed(42))
+        (out[:, 0] * g.to(DEV)).sum().backward()
+        lp, ent, _ = ohead.head_forward(h, W, y, T)
+        tol = tol0 + 4e-7 * big
+        o = out.detach().cpu().double()
+        assert torch.isfinite(o).all()
+        assert (o[:, 0] - lp).abs().max() <= tol and (o[:, 1] - ent).abs().max() <= tol, T
+        if T == 1.0:
+            assert o[::2, 0].abs().max() <= tol and o[::2, 1].abs().max() <= tol  # the peak's rows
+        gh, gw = ohead.head_backward(h, W, y, T, g)
+        # the bar: the usual one plus the error of the reference's own composite in the same dtype (GEMM with its
+        # logits in that dtype, fp32 log_softmax, autograd: dz cast to the dtype before the gradient GEMMs), which
+        # is large where the weights' shared component makes grad_h a sum of large cancelling terms (at logits
+        # near -1,400 nats: 1.2e-4 in fp32, 0.72 in bf16; this path: 1.6e-4 and 0.72)
+        hr = h.detach().clone().requires_grad_(True)
+        Wr = W.detach().clone().requires_grad_(True)
+        (torch.log_softmax((hr @ Wr.T).float() / T, dim=1).gather(1, y[:, None])[:, 0] * g).sum().backward()
+        bar = 1e-4 if dtype == torch.float32 else 1e-2
+        bar_h = bar + 1.25 * _rel(hr.grad, gh)
+        bar_w = bar + 1.25 * _rel(Wr.grad, gw)
+        assert _rel(hd.grad.cpu(), gh) <= bar_h and _rel(Wd.grad.cpu(), gw) <= bar_w, (T, bar_h, bar_w)
+    if dtype == torch.float32:  # _head_columns on the same logits, materialised: each dlogits row sums to 0
+        from octopus_amd.rl import lm_head
+        T = 0.7
+        logits = (base / 10 - 1000.0).expand(n, V).contiguous()
+        x = logits.to(DEV).requires_grad_(True)
+        g = torch.randn(n, generator=torch.Generator().manual_seed(43))
+        (lm_head._head_columns(x, T, y.to(DEV))[:, 0] * g.to(DEV)).sum().backward()
+        s64 = logits.double() / T
+        p64 = torch.softmax(s64, dim=1)
+        dl64 = g.double()[:, None] * (torch.nn.functional.one_hot(y, V).double() - p64) / T
+        assert (x.grad.cpu().double() - dl64).abs().max() <= 1e-5
+        assert x.grad.cpu().double().sum(dim=1).abs().max() <= 1e-5
+
+
 def test_scored_rows_equal_the_unscored_rows_bitwise():
     n, d, V = 777, 128, 3000
     h, W, y = _inputs(n, d, V, torch.bfloat16, seed=2)
