@@ -265,6 +265,34 @@ def test_extreme_logits_are_stable(dtype):
         assert x.grad.cpu().double().sum(dim=1).abs().max() <= 1e-5
 
 
+def test_hidden_of_more_than_2_gib_through_idx_over_two_backward_passes():
+    """The gathered copy of the compact rows serves every backward pass: 70,000 scored rows (65,536 + 4,464) of a
+    2.2 GB bf16 hidden matrix, against the chunked fp32 torch reference on the GPU."""
+    from tests.gpu_reference import head_fp32
+    rows_total, d, V = 270_000, 4096, 1000
+    gen = torch.Generator(device=DEV).manual_seed(51)
+    h = torch.randn(rows_total, d, device=DEV, generator=gen)
+    h = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    W = (torch.randn(V, d, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    y = torch.randint(0, V, (rows_total,), device=DEV, generator=gen)
+    mask = torch.zeros(rows_total, dtype=torch.bool, device=DEV)
+    mask[torch.randperm(rows_total, device=DEV, generator=gen)[:70_000]] = True
+    idx, count = head_op.compact_rows(mask)
+    n = int(count.item())
+    assert n == 70_000
+    g = torch.randn(rows_total, device=DEV, generator=gen) * mask
+    a = h.requires_grad_(True)
+    b = W.clone().requires_grad_(True)
+    out = fused_head(a, b, y, 1.0, idx=idx, count=count, labels_via_idx=True, scatter=True)
+    (out[:, 0] * g).sum().backward()
+    sel = idx[:n]
+    lp, ent, gr, gw = head_fp32(h.detach()[sel], W.float(), y[sel], 1.0, g=g[sel])
+    assert (out.detach()[sel, 0] - lp).abs().max().item() <= 2e-3
+    assert (out.detach()[sel, 1] - ent).abs().max().item() <= 2e-3
+    assert _rel(a.grad[sel], gr) <= 1e-2 and _rel(b.grad, gw) <= 1e-2
+    assert _rel(a.grad[sel][65536:], gr[65536:]) <= 1e-2  # the second pass's rows
+
+
 def test_scored_rows_equal_the_unscored_rows_bitwise():
     n, d, V = 777, 128, 3000
     h, W, y = _inputs(n, d, V, torch.bfloat16, seed=2)
