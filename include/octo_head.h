@@ -119,7 +119,7 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
  *   grad_w : NULL or [V, d] (row stride d) of gw_dtype (BF16, F16 or F32); = or += (OCTO_GRADW_ACCUMULATE),
  *            summed in fp32 and rounded once to gw_dtype. Not available for FP8E4M3 weights.
  * The logits are recomputed tile by tile; dz = g (onehot - p) / T is staged in the workspace (bf16 / f16 / f32)
- * in passes of at most 32,768 rows. */
+ * in passes of at most 65,536 rows. */
 int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                   const void *w, int64_t ldw, int w_dtype, const float *w_scale,
                   const int64_t *labels, const int64_t *idx, const int32_t *count,

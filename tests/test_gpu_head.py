@@ -293,6 +293,45 @@ def test_hidden_of_more_than_2_gib_through_idx_over_two_backward_passes():
     assert _rel(a.grad[sel][65536:], gr[65536:]) <= 1e-2  # the second pass's rows
 
 
+def test_c_abi_plain_and_paired_row_state():
+    """octo_head_fwd / octo_head_bwd through the C ABI with the plain natural-log lse (flags 0) and with the paired row
+    state (OCTO_LSE_PAIR): the forward's outputs are the same bits either way, the plain lse is (m2 + l2S) ln 2 of the
+    pair and matches the oracle, and both backward forms match the oracle's gradients."""
+    import ctypes
+    from octopus_amd import _lib
+    n, d, V, T = 300, 256, 1024, 0.7
+    h, W, y = _inputs(n, d, V, torch.bfloat16, seed=61)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    g = torch.randn(n, generator=torch.Generator().manual_seed(62))
+    gd = g.to(DEV)
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    lp_ref, ent_ref, lse_ref = ohead.head_forward(h, W, y, T)
+    gh_ref, gw_ref = ohead.head_backward(h, W, y, T, g)
+    res = {}
+    for flags in (0, _lib.LSE_PAIR):
+        out = torch.zeros(n, 2, device=DEV)
+        lse = torch.zeros((n, 2) if flags else (n,), device=DEV)
+        ws = torch.empty(_lib.workspace_bytes(n, d, V, _lib.BF16, 0), dtype=torch.uint8, device=DEV)
+        _lib.call("octo_head_fwd", P(hd), n, hd.stride(0), _lib.BF16, P(Wd), Wd.stride(0), _lib.BF16, None, P(yd),
+                  None, None, n, d, V, flags, 1.0 / T, 1.0, 1.0, 0, None, None, P(lse), P(out), 2, P(ws), ws.numel(),
+                  st)
+        wsb = torch.empty(_lib.workspace_bytes(n, d, V, _lib.BF16, _lib.WS_BACKWARD), dtype=torch.uint8, device=DEV)
+        gh = torch.empty(n, d, dtype=torch.bfloat16, device=DEV)
+        gw = torch.empty(V, d, dtype=torch.bfloat16, device=DEV)
+        _lib.call("octo_head_bwd", P(hd), n, hd.stride(0), _lib.BF16, P(Wd), Wd.stride(0), _lib.BF16, None, P(yd),
+                  None, None, n, d, V, flags, 1.0 / T, 1.0, 1.0, 0, P(lse), P(gd), P(gh), d, _lib.BF16, P(gw),
+                  _lib.BF16, P(wsb), wsb.numel(), st)
+        torch.cuda.synchronize()
+        res[flags] = (out.cpu(), lse.cpu(), gh.cpu(), gw.cpu())
+        assert _rel(gh.cpu(), gh_ref) <= 1e-2 and _rel(gw.cpu(), gw_ref) <= 1e-2, flags
+    (o0, l0, _, _), (o1, l1, _, _) = res[0], res[_lib.LSE_PAIR]
+    assert torch.equal(o0, o1)
+    assert ((l1[:, 0] + l1[:, 1]) * np.log(2.0) - l0).abs().max() <= 1e-6 * l0.abs().max() + 1e-6
+    assert (l0.double() - lse_ref).abs().max() <= 2e-3
+    assert (o0[:, 0].double() - lp_ref).abs().max() <= 2e-3 and (o0[:, 1].double() - ent_ref).abs().max() <= 2e-3
+
+
 def test_scored_rows_equal_the_unscored_rows_bitwise():
     n, d, V = 777, 128, 3000
     h, W, y = _inputs(n, d, V, torch.bfloat16, seed=2)
