@@ -1,13 +1,13 @@
 // The MFMA GEMM core shared by every contraction of the LM-head path.
 //
-//   C[m, n] = sum_k A[m, k] * B[n, k]        (both operands K-contiguous, "NT")
+//   C[m, n] = sum_k A[m, k] * B[n, k]        (operands K-contiguous, "NT", or one of them K-major: OpColsN)
 //
-// One workgroup = 256 threads = 4 wave64s computes a 256 x 256 tile of C; the waves sit 2 x 2 and
-// each owns a 128 x 128 sub-tile, i.e. all 256 accumulation registers of a wave: 8 x 8 blocks of
-// v_mfma_f32_16x16x32_{bf16,f16} in the 16-bit loop (Acc16), 4 x 4 blocks of v_mfma_f32_32x32x2_f32 in the fp32
-// loop (Acc32). Under the part's power limit the 16x16x32 form
-// sustains 12% more bf16 FLOP/s than the 32x32x16 one on random operands (2.10 against 1.88 PFLOP/s, a
-// register-only loop on every SIMD), and each MFMA streams fewer accumulator bytes per FLOP.
+// One workgroup computes a 256 x 256 tile of C. The 16-bit loop runs 512 threads = 8 wave64s, two per SIMD, sat
+// 2 x 4, each owning a 128 x 64 sub-tile as 8 x 4 blocks of v_mfma_f32_16x16x32_{bf16,f16} (Acc16N<4>, 128
+// accumulation registers): while one wave of a SIMD waits on a stage the other issues MFMAs. The fp32 loop runs 4
+// waves, 2 x 2, each 128 x 128 as 4 x 4 blocks of v_mfma_f32_32x32x2_f32 (Acc32). Under the part's power limit the
+// 16x16x32 form sustains 12% more bf16 FLOP/s than the 32x32x16 one on random operands (2.10 against 1.88 PFLOP/s,
+// a register-only loop on every SIMD), and each MFMA streams fewer accumulator bytes per FLOP.
 //
 // The mainloop feeds the MFMAs from LDS: the A and B K-slices go straight from global memory into a ring of
 // LDS stages by buffer_load_dwordx4 ... lds (no register hop), with the instruction order fixed in the source:
@@ -297,7 +297,7 @@ __device__ __forceinline__ void mainloop_dma(const Operand &A, const Operand &B,
 // B_(k-1)), its B slice under K-step 1 (the slot freed at B_k). At B_k only stage k + 2's A slice may still be in
 // flight: vmcnt(32 / NW).
 //
-//   OpRows128 (K-contiguous rows): a slice is 256 rows x 128 bytes. Chunk c (0..7) of row r sits at physical
+//   OpRowsN (K-contiguous rows): a slice is 256 rows x 128 bytes. Chunk c (0..7) of row r sits at physical
 //     chunk c ^ ((r >> 1) & 7), so a 16-lane pass of fragment reads (rows r0..r0+15, r0 a multiple of 16, of
 //     one logical chunk) covers all 64 banks once. DMA instruction q of wave w fills slice rows (NW q + w) * 8 ..
 //     + 8; lane i takes row + (i >> 3) and physical chunk i & 7, so the 8 lanes of a row fetch its 128 bytes.
@@ -355,7 +355,6 @@ struct OpRowsN {
   }
 };
 
-typedef OpRowsN<4, 128> OpRows128;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -609,7 +608,6 @@ struct Acc16N {
   }
   static __device__ __forceinline__ bool col_lane(int lane) { return lane < 16; }
 };
-typedef Acc16N<8> Acc16;
 // The fp32 path's layout.
 __device__ __forceinline__ int acc_row(int wm, int i, int v, int lane) { return Acc32::row(wm, i, v, lane); }
 __device__ __forceinline__ int acc_col(int wn, int j, int lane) { return Acc32::col(wn, j, lane); }
