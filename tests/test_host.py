@@ -204,3 +204,18 @@ def test_tiled_and_no_inner():
 
 def test_prefix_tree_module_exports():
     assert callable(prefix_tree.build_tree) and callable(prefix_tree.tree_head_output)
+
+
+def test_gather_flag_asks_for_the_row_copy_only_past_2_gib_through_idx():
+    """The torch op requests OCTO_WS_GATHER exactly when rows are read through idx from a matrix whose rows x row
+    stride x element bytes reach 2^31 - 1, the C ABI's own test (meta tensors: shapes and strides, no memory)."""
+    from octopus_amd import _lib
+    from octopus_amd.head_op import _gather_flag
+    idx = torch.zeros(4, dtype=torch.int64)
+    small = torch.empty_strided((262_143, 4096), (4096, 1), dtype=torch.bfloat16, device="meta")  # 2^31 - 2^13 B
+    big = torch.empty_strided((262_144, 4096), (4096, 1), dtype=torch.bfloat16, device="meta")    # 2^31 B
+    wide = torch.empty_strided((131_072, 4096), (8192, 1), dtype=torch.bfloat16, device="meta")   # strided: 2^31 B
+    assert _gather_flag(small, idx) == 0
+    assert _gather_flag(big, idx) == _lib.WS_GATHER
+    assert _gather_flag(wide, idx) == _lib.WS_GATHER
+    assert _gather_flag(big, None) == 0  # without idx each tile's rows are addressed from their own base
