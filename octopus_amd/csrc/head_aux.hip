@@ -54,6 +54,26 @@ __device__ __forceinline__ float row_dot(const void *h, int h_dtype, int64_t hof
     }
     return dot;
   }
+  if (h_dtype == OCTO_BF16 && w_dtype == OCTO_FP8E4M3 && d % 16 == 0) {
+    // 16 e4m3 weights per 16-byte load against 16 bf16 hidden values (rows are 16-byte aligned: the head's checks);
+    // byte-wise loads made the merge 0.75 ms at 114,688 rows, d 2560
+    const char *hp = (const char *)h + hoff * 2;
+    const uint8_t *wp = (const uint8_t *)w + woff;
+    for (int k = lane; k < d / 16; k += 64) {
+      const i32x4 wv = *(const i32x4 *)(wp + k * 16);
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        float a[8];
+        unpack8(*(const i32x4 *)(hp + k * 32 + half * 16), false, a);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t byte = ((uint32_t)wv[2 * half + (e >> 2)] >> (8 * (e & 3))) & 0xffu;
+          dot = __builtin_fmaf(a[e], e4m3_to_f32(byte), dot);
+        }
+      }
+    }
+    return dot;
+  }
   for (int k = lane; k < d; k += 64) {
     const float hv = load_as_f32(h, h_dtype, hoff + k);
     const float wv = w_dtype == OCTO_FP8E4M3 ? e4m3_to_f32(((const uint8_t *)w)[woff + k])
