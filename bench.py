@@ -217,6 +217,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="cfg3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--bwd-workspace-mib", type=int, default=0,
+                    help="give the backward this much workspace instead of the queried size (its plan of row passes "
+                         "and vocabulary chunks follows the workspace)")
     ap.add_argument("--hipblaslt", action="store_true",
                     help="only time torch.matmul (hipBLASLt) on the four plain GEMMs of the workload's step, "
                          "without any epilogue, for context; then exit")
@@ -254,6 +257,8 @@ def main() -> int:
 
     from octopus_amd import _lib, head_op
     from octopus_amd.workloads import CONFIGS, make_batch
+    if args.bwd_workspace_mib:
+        head_op.BWD_WORKSPACE_BYTES = args.bwd_workspace_mib << 20
 
     cfg = CONFIGS[args.workload]
     dev = torch.device("cuda", 0)

@@ -14,8 +14,9 @@
  *     octo_last_error() gives a message for the last failing call on the calling thread;
  *   - takes plain device pointers, element strides and sizes, and an explicit hipStream_t
  *     (passed as void* so that the header needs no HIP include); all work is queued on that stream;
- *   - allocates nothing: scratch memory comes from a caller-provided workspace whose size the
- *     matching *_workspace_bytes query returns;
+ *   - allocates no device memory: scratch memory comes from a caller-provided workspace whose size the
+ *     matching *_workspace_bytes query returns (the one exception is the timing hook below, which
+ *     creates HIP events while it is enabled);
  *   - does no device-to-host synchronisation: row counts produced on the device (octo_compact_rows)
  *     are read by the kernels themselves.
  *
@@ -84,8 +85,16 @@ int octo_timing_read(const char *kernel, int *launches, double *total_ms);
 /* Workspace bytes for octo_head_fwd (flags without OCTO_WS_BACKWARD) or octo_head_bwd
  * (OCTO_WS_BACKWARD [| OCTO_WS_NO_GRADW]) at n_max rows, width d, vocabulary V. With idx, a hidden matrix of
  * 2 GiB or more (h_rows * ldh * element bytes >= 2^31) is first gathered into the workspace (the GEMMs address
- * mapped rows with 32-bit offsets): add OCTO_WS_GATHER for those calls. */
+ * mapped rows with 32-bit offsets): add OCTO_WS_GATHER for those calls.
+ * Backward: the size of its plan at a 2 GiB staging budget (see octo_head_bwd); a smaller workspace is accepted
+ * down to the plan at a 1 MiB budget, a larger one may run fewer chunks. */
 int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes);
+
+/* The chunking octo_head_bwd runs in ws_bytes of workspace (a planning aid; no counterpart in the reference):
+ * plan[0] rows per pass, plan[1] passes, plan[2] vocabulary columns per chunk, plan[3] chunks. flags as for
+ * octo_head_workspace_bytes (OCTO_WS_NO_GRADW, OCTO_WS_GATHER); grad_h is assumed asked for.
+ * OCTO_EWORKSPACE when no plan fits. */
+int octo_head_bwd_plan(int64_t n_max, int d, int V, int w_dtype, int flags, size_t ws_bytes, int64_t plan[4]);
 
 /* Masked-row compaction (lm_head.py:128 `scored.nonzero()[:, 0]`): idx[0..count) = the positions
  * r < n with mask[r] != 0, ascending; *count written on the device. idx must hold n entries;
@@ -119,7 +128,11 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
  *   grad_w : NULL or [V, d] (row stride d) of gw_dtype (BF16, F16 or F32); = or += (OCTO_GRADW_ACCUMULATE),
  *            summed in fp32 and rounded once to gw_dtype. Not available for FP8E4M3 weights.
  * The logits are recomputed tile by tile; dz = g (onehot - p) / T is staged in the workspace (bf16 / f16 / f32)
- * in passes of at most 65,536 rows. */
+ * one (row pass, vocabulary chunk) at a time: passes of at most 32,768 rows, chunks of a multiple of 256 columns
+ * as wide as the staging budget allows. The staging (dz, fp32 grad_h partials across chunks, the chunk's W^T or
+ * widened fp8 rows) stays within the budget; outside it are h^T of a pass [d, rows] and, over several passes with
+ * a 16-bit grad_w, fp32 grad_w partials [V, d]. The plan is the largest that fits ws_bytes (octo_head_bwd_plan);
+ * fp32 sums across chunks and passes follow it, so results are reproducible for a given workspace size. */
 int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                   const void *w, int64_t ldw, int w_dtype, const float *w_scale,
                   const int64_t *labels, const int64_t *idx, const int32_t *count,

@@ -42,6 +42,7 @@ SIGNATURES = {
     "octo_timing_enable": [_i32],
     "octo_timing_read": [ctypes.c_char_p, ctypes.POINTER(_i32), ctypes.POINTER(ctypes.c_double)],
     "octo_head_workspace_bytes": [_i64, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)],
+    "octo_head_bwd_plan": [_i64, _i32, _i32, _i32, _i32, _sz, ctypes.POINTER(_i64)],
     "octo_compact_rows": [_p, _i64, _p, _p, _p],
     "octo_head_fwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                       _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, _p, _sz, _p],
@@ -111,6 +112,13 @@ def workspace_bytes(n_max: int, d: int, V: int, w_dtype: int, flags: int) -> int
     out = _sz(0)
     call("octo_head_workspace_bytes", n_max, d, V, w_dtype, flags, ctypes.byref(out))
     return out.value
+
+
+def bwd_plan(n_max: int, d: int, V: int, w_dtype: int, flags: int, ws_bytes: int) -> tuple[int, int, int, int]:
+    """(rows per pass, passes, vocabulary columns per chunk, chunks) that octo_head_bwd runs in ws_bytes."""
+    out = (_i64 * 4)()
+    call("octo_head_bwd_plan", n_max, d, V, w_dtype, flags, ws_bytes, out)
+    return tuple(out)
 
 
 def timing_read(kernel: str) -> tuple[int, float]:

@@ -68,10 +68,17 @@ struct TimedLaunch {
   ~TimedLaunch() { done(); }
 };
 
-// Backward rows per pass: bounds the dz staging buffer (16-bit, token-major: 2 V_pad bytes per row, 16.8 GB at 65,536
-// rows and V = 128,256, 6% of a 288 GB MI355X). A pass runs each gradient GEMM once; a later pass with few rows runs them
-// at low occupancy and makes grad_W round-trip fp32 partials, so the cap is set to take 65,536 packed tokens whole.
-constexpr int64_t kPassRows = 65536;
+// The backward stages dz = g (onehot - p) / T per (row pass, vocabulary chunk): [P rows, Vc columns] in the MFMA
+// type. Per chunk, grad_W rows v0 .. v0 + Vc are complete once every pass has run, and grad_h of the pass's rows sums
+// over the chunks. Rows that carry across chunks (grad_h) or passes (grad_W) are summed in fp32: grad_h partials
+// [P, d], grad_W partials [V, d]. For a fixed staging area P x Vc the partial round trips cost in proportion to
+// 1 / Vc + 1 / P, so rows per pass are capped where the chunk is about square at the default budget.
+constexpr int64_t kPassRowsMax = 32768;
+// Default budget of the chunk-sized staging (dz, grad_h partials, the chunk's W^T or widened fp8 rows): 2 GiB, against
+// 2 V bytes per row for the whole dz (7.5 GB at 24,576 rows and V = 151,936).
+constexpr size_t kStagingBudget = (size_t)2 << 30;
+// The forward widens fp8 weights to bf16 one vocabulary chunk at a time, at most this many bytes of them.
+constexpr size_t kFwdWideBytes = (size_t)256 << 20;
 constexpr size_t kAlign = 256;
 #ifndef OCTO_GROUP_M
 #define OCTO_GROUP_M 4
@@ -81,25 +88,43 @@ constexpr int kGroupM = OCTO_GROUP_M;  // M-tiles per L2 group of the tile order
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 int elem_bytes(int dt) { return dt == OCTO_F32 ? 4 : (dt == OCTO_FP8E4M3 ? 1 : 2); }
-// MFMA operand type for a weight dtype: fp8 weights are widened to bf16 in LDS.
+// MFMA operand type for a weight dtype: fp8 weights are widened to bf16 (exactly) in the workspace, one vocabulary
+// chunk at a time, and run the bf16 GEMMs with their row scale applied in the epilogues.
 int staged_dtype(int w_dtype) { return w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_dtype; }
 
+// Vocabulary chunks of Vc columns (a multiple of 256) covering V_pad: the smallest count whose chunks fit vmax, then
+// balanced, then the count recomputed so that no chunk is empty.
+void vocab_chunks(int64_t V_pad, int64_t vmax, int64_t &Vc, int64_t &chunks) {
+  chunks = cdiv(V_pad, vmax);
+  Vc = round_up(cdiv(V_pad, chunks), TM);
+  chunks = cdiv(V_pad, Vc);
+}
+
 struct FwdLayout {
-  int64_t mtiles;
+  int64_t mtiles, Vc, chunks;
   size_t part, wide, z, rows, total;
 };
 // Bytes of the contiguous copy of the n_max gathered hidden rows [n_max, d] (OCTO_WS_GATHER).
 size_t gather_bytes(int64_t n_max, int d, int h_dtype) { return align_up((size_t)n_max * d * elem_bytes(h_dtype)); }
 
-// part: (m, S, U) per (row, vocab tile). wide: fp8 weights widened to bf16 [V, d]. z: the GRPO tail's token count.
-// rows: the gathered hidden rows, when asked for (last, so the other offsets do not depend on it).
+// part: (m, S, U) per (row, vocab tile). wide: one chunk of fp8 weights widened to bf16 [Vc, d] (the forward GEMM runs
+// once per chunk; one chunk covering V for 16-bit weights). z: the GRPO tail's token count. rows: the gathered hidden
+// rows, when asked for (last, so the other offsets do not depend on it).
 FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype, bool gather) {
   FwdLayout L;
   L.mtiles = cdiv(V, TM);
+  const int64_t V_pad = L.mtiles * TM;
+  if (w_dtype == OCTO_FP8E4M3) {
+    const int64_t vmax = (int64_t)(kFwdWideBytes / ((size_t)d * 2)) / TM * TM;
+    vocab_chunks(V_pad, vmax < TM ? TM : vmax, L.Vc, L.chunks);
+  } else {
+    L.Vc = V_pad;
+    L.chunks = 1;
+  }
   L.part = 0;
   size_t off = align_up((size_t)n_max * L.mtiles * sizeof(f32x4));
   L.wide = off;
-  if (w_dtype == OCTO_FP8E4M3) off += align_up((size_t)V * d * 2);
+  if (w_dtype == OCTO_FP8E4M3) off += align_up((size_t)L.Vc * d * 2);
   L.z = off;
   off += kAlign;
   L.rows = off;
@@ -110,44 +135,104 @@ FwdLayout fwd_layout(int64_t n_max, int d, int V, int w_dtype, bool gather) {
 
 
 // The backward stages the gradient GEMMs' operands so each mainloop row fetch is whole cache lines: the pass's
-// hidden rows transposed to h^T [d, P] for grad_W = dz^T . h, and dz token-major [P, V_pad], which grad_h reads
-// K-contiguous and 16-bit grad_W K-major (transposing LDS reads). 16-bit grad_h = dz . W reads W K-major as stored
-// when V is a multiple of 64 (the loader's K-row granule) and d of 256 (its column granule); otherwise, and for
-// fp32, W^T [d, V_pad] is staged. fp32 dz is also written vocab-major [V_pad, P] for the fp32 loop, which reads
-// K-contiguous operands only.
+// hidden rows transposed to h^T [d, P] for grad_W = dz^T . h, and dz token-major [P, Vc] per vocabulary chunk, which
+// grad_h reads K-contiguous and 16-bit grad_W K-major (transposing LDS reads). 16-bit grad_h = dz . W reads the
+// chunk's W rows K-major as stored when V is a multiple of 64 (the loader's K-row granule) and d of 256 (its column
+// granule); otherwise, and for fp32, the chunk's W^T [d, Vc] is staged. fp32 dz is also written chunk-major [Vc, P]
+// for the fp32 loop, which reads K-contiguous operands only.
 bool gh_reads_w(int d, int V, int w_dtype) {
   return elem_bytes(staged_dtype(w_dtype)) == 2 && V % 64 == 0 && d % 256 == 0;
 }
 struct BwdLayout {
-  int64_t P, V_pad, passes;
+  int64_t P, passes, Vc, chunks, V_pad;
   int esz;
-  size_t wt, ht, dza, dzb, hit, wide, gacc, rows, total;
+  bool hacc_on, gacc_on;
+  size_t wt, ht, dza, dzb, hit, wide, hacc, gacc, rows, total;
 };
-BwdLayout bwd_layout(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw, bool gather) {
-  BwdLayout L;
+
+// The plan for a staging budget (0: unbounded, one chunk). Rows per pass start at kPassRowsMax (balanced over the
+// passes); the chunk width is the widest multiple of 256 whose staging fits the budget, and rows per pass halve
+// while not even 256 columns fit. Returns false when no plan fits (a budget below one 256 x 256 chunk).
+bool bwd_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw, bool gather, size_t budget,
+              BwdLayout &L) {
   L.esz = elem_bytes(staged_dtype(w_dtype));
   L.V_pad = round_up(V, TM);
-  L.P = n_max == 0 ? 0 : (round_up(n_max, TN) < kPassRows ? round_up(n_max, TN) : kPassRows);
-  L.passes = L.P == 0 ? 0 : cdiv(n_max, L.P);
+  const bool dz_a = need_gh || (need_gw && L.esz == 2), dz_b = need_gw && L.esz == 4;
+  const bool wt = need_gh && !gh_reads_w(d, V, w_dtype), wide = w_dtype == OCTO_FP8E4M3;
+  L.P = L.passes = 0;
+  L.Vc = L.V_pad;
+  L.chunks = 1;
+  if (n_max > 0) {
+    int64_t passes = cdiv(n_max, kPassRowsMax);
+    for (;;) {
+      const int64_t P = round_up(cdiv(n_max, passes), TN);
+      const size_t per_col = (size_t)P * L.esz * ((dz_a ? 1 : 0) + (dz_b ? 1 : 0)) + (wt ? (size_t)d * L.esz : 0) +
+                             (wide ? (size_t)d * 2 : 0);  // staging bytes per vocabulary column of a chunk
+      int64_t Vc = 0, chunks = 0;
+      if (budget == 0 || per_col * (size_t)L.V_pad <= budget) {
+        Vc = L.V_pad;
+        chunks = 1;
+      } else {
+        const size_t hb = need_gh ? (size_t)P * d * sizeof(float) : 0;  // grad_h partials, with more than one chunk
+        if (budget > hb) {
+          const int64_t vmax = (int64_t)((budget - hb) / per_col) / TM * TM;
+          if (vmax >= TM) vocab_chunks(L.V_pad, vmax, Vc, chunks);
+        }
+      }
+      if (chunks > 0) {
+        L.P = P;
+        L.passes = cdiv(n_max, P);
+        L.Vc = Vc;
+        L.chunks = chunks;
+        break;
+      }
+      if (P <= TN) return false;
+      passes = cdiv(n_max, P / 2);
+    }
+  }
+  L.hacc_on = need_gh && L.chunks > 1;
+  L.gacc_on = need_gw && L.passes > 1 && w_dtype != OCTO_F32;
   size_t off = 0;
-  L.wt = off;  // W^T [d, V_pad] (grad_h, unless it reads W K-major)
-  if (need_gh && !gh_reads_w(d, V, w_dtype)) off += align_up((size_t)d * L.V_pad * L.esz);
+  L.wt = off;  // W^T [d, Vc] of the chunk (grad_h, unless it reads W K-major)
+  if (wt) off += align_up((size_t)d * L.Vc * L.esz);
   L.ht = off;  // h^T [d, P] of the pass's rows (grad_W)
   if (need_gw) off += align_up((size_t)d * L.P * L.esz);
-  L.dza = off;  // dz [P, V_pad], token-major (grad_h; 16-bit grad_W)
-  if (need_gh || (need_gw && L.esz == 2)) off += align_up((size_t)L.P * L.V_pad * L.esz);
-  L.dzb = off;  // dz [V_pad, P], vocab-major (fp32 grad_W)
-  if (need_gw && L.esz == 4) off += align_up((size_t)L.V_pad * L.P * L.esz);
+  L.dza = off;  // dz [P, Vc], token-major (grad_h; 16-bit grad_W)
+  if (dz_a) off += align_up((size_t)L.P * L.Vc * L.esz);
+  L.dzb = off;  // dz [Vc, P], chunk-major (fp32 grad_W)
+  if (dz_b) off += align_up((size_t)L.Vc * L.P * L.esz);
   L.hit = off;  // dz at each row's label [P] fp32 (16-bit dz epilogue)
   if (L.esz == 2) off += align_up((size_t)L.P * sizeof(float));
-  L.wide = off;  // fp8 weights widened to bf16 [V, d] (the dz recompute's operand)
-  if (w_dtype == OCTO_FP8E4M3) off += align_up((size_t)V * d * 2);
+  L.wide = off;  // the chunk's fp8 weights widened to bf16 [Vc, d] (the dz recompute's and grad_h's operand)
+  if (wide) off += align_up((size_t)L.Vc * d * 2);
+  L.hacc = off;  // fp32 grad_h partial sums across chunks [P, d]
+  if (L.hacc_on) off += align_up((size_t)L.P * d * sizeof(float));
   L.gacc = off;  // fp32 grad_W partial sums across passes, for a 16-bit grad_W
-  if (need_gw && L.passes > 1 && w_dtype != OCTO_F32) off += align_up((size_t)V * d * sizeof(float));
+  if (L.gacc_on) off += align_up((size_t)V * d * sizeof(float));
   L.rows = off;  // the gathered hidden rows (OCTO_WS_GATHER), last
   if (gather) off += gather_bytes(n_max, d, w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_dtype);
   L.total = off;
-  return L;
+  return true;
+}
+
+// Candidate staging budgets, largest first: 2^(q / 4) bytes for q = 160 .. 80 (2^40 down to 2^20 in steps of 2^(1/4),
+// 2^31 among them).
+size_t staging_candidate(int q) {
+  static const uint32_t frac[4] = {4096, 4871, 5793, 6889};  // 2^(j / 4) x 4096
+  return ((size_t)1 << (q / 4 - 12)) * frac[q % 4];
+}
+constexpr int kBudgetQMax = 160, kBudgetQMin = 80;
+
+// The plan the backward runs in ws_bytes of workspace: unbounded if it fits, else the largest candidate staging
+// budget whose plan fits. With the queried size (the plan at kStagingBudget = 2^31, a candidate) this is that plan or
+// one with fewer chunks in no more bytes. Returns false when none fits.
+bool bwd_plan_for(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw, bool gather, size_t ws_bytes,
+                  BwdLayout &L) {
+  if (bwd_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, 0, L) && L.total <= ws_bytes) return true;
+  for (int q = kBudgetQMax; q >= kBudgetQMin; --q)
+    if (bwd_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, staging_candidate(q), L) && L.total <= ws_bytes)
+      return true;
+  return false;
 }
 
 struct Common {
@@ -222,12 +307,14 @@ Operand weight_operand(const void *w, int64_t ldw, const Common &cm, int V) {
   return A;
 }
 
-// The GEMMs' weight operand: W as stored, or for fp8 weights its bf16 widening in the workspace.
-Operand gemm_weight(const void *w, int64_t ldw, const Common &cm, int V, int d, void *wide, hipStream_t st, int &rc) {
+// The GEMMs' weight operand for the vocabulary rows [v0, v0 + vc): W as stored, or for fp8 weights those rows widened
+// to bf16 into `wide` (queued on st).
+Operand gemm_weight(const void *w, int64_t ldw, const Common &cm, int64_t v0, int64_t vc, int d, void *wide,
+                    hipStream_t st, int &rc) {
   rc = OCTO_OK;
-  if (!cm.fp8) return weight_operand(w, ldw, cm, V);
-  rc = launch_widen_fp8(w, ldw, V, d, wide, st);
-  Operand A = weight_operand(wide, d, cm, V);
+  if (!cm.fp8) return weight_operand((const char *)w + v0 * ldw * cm.wesz, ldw, cm, (int)vc);
+  rc = launch_widen_fp8((const uint8_t *)w + v0 * ldw, ldw, vc, d, wide, st);
+  Operand A = weight_operand(wide, d, cm, (int)vc);
   A.ld = (int64_t)d * 2;
   return A;
 }
@@ -311,15 +398,12 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
     if (rc) return rc;
   }
 
-  const Operand A = gemm_weight(w, ldw, cm, V, d, (char *)ws + L.wide, st, rc);
-  if (rc) return rc;
   void *gathered = cm.gather ? (char *)ws + L.rows : nullptr;
   if (gathered) {
     rc = launch_rows_gather(h, ldh * cm.hesz, idx, count, n_max, (int64_t)d * cm.hesz, gathered, st);
     if (rc) return rc;
   }
   const Operand B = hidden_operand(h, ldh, idx, count, 0, n_max, cm, gathered, d);
-  const GemmShape s = shape(V, n_max, d, kGroupM, 2, count, 0);
   StatsArgs e;
   e.part = (f32x4 *)((char *)ws + L.part);
   e.mtiles = L.mtiles;
@@ -327,11 +411,18 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
   e.wscale = w_scale;
   e.c = cm.c;
   e.pre = cm.pre;
-  {
-    TimedLaunch t("gemm_stats", st);
-    rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, A, B, s, e, st);
+  for (int64_t c = 0; c < L.chunks; ++c) {  // one chunk covering V, except for fp8 weights (widened chunk by chunk)
+    e.v0 = c * L.Vc;
+    const int64_t vc = (V - e.v0) < L.Vc ? (V - e.v0) : L.Vc;
+    const Operand A = gemm_weight(w, ldw, cm, e.v0, vc, d, (char *)ws + L.wide, st, rc);
+    if (rc) return rc;
+    const GemmShape s = shape(vc, n_max, d, kGroupM, 2, count, 0);
+    {
+      TimedLaunch t("gemm_stats", st);
+      rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, A, B, s, e, st);
+    }
+    if (rc) return rc;
   }
-  if (rc) return rc;
 
   MergeArgs m;
   m.part = e.part;
@@ -416,10 +507,27 @@ int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flag
   OCTO_CHECK_ARG(n_max >= 0 && d > 0 && V > 0, "workspace_bytes: bad sizes");
   OCTO_CHECK_ARG(w_dtype >= OCTO_BF16 && w_dtype <= OCTO_FP8E4M3, "workspace_bytes: dtype %d", w_dtype);
   if (flags & OCTO_WS_BACKWARD) {
-    *bytes = bwd_layout(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW), flags & OCTO_WS_GATHER).total;
+    BwdLayout L;
+    if (!bwd_plan(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW), flags & OCTO_WS_GATHER, kStagingBudget, L))
+      return octo_fail(OCTO_EINVAL, "workspace_bytes: no backward plan for d=%d", d);
+    *bytes = L.total;
   } else {
     *bytes = fwd_layout(n_max, d, V, w_dtype, flags & OCTO_WS_GATHER).total;
   }
+  return OCTO_OK;
+}
+
+int octo_head_bwd_plan(int64_t n_max, int d, int V, int w_dtype, int flags, size_t ws_bytes, int64_t plan[4]) {
+  OCTO_CHECK_ARG(plan != nullptr, "bwd_plan: null pointer");
+  OCTO_CHECK_ARG(n_max >= 0 && d > 0 && V > 0, "bwd_plan: bad sizes");
+  OCTO_CHECK_ARG(w_dtype >= OCTO_BF16 && w_dtype <= OCTO_FP8E4M3, "bwd_plan: dtype %d", w_dtype);
+  BwdLayout L;
+  if (!bwd_plan_for(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW), flags & OCTO_WS_GATHER, ws_bytes, L))
+    return octo_fail(OCTO_EWORKSPACE, "bwd_plan: no plan fits %zu bytes", ws_bytes);
+  plan[0] = L.P;
+  plan[1] = L.passes;
+  plan[2] = L.Vc;
+  plan[3] = L.chunks;
   return OCTO_OK;
 }
 
@@ -462,47 +570,43 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
   }
   const bool need_gh = grad_h != nullptr, need_gw = grad_w != nullptr;
   if (n_max == 0 || (!need_gh && !need_gw)) return OCTO_OK;
-  const BwdLayout L = bwd_layout(n_max, d, V, w_dtype, need_gh, need_gw, cm.gather);
-  if (!ws || ws_bytes < L.total)
-    return octo_fail(OCTO_EWORKSPACE, "head_bwd: workspace %zu < %zu bytes%s", ws_bytes, L.total,
+  BwdLayout L;
+  if (!ws || !bwd_plan_for(n_max, d, V, w_dtype, need_gh, need_gw, cm.gather, ws_bytes, L)) {
+    BwdLayout Lmin;
+    size_t least = 0;
+    for (int q = kBudgetQMin; q <= kBudgetQMax; ++q)
+      if (bwd_plan(n_max, d, V, w_dtype, need_gh, need_gw, cm.gather, staging_candidate(q), Lmin) &&
+          (!least || Lmin.total < least))
+        least = Lmin.total;
+    return octo_fail(OCTO_EWORKSPACE, "head_bwd: workspace %zu bytes, below the smallest plan's %zu%s",
+                     ws ? ws_bytes : (size_t)0, least,
                      cm.gather ? " (hidden of 2 GiB or more through idx: query with OCTO_WS_GATHER)" : "");
+  }
   if (need_gw && L.passes > 1 && gw_dtype != OCTO_F32 && w_dtype == OCTO_F32)
     return octo_fail(OCTO_EUNSUPPORTED, "head_bwd: 16-bit grad_w of fp32 weights over several passes");
   hipStream_t st = (hipStream_t)stream;
   char *wsb = (char *)ws;
   void *wt = wsb + L.wt, *ht = wsb + L.ht, *dza = wsb + L.dza, *dzb = wsb + L.dzb;
-  float *gacc = (float *)(wsb + L.gacc);
+  float *gacc = (float *)(wsb + L.gacc), *hacc = (float *)(wsb + L.hacc);
   const int esz = L.esz;
-  const bool gw_staged = need_gw && L.passes > 1 && gw_dtype != OCTO_F32;  // fp32 partials in gacc
 
-  const Operand Aw = gemm_weight(w, ldw, cm, V, d, wsb + L.wide, st, rc);
-  if (rc) return rc;
   void *gathered = cm.gather ? wsb + L.rows : nullptr;
   if (gathered) {
     rc = launch_rows_gather(h, ldh * cm.hesz, idx, count, n_max, (int64_t)d * cm.hesz, gathered, st);
     if (rc) return rc;
   }
-  // W^T [d, V_pad] in the staged type (fp8 weights: from their exact bf16 widening; the row scale is in dz), unless
-  // grad_h reads W (or the widening) K-major
+  // grad_h reads the chunk's W rows (or their bf16 widening) K-major as stored, or else their staged W^T [d, Vc]
   const bool wk = gh_reads_w(d, V, w_dtype);
-  if (need_gh && !wk) {
-    if (cm.fp8) rc = launch_transpose(wsb + L.wide, d, OCTO_BF16, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt,
-                                      L.V_pad, cm.dt, st);
-    else rc = launch_transpose(w, ldw, w_dtype, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt, L.V_pad, cm.dt, st);
-    if (rc) return rc;
-  }
 
   for (int64_t p = 0; p < L.passes; ++p) {
     const int64_t r0 = p * L.P;
     const int64_t rows = (n_max - r0) < L.P ? (n_max - r0) : L.P;
-    const bool last = p + 1 == L.passes;
+    const bool last_pass = p + 1 == L.passes;
 
-    // dz of this pass, recomputed tile by tile
     const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm, gathered, d);
-    const GemmShape s1 = shape(V, rows, d, kGroupM, 2, count, r0);
     DzArgs e;
     e.dzA = (need_gh || (need_gw && esz == 2)) ? dza : nullptr;
-    e.ldA = L.V_pad;
+    e.ldA = L.Vc;
     e.dzB = (need_gw && esz == 4) ? dzb : nullptr;
     e.ldB = L.P;
     e.lse = lse;
@@ -547,57 +651,86 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
       if (rc) return rc;
       e.hit = ha.hit;
     }
-    {
-      TimedLaunch t("gemm_dz", st);
-      rc = launch_gemm_dz(cm.dt, cm.fp8, use_tanh != 0, Aw, Bh, s1, e, st);
-    }
-    if (rc) return rc;
-
-    if (need_gh) {  // grad_h[rows] = dz . W   (K = V, or V_pad through the staged W^T)
-      const Operand A2 = plain_operand(dza, L.V_pad * esz, rows, count, r0);
-      const Operand B2 = wk ? plain_operand(Aw.base, Aw.ld, d, nullptr, 0) : plain_operand(wt, L.V_pad * esz, d, nullptr, 0);
-      const GemmShape s2 = shape(rows, d, wk ? V : L.V_pad, kGroupM, 1, count, r0);
-      StoreArgs o;
-      o.C = (char *)grad_h + r0 * ld_gh * elem_bytes(gh_dtype);
-      o.addend = nullptr;
-      o.ldc = ld_gh;
-      o.dtype = gh_dtype;
-      o.accumulate = 0;
-      {
-        TimedLaunch t("gemm_store_grad_h", st);
-        rc = launch_gemm_store(cm.dt, A2, B2, s2, o, st, wk ? KM_B : KM_NONE);
-      }
-      if (rc) return rc;
-    }
-    if (need_gw) {  // grad_W += dz^T . h   (K = this pass's rows)
+    if (need_gw) {  // h^T [d, P] of the pass's rows, zero past the count (grad_W's K-contiguous operand)
       const int64_t rows_pad = round_up(rows, TN);
       rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, nullptr,
                             idx ? idx + r0 : nullptr, count, r0, rows, rows_pad, d, ht, L.P, cm.dt, st);
       if (rc) return rc;
-      const int kmajor = esz == 2 ? KM_A : KM_NONE;  // dz token-major read K-major, else the fp32 vocab-major copy
-      const Operand A3 = kmajor ? plain_operand(dza, L.V_pad * esz, L.P, nullptr, 0)
-                                : plain_operand(dzb, L.P * esz, L.V_pad, nullptr, 0);
-      const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
-      const GemmShape s3 = shape(V, d, rows, kGroupM, 3, count, r0);
-      StoreArgs o;
-      const bool acc_out = flags & OCTO_GRADW_ACCUMULATE;
-      if (gw_staged && !last) {  // fp32 partial sums of the passes so far
-        o.C = gacc;
-        o.addend = nullptr;
-        o.dtype = OCTO_F32;
-        o.accumulate = p > 0 ? 1 : 0;
-      } else {
-        o.C = grad_w;
-        o.addend = (gw_staged && p > 0) ? gacc : nullptr;
-        o.dtype = gw_dtype;
-        o.accumulate = (acc_out || (!gw_staged && p > 0)) ? 1 : 0;
-      }
-      o.ldc = d;
+    }
+
+    for (int64_t c = 0; c < L.chunks; ++c) {
+      const int64_t v0 = c * L.Vc;
+      const int64_t vc = (V - v0) < L.Vc ? (V - v0) : L.Vc;           // vocabulary rows of the chunk
+      const int64_t vc_pad = (L.V_pad - v0) < L.Vc ? (L.V_pad - v0) : L.Vc;  // dz columns written (zero past V)
+      const bool first_chunk = c == 0, last_chunk = c + 1 == L.chunks;
+
+      // dz of the pass's rows over the chunk, recomputed tile by tile
+      const Operand Aw = gemm_weight(w, ldw, cm, v0, vc, d, wsb + L.wide, st, rc);
+      if (rc) return rc;
+      e.v0 = v0;
       {
-        TimedLaunch t("gemm_store_grad_w", st);
-        rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st, kmajor);
+        TimedLaunch t("gemm_dz", st);
+        rc = launch_gemm_dz(cm.dt, cm.fp8, use_tanh != 0, Aw, Bh, shape(vc, rows, d, kGroupM, 2, count, r0), e, st);
       }
       if (rc) return rc;
+
+      if (need_gh) {  // grad_h[rows] (+)= dz . W[v0 .. v0 + vc)   (K = vc, or vc_pad through the staged W^T)
+        if (!wk) {  // W^T [d, Vc] of the chunk's rows in the staged type (fp8: from the widened rows), zero past vc
+          rc = launch_transpose(Aw.base, Aw.ld / esz, cm.dt, nullptr, nullptr, nullptr, 0, vc, L.Vc, d, wt, L.Vc,
+                                cm.dt, st);
+          if (rc) return rc;
+        }
+        const Operand A2 = plain_operand(dza, L.Vc * esz, rows, count, r0);
+        const Operand B2 = wk ? plain_operand(Aw.base, Aw.ld, d, nullptr, 0) : plain_operand(wt, L.Vc * esz, d, nullptr, 0);
+        const GemmShape s2 = shape(rows, d, wk ? vc : vc_pad, kGroupM, 1, count, r0);
+        StoreArgs o;
+        o.ld_add = d;
+        if (L.chunks > 1 && !last_chunk) {  // fp32 partial sums of the chunks so far
+          o.C = hacc;
+          o.addend = nullptr;
+          o.ldc = d;
+          o.dtype = OCTO_F32;
+          o.accumulate = first_chunk ? 0 : 1;
+        } else {
+          o.C = (char *)grad_h + r0 * ld_gh * elem_bytes(gh_dtype);
+          o.addend = L.chunks > 1 ? hacc : nullptr;
+          o.ldc = ld_gh;
+          o.dtype = gh_dtype;
+          o.accumulate = 0;
+        }
+        {
+          TimedLaunch t("gemm_store_grad_h", st);
+          rc = launch_gemm_store(cm.dt, A2, B2, s2, o, st, wk ? KM_B : KM_NONE);
+        }
+        if (rc) return rc;
+      }
+      if (need_gw) {  // grad_W[v0 .. v0 + vc) (+)= dz^T . h   (K = this pass's rows)
+        const int kmajor = esz == 2 ? KM_A : KM_NONE;  // dz token-major read K-major, else the fp32 chunk-major copy
+        const Operand A3 = kmajor ? plain_operand(dza, L.Vc * esz, L.P, nullptr, 0)
+                                  : plain_operand(dzb, L.P * esz, L.Vc, nullptr, 0);
+        const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
+        const GemmShape s3 = shape(vc, d, rows, kGroupM, 3, count, r0);
+        StoreArgs o;
+        const bool acc_out = flags & OCTO_GRADW_ACCUMULATE;
+        if (L.gacc_on && !last_pass) {  // fp32 partial sums of the passes so far
+          o.C = gacc + v0 * d;
+          o.addend = nullptr;
+          o.dtype = OCTO_F32;
+          o.accumulate = p > 0 ? 1 : 0;
+        } else {
+          o.C = (char *)grad_w + v0 * d * elem_bytes(gw_dtype);
+          o.addend = (L.gacc_on && p > 0) ? gacc + v0 * d : nullptr;
+          o.dtype = gw_dtype;
+          o.accumulate = (acc_out || (!L.gacc_on && p > 0)) ? 1 : 0;
+        }
+        o.ldc = d;
+        o.ld_add = d;
+        {
+          TimedLaunch t("gemm_store_grad_w", st);
+          rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st, kmajor);
+        }
+        if (rc) return rc;
+      }
     }
   }
   return OCTO_OK;

@@ -2,17 +2,18 @@
 //
 //   gemm_stats : S^T = W . H^T tile -> per (row, vocab tile) online softmax statistics (m, S, U)
 //                (forward; octopus/rl/lm_head.py:102-112 without the [rows, V] logits)
-//   gemm_dz    : the same tile recomputed -> dz = g (onehot - p) / T * post'(z), written as bf16 in
-//                the row-major [tokens, V] layout and/or the vocab-major [V, tokens] layout
+//   gemm_dz    : the same tile recomputed -> dz = g (onehot - p) / T * post'(z) of one vocabulary chunk, written
+//                token-major [tokens, chunk columns] in the 16-bit MFMA type (fp32 inputs: also chunk-major)
 //                (backward recompute, lm_head.py:118-121 under checkpoint)
-//   gemm_store : plain C = A . B^T with fp32/bf16/f16 output, optionally accumulated: grad_h = dz . W from a
-//                staged W^T, grad_W = dz^T . h from vocab-major dz and a staged h^T (both operands K-contiguous)
+//   gemm_store : plain C = A . B^T with fp32/bf16/f16 output, optionally accumulated or with an fp32 addend:
+//                grad_h = dz . W (dz read K-contiguous, W read K-major as stored), grad_W = dz^T . h (dz read
+//                K-major by transposing LDS reads, h^T staged K-contiguous)
 //
-// Orientation: the first operand (MFMA "A", tile rows) of gemm_stats / gemm_dz is the vocabulary,
-// the second (tile columns) the tokens. In the 32x32 MFMA output layout a lane holds one column
-// and 16 rows, so each lane holds 64 vocabulary entries of each of its 4 tokens and the softmax
-// reductions over the vocabulary are almost entirely in registers: one lane-pair exchange (rows
-// split across lane halves) and one LDS exchange between the two waves that share the tokens.
+// Orientation: the first operand (MFMA "A", tile rows) of gemm_stats / gemm_dz is the vocabulary, the second (tile
+// columns) the tokens. The 16-bit kernels run v_mfma_f32_16x16x32 on 8 waves of 128 x 64 (Acc16N<4>): a lane holds
+// 32 vocabulary rows of each of its 4 token columns, so the softmax reductions over the vocabulary are in registers
+// plus a 4-lane shuffle and one LDS exchange between the two waves of a token column.
+// fp32 operands run v_mfma_f32_32x32x2 on 4 waves (Acc32).
 #include <type_traits>
 
 #include "gemm_nt.h"
@@ -115,9 +116,10 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   lds_f32x4 *red = (lds_f32x4 *)smem;
   f32x16 acc[4][4];
   mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
-  pre_transform<Acc32, false, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-  if (m0 + TM > e.V) stats_cols<Acc32, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
-  else stats_cols<Acc32, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  const int64_t ma = e.v0 + m0;  // first vocabulary row of the tile
+  pre_transform<Acc32, false, TANH>(acc, ma, wm, lane, e.wscale, e.V, e.pre);
+  if (ma + TM > e.V) stats_cols<Acc32, true>(acc, ma, wm, wn, lane, e.V, e.c, red);
+  else stats_cols<Acc32, false>(acc, ma, wm, wn, lane, e.V, e.c, red);
   __syncthreads();
   const int t = threadIdx.x;
   if (t < nvalid) {
@@ -126,7 +128,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
     Stat3 r = stat_merge(sa, sb);
     f32x4 o;
     o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
-    e.part[(n0 + t) * e.mtiles + mt] = o;
+    e.part[(n0 + t) * e.mtiles + e.v0 / TM + mt] = o;
   }
 }
 
@@ -374,8 +376,10 @@ __device__ __forceinline__ void dz_stage(const typename L::V (&acc)[L::NI][L::NJ
   }
 }
 
+// ma: the tile's first vocabulary row; m0: its first dz column (ma - v0)
 template <class L, typename P2, int NT = NTHREADS>
-__device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0, int64_t nvalid, lds_char *tile) {
+__device__ __forceinline__ void dz_write(const DzArgs &e, int64_t ma, int64_t m0, int64_t n0, int64_t nvalid,
+                                         lds_char *tile) {
   typedef typename std::conditional<std::is_same<P2, bf16x2>::value, __bf16, _Float16>::type ET;
   const int t = threadIdx.x;
   // the label entry of token t (column t of the tile), loaded before the barrier that ends the dense pass
@@ -383,8 +387,8 @@ __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t m0, int64_t n0
   float hv = 0.f;
   if (t < nvalid) {
     const int64_t r = e.row_off + n0 + t;
-    const int64_t y = e.labels[e.label_idx ? e.label_idx[r] : r] - m0;
-    if (y >= 0 && y < TM && m0 + y < e.V) {
+    const int64_t y = e.labels[e.label_idx ? e.label_idx[r] : r] - ma;
+    if (y >= 0 && y < TM && ma + y < e.V) {
       yl = (int)y;
       hv = e.hit[n0 + t];
     }
@@ -414,17 +418,17 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1;
   f32x16 acc[4][4];
   mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
-  dz_in_place<false, TANH>(acc, e, m0, n0, nvalid, wm, wn, lane);
-  dz_store_direct(acc, e, m0, n0, wm, wn, lane);
+  dz_in_place<false, TANH>(acc, e, e.v0 + m0, n0, nvalid, wm, wn, lane);  // vocabulary rows from v0 + m0
+  dz_store_direct(acc, e, m0, n0, wm, wn, lane);                            // dz columns from m0
 }
 
 // ---- epilogue: plain store -------------------------------------------------------------------
 
-// C = acc (+ addend, fp32, same strides) (+ C when ACC), rounded once to OT.
+// C = acc (+ addend, fp32, row stride ld_add) (+ C when ACC), rounded once to OT.
 template <class L, typename OT, bool ACC, bool ADD, bool EDGE>
 __device__ __forceinline__ void store_tile(const typename L::V (&acc)[L::NI][L::NJ], OT *C, const float *addend,
-                                           int64_t ldc, int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int wm,
-                                           int wn, int lane) {
+                                           int64_t ldc, int64_t ld_add, int64_t m0, int64_t n0, int64_t mvalid,
+                                           int64_t nvalid, int wm, int wn, int lane) {
 #pragma unroll
   for (int i = 0; i < L::NI; ++i)
 #pragma unroll
@@ -432,7 +436,7 @@ __device__ __forceinline__ void store_tile(const typename L::V (&acc)[L::NI][L::
       const int rr = L::row(wm, i, v, lane);
       if (EDGE && rr >= mvalid) continue;
       OT *crow = C + (m0 + rr) * ldc + n0;
-      const float *arow = ADD ? addend + (m0 + rr) * ldc + n0 : nullptr;
+      const float *arow = ADD ? addend + (m0 + rr) * ld_add + n0 : nullptr;
 #pragma unroll
       for (int j = 0; j < L::NJ; ++j) {
         const int cc = L::col(wn, j, lane);
@@ -447,24 +451,24 @@ __device__ __forceinline__ void store_tile(const typename L::V (&acc)[L::NI][L::
 
 template <class L, typename OT, bool ACC, bool ADD>
 __device__ __forceinline__ void store_edge(const typename L::V (&acc)[L::NI][L::NJ], OT *C, const float *addend,
-                                           int64_t ldc, int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid, int wm,
-                                           int wn, int lane) {
-  if (mvalid < TM || nvalid < TN) store_tile<L, OT, ACC, ADD, true>(acc, C, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
-  else store_tile<L, OT, ACC, ADD, false>(acc, C, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+                                           int64_t ldc, int64_t ld_add, int64_t m0, int64_t n0, int64_t mvalid,
+                                           int64_t nvalid, int wm, int wn, int lane) {
+  if (mvalid < TM || nvalid < TN)
+    store_tile<L, OT, ACC, ADD, true>(acc, C, addend, ldc, ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
+  else store_tile<L, OT, ACC, ADD, false>(acc, C, addend, ldc, ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
 }
 
 template <class L, typename OT>
-__device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::NJ], void *C, const float *addend,
-                                          int64_t ldc, int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid,
-                                          int accumulate) {
+__device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::NJ], const StoreArgs &e, int64_t m0,
+                                          int64_t n0, int64_t mvalid, int64_t nvalid) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = L::wm(w), wn = L::wn(w);
-  OT *c = (OT *)C;
-  if (accumulate) {
-    if (addend) store_edge<L, OT, true, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
-    else store_edge<L, OT, true, false>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+  OT *c = (OT *)e.C;
+  if (e.accumulate) {
+    if (e.addend) store_edge<L, OT, true, true>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
+    else store_edge<L, OT, true, false>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
   } else {
-    if (addend) store_edge<L, OT, false, true>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
-    else store_edge<L, OT, false, false>(acc, c, addend, ldc, m0, n0, mvalid, nvalid, wm, wn, lane);
+    if (e.addend) store_edge<L, OT, false, true>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
+    else store_edge<L, OT, false, false>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
   }
 }
 
@@ -483,7 +487,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (mvalid <= 0 || nvalid <= 0) return;
   f32x16 acc[4][4];
   mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
-  store_any<Acc32, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
+  store_any<Acc32, typename Elem<OT>::T>(acc, e, m0, n0, mvalid, nvalid);
 }
 
 // The 16-bit gradient GEMMs' 8-wave form: 512 threads, two waves per SIMD, each 128 x 64 of the tile; the second
@@ -508,7 +512,7 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   if constexpr (KM == KM_A) mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
   else if constexpr (KM == KM_B) mainloop_ring5<DT, OpRowsN<8, 128>, OpColsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
   else mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
-  store_any<Acc16N<4>, typename Elem<OT>::T>(acc, e.C, e.addend, e.ldc, m0, n0, mvalid, nvalid, e.accumulate);
+  store_any<Acc16N<4>, typename Elem<OT>::T>(acc, e, m0, n0, mvalid, nvalid);
 }
 
 // The logits-shaped GEMMs on the 8-wave loop (16-bit operands): 512 threads, two waves per SIMD, each 128 x 64, with
@@ -530,9 +534,10 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   lds_f32x4 *red = (lds_f32x4 *)smem;
   f32x4 acc[8][4];
   mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, s.K, smem, acc);
-  pre_transform<L, A_FP8, TANH>(acc, m0, wm, lane, e.wscale, e.V, e.pre);
-  if (m0 + TM > e.V) stats_cols<L, true>(acc, m0, wm, wn, lane, e.V, e.c, red);
-  else stats_cols<L, false>(acc, m0, wm, wn, lane, e.V, e.c, red);
+  const int64_t ma = e.v0 + m0;  // first vocabulary row of the tile
+  pre_transform<L, A_FP8, TANH>(acc, ma, wm, lane, e.wscale, e.V, e.pre);
+  if (ma + TM > e.V) stats_cols<L, true>(acc, ma, wm, wn, lane, e.V, e.c, red);
+  else stats_cols<L, false>(acc, ma, wm, wn, lane, e.V, e.c, red);
   __syncthreads();
   const int t = threadIdx.x;
   if (t < nvalid) {
@@ -541,7 +546,7 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
     Stat3 r = stat_merge(sa, sb);
     f32x4 o;
     o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
-    e.part[(n0 + t) * e.mtiles + mt] = o;
+    e.part[(n0 + t) * e.mtiles + e.v0 / TM + mt] = o;
   }
 }
 
@@ -560,14 +565,15 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   typedef typename std::conditional<DT == OCTO_BF16, bf16x2, f16x2_t>::type P2;
   f32x4 acc[8][4];
   mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, s.K, smem, acc);
+  const int64_t ma = e.v0 + m0;  // first vocabulary row of the tile; its dz columns start at m0
   if constexpr (A_FP8) {
-    if (m0 + TM > e.V) dz_stage_fp8<L, P2, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-    else dz_stage_fp8<L, P2, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+    if (ma + TM > e.V) dz_stage_fp8<L, P2, TANH, true>(acc, e, ma, n0, nvalid, wm, wn, lane, smem);
+    else dz_stage_fp8<L, P2, TANH, false>(acc, e, ma, n0, nvalid, wm, wn, lane, smem);
   } else {
-    if (m0 + TM > e.V) dz_stage<L, P2, TANH, true>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
-    else dz_stage<L, P2, TANH, false>(acc, e, m0, n0, nvalid, wm, wn, lane, smem);
+    if (ma + TM > e.V) dz_stage<L, P2, TANH, true>(acc, e, ma, n0, nvalid, wm, wn, lane, smem);
+    else dz_stage<L, P2, TANH, false>(acc, e, ma, n0, nvalid, wm, wn, lane, smem);
   }
-  dz_write<L, P2, 2 * NTHREADS>(e, m0, n0, nvalid, smem);
+  dz_write<L, P2, 2 * NTHREADS>(e, ma, m0, n0, nvalid, smem);
 }
 
 // ---- host launchers ----------------------------------------------------------------------------

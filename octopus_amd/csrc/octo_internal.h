@@ -8,10 +8,13 @@ namespace octo {
 struct Operand;
 struct GemmShape;
 
-// gemm_stats epilogue arguments: part[row * mtiles + mt] = (m, S, U) of row over vocab tile mt.
+// gemm_stats epilogue arguments: part[row * mtiles + mt] = (m, S, U) of row over vocab tile mt. The GEMM's first
+// operand holds the vocabulary rows v0 .. (a chunk of W starting at row v0, a multiple of 256): its tile mt is vocab
+// tile v0 / 256 + mt.
 struct StatsArgs {
   f32x4 *part;
   int64_t mtiles;
+  int64_t v0;
   int64_t V;
   const float *wscale;  // per-vocab-row scale (fp8 weights) or NULL
   float c;              // base-2 softmax scale of the (transformed) logit
@@ -34,12 +37,14 @@ __device__ __forceinline__ void row_state(const float *lse, int pair, int64_t r,
   }
 }
 
-// gemm_dz epilogue arguments (tokens are pass-local; compact row = row_off + token).
+// gemm_dz epilogue arguments (tokens are pass-local; compact row = row_off + token). The GEMM's first operand holds
+// the vocabulary rows v0 .. v0 + its M (a chunk of W; v0 a multiple of 256); dz columns are chunk-local.
 struct DzArgs {
-  void *dzA;  // [tokens, ldA] vocabulary contiguous, staged MFMA type, or NULL
+  void *dzA;  // [tokens, ldA] chunk columns contiguous, staged MFMA type, or NULL
   int64_t ldA;
-  void *dzB;  // [V_pad, ldB] tokens contiguous, fp32 only, or NULL
+  void *dzB;  // [chunk columns, ldB] tokens contiguous, fp32 only, or NULL
   int64_t ldB;
+  int64_t v0;
   const float *lse;
   const float *g;
   const int64_t *labels;
@@ -78,8 +83,9 @@ int launch_hit(const HitArgs &a, hipStream_t st);
 
 struct StoreArgs {
   void *C;
-  const float *addend;  // optional fp32 term added before the store, same strides as C
+  const float *addend;  // optional fp32 term added before the store, [M, ld_add]
   int64_t ldc;          // elements
+  int64_t ld_add;       // elements
   int dtype;
   int accumulate;
 };

@@ -63,6 +63,11 @@ def _workspace(nbytes: int, like: Tensor) -> Tensor:
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=like.device)
 
 
+# Bytes of workspace head_bwd gives the library (None: the size octo_head_workspace_bytes returns, the plan at a
+# 2 GiB staging budget). The backward runs the largest plan of row passes and vocabulary chunks that fits it.
+BWD_WORKSPACE_BYTES: Optional[int] = None
+
+
 # ---- fused head ---------------------------------------------------------------------------------
 
 def _gather_flag(rows: Tensor, idx: Optional[Tensor]) -> int:
@@ -166,17 +171,21 @@ def head_bwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
     w_code = _dtype_code(weight2)
     flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | _lib.LSE_PAIR
     ws_flags = _lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, idx)
-    ws = _workspace(_lib.workspace_bytes(n_max, d, V, w_code, ws_flags), rows2)
+    nbytes = _lib.workspace_bytes(n_max, d, V, w_code, ws_flags)
+    if BWD_WORKSPACE_BYTES is not None:
+        nbytes = int(BWD_WORKSPACE_BYTES)
+    ws = _workspace(nbytes, rows2)
     gh = None
     if need_rows:
         # compact-order rows; scattered (runs of equal idx summed) into grad_rows below
         gh = grad_rows if idx is None else torch.empty(n_max, d, dtype=rows2.dtype, device=rows2.device)
     if need_weight:  # written in the weight's dtype (summed in fp32 inside, rounded once)
         grad_w = torch.empty(V, d, dtype=weight.dtype, device=rows2.device)
+    lse_c, g_c = lse.contiguous(), g.contiguous()  # kept alive until the call has queued its kernels
     _lib.call("octo_head_bwd", _p(rows2), rows2.shape[0], rows2.stride(0), _dtype_code(rows2),
               _p(weight2), weight2.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
-              n_max, d, V, flags, inv_T, pre, post, int(use_tanh), _p(lse.contiguous()),
-              _p(g.contiguous()), _p(gh), d, _dtype_code(rows2) if need_rows else _lib.F32,
+              n_max, d, V, flags, inv_T, pre, post, int(use_tanh), _p(lse_c),
+              _p(g_c), _p(gh), d, _dtype_code(rows2) if need_rows else _lib.F32,
               _p(grad_w if need_weight else None), _dtype_code(grad_w) if need_weight else _lib.F32,
               _p(ws), ws.numel(), _stream(rows2))
     if need_rows and idx is not None:
@@ -194,12 +203,17 @@ def _(rows, weight, w_scale, labels, idx, count, lse, g, inv_T, pre, post, use_t
 
 def _head_setup(ctx, inputs, output):
     rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, labels_via_idx, scatter = inputs
-    ctx.save_for_backward(rows, weight, w_scale, labels, idx, count, output[1])
+    # The weight is held by reference, not saved: the backward reads the weight the module holds, as the reference's
+    # checkpoint recompute reads self.weight (lm_head.py:116-117), and an activation-offload pack hook
+    # (saved_tensors_hooks) never copies the [V, d] matrix to the host and back.
+    ctx.weight = weight
+    ctx.save_for_backward(rows, w_scale, labels, idx, count, output[1])
     ctx.params = (inv_T, pre, post, use_tanh, labels_via_idx, scatter)
 
 
 def _head_backward(ctx, gout, _glse):
-    rows, weight, w_scale, labels, idx, count, lse = ctx.saved_tensors
+    rows, w_scale, labels, idx, count, lse = ctx.saved_tensors
+    weight = ctx.weight
     inv_T, pre, post, use_tanh, labels_via_idx, scatter = ctx.params
     need_rows, need_weight = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
     if need_weight and weight.dtype == torch.float8_e4m3fn:
@@ -207,9 +221,9 @@ def _head_backward(ctx, gout, _glse):
     gout = gout.float()
     if scatter:  # g of compact row r is the output gradient at its hidden row idx[r]
         col = gout[:, 0].contiguous()
+        idx64 = idx.to(torch.int64).contiguous()
         g = torch.empty(idx.numel(), dtype=torch.float32, device=gout.device)
-        _lib.call("octo_gather_f32", _p(col), 1, _p(idx.to(torch.int64).contiguous()), _p(count), idx.numel(),
-                  _p(g), _stream(gout))
+        _lib.call("octo_gather_f32", _p(col), 1, _p(idx64), _p(count), idx.numel(), _p(g), _stream(gout))
     else:
         g = gout[:, 0].contiguous()
     grad_rows, grad_w = head_bwd(rows, weight, w_scale, labels, idx, count, lse, g, inv_T, pre, post, use_tanh,
@@ -259,11 +273,11 @@ def columns_bwd(logits: Tensor, labels: Tensor, inv_T: float, lse: Tensor, g: Te
     labels = _index(labels)
     n, V = logits.shape
     dl = torch.empty_like(logits)
+    lse, g = lse.contiguous(), g.contiguous()  # bound here: a temporary's block could be reused before the call
     for r0 in range(0, n, 65535):
         r1 = min(n, r0 + 65535)
         _lib.call("octo_columns_bwd", _p(logits[r0:r1]), logits.stride(0), _dtype_code(logits), _p(labels[r0:r1]),
-                  r1 - r0, V, inv_T, _p(lse[r0:r1].contiguous()), _p(g[r0:r1].contiguous()), _p(dl[r0:r1]),
-                  dl.stride(0), _stream(logits))
+                  r1 - r0, V, inv_T, _p(lse[r0:r1]), _p(g[r0:r1]), _p(dl[r0:r1]), dl.stride(0), _stream(logits))
     return dl
 
 

@@ -27,39 +27,88 @@ def test_library_exports_every_declared_symbol():
     assert lib.octo_version().startswith(b"octo_head")
 
 
-def test_workspace_query():
+GIB = 1 << 30
+BUDGET = 2 * GIB  # the backward's default staging budget
+
+
+def _rows(n):
+    """Rows per pass the backward takes for n rows: at most 32,768, balanced over the passes, a multiple of 256."""
+    passes = -(-n // 32768)
+    return -(-(-(-n // passes)) // 256) * 256
+
+
+def test_forward_workspace_query():
     V, d = 151936, 2560
     fwd = _lib.workspace_bytes(32768, d, V, _lib.BF16, 0)
-    assert fwd >= 32768 * ((V + 255) // 256) * 16
-    Vp = (V + 255) // 256 * 256
-    # 16-bit, V a multiple of 64 and d of 256: h^T [d, P] and dz token-major [P, V_pad] (grad_W reads it K-major,
-    # grad_h reads W K-major as stored)
-    bwd = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_BACKWARD)
-    no_gw = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_BACKWARD | _lib.WS_NO_GRADW)
-    assert bwd >= (32768 * Vp + d * 32768) * 2 and bwd < (32768 * Vp + d * 32768) * 2 + (1 << 20)
-    # without grad_W: dz only
-    assert no_gw >= 32768 * Vp * 2 and no_gw < 32768 * Vp * 2 + (1 << 20)
-    # other shapes stage W^T [d, V_pad] for grad_h as well
-    for V2, d2 in ((151937, 2560), (151936, 2304 + 64)):
-        Vp2 = (V2 + 255) // 256 * 256
-        bwd2 = _lib.workspace_bytes(32768, d2, V2, _lib.BF16, _lib.WS_BACKWARD)
-        full = (d2 * Vp2 + 32768 * Vp2 + d2 * 32768) * 2
-        assert full <= bwd2 < full + (1 << 20)
+    assert 32768 * ((V + 255) // 256) * 16 <= fwd < 32768 * ((V + 255) // 256) * 16 + (1 << 20)
+    # fp8 weights are widened to bf16 one vocabulary chunk of at most 256 MiB at a time
+    f8 = _lib.workspace_bytes(32768, d, V, _lib.FP8E4M3, 0)
+    assert fwd < f8 <= fwd + (256 << 20) + (1 << 20)
     # OCTO_WS_GATHER adds a contiguous copy of the n_max rows read through idx (hidden of 2 GiB or more)
     for flags in (0, _lib.WS_BACKWARD):
         plain = _lib.workspace_bytes(32768, d, V, _lib.BF16, flags)
         assert _lib.workspace_bytes(32768, d, V, _lib.BF16, flags | _lib.WS_GATHER) >= plain + 32768 * d * 2
     assert _lib.workspace_bytes(1000, 4096, V, _lib.FP8E4M3, _lib.WS_GATHER) >= \
         _lib.workspace_bytes(1000, 4096, V, _lib.FP8E4M3, 0) + 1000 * 4096 * 2  # bf16 rows under fp8 weights
-    # one pass takes 65,536 rows; two passes of a 16-bit grad_W keep fp32 partial sums
-    one = _lib.workspace_bytes(65536, d, V, _lib.BF16, _lib.WS_BACKWARD)
-    two = _lib.workspace_bytes(65536 + 256, d, V, _lib.BF16, _lib.WS_BACKWARD)
-    assert two >= one + V * d * 4
-    # fp32: W^T [d, V_pad], h^T [d, P] and dz in both layouts
-    f32 = _lib.workspace_bytes(32768, d, V, _lib.F32, _lib.WS_BACKWARD)
-    assert f32 >= (d * Vp + 2 * 32768 * Vp + d * 32768) * 4
     with pytest.raises(ValueError):
         _lib.workspace_bytes(-1, d, V, _lib.BF16, 0)
+
+
+@pytest.mark.parametrize("n,d,V,w,flags", [
+    (24576, 2560, 151936, _lib.BF16, 0),                    # 24,576 scored of 32,768 packed tokens, grad_h + grad_W
+    (29491, 4096, 128256, _lib.BF16, 0),                    # d 4096, V 128,256
+    (32768, 2560, 151936, _lib.BF16, 0),                    # every one of 32,768 rows scored
+    (114688, 2560, 151936, _lib.FP8E4M3, _lib.WS_NO_GRADW),  # fp8 weights, grad_h only, four passes
+    (24576, 2560, 151937, _lib.BF16, 0),                    # V not a multiple of 64: W^T staged per chunk
+    (24576, 2560, 151936, _lib.F32, 0),                     # fp32: dz in both layouts
+])
+def test_backward_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
+    """The backward's workspace at the default plan is the 2 GiB staging budget (dz of one row pass and vocabulary
+    chunk, fp32 grad_h partials across chunks, the chunk's W^T or widened fp8 rows) plus h^T of a pass, the label
+    entries, and over several passes with a 16-bit grad_W its fp32 partials [V, d]; no [rows, V] dz exists."""
+    ws = _lib.workspace_bytes(n, d, V, w, _lib.WS_BACKWARD | flags)
+    P, passes, Vc, chunks = _lib.bwd_plan(n, d, V, w, flags, ws)
+    Vp = (V + 255) // 256 * 256
+    esz = 4 if w == _lib.F32 else 2
+    assert P == _rows(n) and passes == -(-n // P)
+    assert Vc % 256 == 0 and chunks == -(-Vp // Vc) and (chunks - 1) * Vc < Vp
+    need_gw = not flags & _lib.WS_NO_GRADW
+    extra = (d * P * esz if need_gw else 0) + P * 4 + (V * d * 4 if need_gw and passes > 1 and esz == 2 else 0)
+    assert ws <= BUDGET + extra + (1 << 20), (ws, extra)
+    whole_dz = n * Vp * esz
+    assert ws < whole_dz  # the [rows, V] staging of a whole pass would not fit
+    # as few chunks as the budget allows: with one chunk fewer the staging would not fit
+    per_col = P * esz * (1 + (esz == 4 and need_gw)) + (d * esz if (V % 64 or d % 256 or esz == 4) else 0) + \
+        (d * 2 if w == _lib.FP8E4M3 else 0)
+    assert per_col * Vc + P * d * 4 <= BUDGET
+    if chunks > 1:
+        wider = -(-(-(-Vp // (chunks - 1))) // 256) * 256
+        assert per_col * wider + (P * d * 4 if chunks > 2 else 0) > BUDGET or per_col * Vp > BUDGET
+
+
+def test_backward_plan_follows_the_workspace():
+    """A larger workspace runs fewer chunks, a smaller one more (down to 256-column chunks and 256-row passes);
+    below the smallest plan the query refuses with EWORKSPACE."""
+    n, d, V = 3000, 256, 5120
+    for flags in (0, _lib.WS_NO_GRADW):
+        big = _lib.workspace_bytes(n, d, V, _lib.BF16, _lib.WS_BACKWARD | flags)
+        assert _lib.bwd_plan(n, d, V, _lib.BF16, flags, big) == (3072, 1, 5120, 1)  # small enough for one chunk
+        seen, last = set(), (1, 0)
+        for ws in (big, big // 2, big // 4, big // 6, big // 8, 3 << 20, 2 << 20):
+            try:
+                P, passes, Vc, chunks = _lib.bwd_plan(n, d, V, _lib.BF16, flags, ws)
+            except ValueError:  # with grad_W, several passes add fp32 partials [V, d]: nothing fits below one pass
+                assert flags == 0 and ws < big // 4
+                continue
+            assert P * passes >= n > P * (passes - 1) and Vc * chunks >= 5120 > Vc * (chunks - 1)
+            assert (passes, chunks) >= last or passes > last[0]  # a smaller workspace never runs fewer pieces
+            last = (passes, chunks)
+            seen.add((passes > 1, chunks > 1))
+        assert (False, True) in seen
+        if flags:
+            assert (True, True) in seen
+    with pytest.raises(ValueError):
+        _lib.bwd_plan(n, d, V, _lib.BF16, 0, 1 << 16)
 
 
 P = ctypes.c_void_p(256)  # never dereferenced: every call below fails its host-side checks first
