@@ -120,6 +120,20 @@ int octo_head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                   float *logp, float *ent, float *lse, float *out2, int64_t ld_out2,
                   void *ws, size_t ws_bytes, void *stream);
 
+/* octo_head_fwd without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). No counterpart in the reference. Its workspace is
+ * a 64 MiB device array inside the library, one copy per GPU, held until the process ends; the call allocates
+ * nothing (no hipMalloc, no timing events). Limit: the forward's workspace for n_max, d, V (octo_head_workspace_bytes
+ * with the same flags) must be at most 64 MiB, about 7,000 rows at V = 151,936, else OCTO_EINVAL before anything is
+ * queued. Every call on one GPU uses the same array: calls that overlap on one GPU (other streams or threads) race;
+ * calls on one stream are ordered. Nothing in the array needs clearing between calls. */
+int octo_head_fwd_noalloc(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
+                          const void *w, int64_t ldw, int w_dtype, const float *w_scale,
+                          const int64_t *labels, const int64_t *idx, const int32_t *count,
+                          int64_t n_max, int d, int V, int flags,
+                          float inv_T, float pre, float post, int use_tanh,
+                          float *logp, float *ent, float *lse, float *out2, int64_t ld_out2, void *stream);
+
 /* Backward of octo_head_fwd's logprob column (the entropy column carries no gradient):
  *   g[r]   : dL/dlogprob of compact row r (fp32, compact order)
  *   lse[r] : from octo_head_fwd on the same inputs (the pair form under OCTO_LSE_PAIR, given to both calls)

@@ -48,6 +48,8 @@ SIGNATURES = {
                       _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, _p, _sz, _p],
     "octo_head_fwd_grpo": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                            _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, ctypes.POINTER(GrpoTail), _p, _sz, _p],
+    "octo_head_fwd_noalloc": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                              _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, _p],
     "octo_head_bwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                       _f32, _f32, _f32, _i32, _p, _p, _p, _i64, _i32, _p, _i32, _p, _sz, _p],
     "octo_columns_fwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p],

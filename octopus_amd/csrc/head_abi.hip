@@ -46,8 +46,8 @@ struct TimedLaunch {
   hipEvent_t a = nullptr, b = nullptr;
   const char *name;
   hipStream_t st;
-  TimedLaunch(const char *n, hipStream_t s) : name(n), st(s) {
-    if (!g_timing) return;
+  TimedLaunch(const char *n, hipStream_t s, bool allowed = true) : name(n), st(s) {
+    if (!g_timing || !allowed) return;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess || hipEventRecord(a, st) != hipSuccess) {
       if (a) (void)hipEventDestroy(a);
       if (b) (void)hipEventDestroy(b);
@@ -376,7 +376,7 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
              const float *w_scale, const int64_t *labels, const int64_t *idx, const int32_t *count, int64_t n_max,
              int d, int V, int flags, float inv_T, float pre, float post, int use_tanh, float *logp, float *ent,
              float *lse, float *out2, int64_t ld_out2, const octo_grpo_tail *gt, void *ws, size_t ws_bytes,
-             void *stream) {
+             void *stream, bool timed = true) {
   Common cm;
   int rc = check_common(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, n_max, d, V, flags, inv_T,
                         pre, post, use_tanh, cm);
@@ -418,7 +418,7 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
     if (rc) return rc;
     const GemmShape s = shape(vc, n_max, d, kGroupM, 2, count, 0);
     {
-      TimedLaunch t("gemm_stats", st);
+      TimedLaunch t("gemm_stats", st, timed);
       rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, A, B, s, e, st);
     }
     if (rc) return rc;
@@ -465,9 +465,68 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
   return launch_merge(m, st);
 }
 
+// ---- the allocation-free forward (octo_head_fwd_noalloc) ----------------------------------------
+// Its workspace is this file-scope device array: one copy on each GPU the library runs on, held until the process
+// ends. In host code the array's name stands for a host-side shadow, not a device address, so it is never passed to
+// a kernel: each device's address comes from hipGetSymbolAddress, taken once per device with that device current,
+// and kept in g_scratch_ptr.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __attribute__((aligned(256))) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on the device that runs `stream` (the current device for the null stream).
+int scratch_on(hipStream_t stream, void **ptr) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return octo_fail(OCTO_EHIP, "head_fwd_noalloc: stream device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return octo_fail(OCTO_EUNSUPPORTED, "head_fwd_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void *p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t back = (cur >= 0 && cur != dev) ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess || p == nullptr)
+      return octo_fail(OCTO_EHIP, "head_fwd_noalloc: scratch address on device %d: %s", dev,
+                       e != hipSuccess ? hipGetErrorString(e) : "null");
+    if (back != hipSuccess)
+      return octo_fail(OCTO_EHIP, "head_fwd_noalloc: restoring device %d: %s", cur, hipGetErrorString(back));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return OCTO_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int octo_head_fwd_noalloc(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw,
+                          int w_dtype, const float *w_scale, const int64_t *labels, const int64_t *idx,
+                          const int32_t *count, int64_t n_max, int d, int V, int flags, float inv_T, float pre,
+                          float post, int use_tanh, float *logp, float *ent, float *lse, float *out2,
+                          int64_t ld_out2, void *stream) {
+  Common cm;
+  int rc = check_common(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, n_max, d, V, flags, inv_T,
+                        pre, post, use_tanh, cm);
+  if (rc) return rc;
+  const size_t need = fwd_layout(n_max, d, V, w_dtype, cm.gather).total;
+  if (need > kScratchBytes)
+    return octo_fail(OCTO_EINVAL, "head_fwd_noalloc: n_max=%lld d=%d V=%d needs %zu bytes of scratch, above its %zu",
+                     (long long)n_max, d, V, need, kScratchBytes);
+  if (n_max == 0) return OCTO_OK;
+  void *ptr = nullptr;
+  rc = scratch_on((hipStream_t)stream, &ptr);
+  if (rc) return rc;
+  return head_fwd(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
+                  pre, post, use_tanh, logp, ent, lse, out2, ld_out2, nullptr, ptr, kScratchBytes, stream,
+                  /*timed=*/false);
+}
 
 const char *octo_version(void) { return "octo_head 0.1 (gfx950)"; }
 const char *octo_last_error(void) { return g_err; }
