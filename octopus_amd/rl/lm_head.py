@@ -16,9 +16,12 @@ does under the reference. A HIP path never falls back to torch: an unsupported d
 
 from __future__ import annotations
 
+import contextlib
+import functools
 import types
 
 import torch
+from torch.overrides import TorchFunctionMode
 from torch.utils import _pytree as pytree
 from torch.utils.checkpoint import checkpoint
 
@@ -27,93 +30,143 @@ from octopus_amd.rl.seq_tiles import _fused
 
 CHUNK = 2048  # rows per checkpointed chunk of the CPU composite path (lm_head.py:20)
 
-_LOGITS = object()  # placeholder for the logits inside a recorded post-head op
+_LOGITS = object()  # stands for the head's logits in a recorded post-head op (func, args, kwargs)
+
+# Tensor methods that write into their first operand (besides the name_ methods and out= calls)
+_WRITES = {"__setitem__", "__iadd__", "__isub__", "__imul__", "__itruediv__", "__ifloordiv__", "__imod__",
+           "__ipow__", "__imatmul__", "__iand__", "__ior__", "__ixor__", "__ilshift__", "__irshift__"}
+
+
+def _replace(tree, match, value):
+    """tree with each leaf for which match(leaf) holds replaced by value."""
+    return pytree.tree_map(lambda leaf: value if match(leaf) else leaf, tree)
+
+
+class _ChainProbe(TorchFunctionMode):
+    """While active, follows one tensor's lineage through a forward: after start(t), every torch function that reads
+    the newest tensor of the lineage is recorded as (func, args, kwargs) with that tensor replaced by _LOGITS, and its
+    result becomes the newest. A write into the lineage, or a read of any tensor of it but the newest (the flow
+    forks), cannot be replayed by one chain of ops: NotImplementedError."""
+
+    def __init__(self):
+        super().__init__()
+        self.lineage: list = []
+        self.ops: list = []
+
+    def start(self, t: torch.Tensor) -> None:
+        self.lineage = [t]
+
+    def __torch_function__(self, func, types_, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        value = func(*args, **kwargs)
+        if not self.lineage:
+            return value
+        read = [x for x in pytree.tree_leaves((args, kwargs)) if any(x is t for t in self.lineage)]
+        if not read:
+            return value
+        name = getattr(func, "__name__", repr(func))
+        newest = self.lineage[-1]
+        if any(x is not newest for x in read):
+            raise NotImplementedError(f"post-head logits: {name} reads an earlier result of the head's output; "
+                                      "one chain of ops cannot reproduce that")
+        if value is None or name in _WRITES or "out" in kwargs or (name.endswith("_") and not name.endswith("__")):
+            raise NotImplementedError(f"post-head logits: {name} writes them in place; it cannot be replayed")
+        if isinstance(value, torch.Tensor):  # (metadata queries such as .shape return other types)
+            self.ops.append(_replace((func, args, kwargs), lambda leaf: leaf is newest, _LOGITS))
+            if value is not newest:
+                self.lineage.append(value)
+        return value
+
+
+@contextlib.contextmanager
+def _forwards(replacements: dict):
+    """Each module's forward replaced by the given callable for the duration (instance attributes, restored after)."""
+    before = {m: m.__dict__.get("forward") for m in replacements}
+    try:
+        for m, f in replacements.items():
+            m.forward = f
+        yield
+    finally:
+        for m, f in before.items():
+            if f is None:
+                m.__dict__.pop("forward", None)
+            else:
+                m.forward = f
+
+
+class _Countdown:
+    """The bound head's output and how many post-head ops of the model are still to pass over it."""
+    __slots__ = ("out", "left")
+
+    def __init__(self, out: torch.Tensor, left: int):
+        self.out, self.left = out, left
 
 
 class _Tail(torch.Tensor):
-    """The logits as the model's forward sees them after its lm_head.
-
-    Probing (`chain` set): every op applied to the newest tail is recorded and yields the next tail; an
-    in-place op or an op on an older result cannot be replayed and raises NotImplementedError.
-    Bound-head output (`skip` > 0): each op the model applies returns the head's output unchanged, `skip`
-    times (the ops already ran inside the head, on each chunk's logits)."""
-    chain = None
-    skip = 0
-    out = None
+    """The bound head's output as the model's own forward sees it after its lm_head. The model's post-head ops ran
+    inside the head already (on each chunk's logits), so each op the model applies to it returns the head's output
+    again, until the ops recorded at bind time have passed; queries that return no tensor (shape, dtype, ...) are
+    answered from the output itself."""
+    _octo_countdown: _Countdown = None
 
     @classmethod
     def __torch_function__(cls, func, types_, args=(), kwargs=None):
         kwargs = kwargs or {}
-        tail = next(a for a in pytree.tree_leaves((args, kwargs)) if isinstance(a, _Tail))
+        countdown = next(x._octo_countdown for x in pytree.tree_leaves((args, kwargs)) if isinstance(x, _Tail))
         with torch._C.DisableTorchFunctionSubclass():
-            result = func(*args, **kwargs)
-        chain = tail.chain
-        if chain is not None and (result is None or tail is not chain["last"]):
-            what = "in place" if result is None else "on an earlier result"
-            raise NotImplementedError(f"post-head logits: {getattr(func, '__name__', func)} {what} "
-                                      "cannot be replayed")
-        if not isinstance(result, torch.Tensor):  # metadata queries (shape, dtype, ...)
-            return result
-        if chain is None:
-            return _skipping(tail.out, tail.skip - 1)
-        chain["ops"].append(pytree.tree_map(lambda a: _LOGITS if isinstance(a, _Tail) else a, (func, args, kwargs)))
-        nxt = result.as_subclass(_Tail)
-        nxt.chain = chain
-        chain["last"] = nxt
-        return nxt
+            value = func(*args, **kwargs)
+        if not isinstance(value, torch.Tensor):
+            return value
+        countdown.left -= 1
+        return countdown.out if countdown.left <= 0 else _as_tail(countdown)
+
+
+def _as_tail(countdown: _Countdown) -> _Tail:
+    t = countdown.out.as_subclass(_Tail)
+    t._octo_countdown = countdown
+    return t
 
 
 def _skipping(out: torch.Tensor, n: int) -> torch.Tensor:
-    """out itself when n == 0, else a tail that swallows the next n post-head ops."""
-    if n == 0:
-        return out
-    tail = out.as_subclass(_Tail)
-    tail.out, tail.skip = out, n
-    return tail
+    """out, seen through the model's next n post-head ops (out itself when n == 0)."""
+    return out if n <= 0 else _as_tail(_Countdown(out, n))
 
 
 def _post_head(ops: list, logits: torch.Tensor) -> torch.Tensor:
-    """Replay recorded post-head ops on logits."""
-    for func, args, kwargs in ops:
-        args, kwargs = pytree.tree_map(lambda a: logits if a is _LOGITS else a, (args, kwargs))
-        logits = func(*args, **kwargs)
-    return logits
+    """The recorded post-head ops applied in order to logits, each to the previous op's result."""
+    def apply(x, op):
+        func, args, kwargs = _replace(op, lambda leaf: leaf is _LOGITS, x)
+        return func(*args, **kwargs)
+    return functools.reduce(apply, ops, logits)
 
 
 def _post_head_ops(model, head) -> list:
     """The ops the model's own forward applies to its lm_head output (Granite's / logits_scaling, Falcon-H1's
-    * lm_head_multiplier, Gemma2's tanh soft-cap, ...), found by running that forward once with its other
-    children stubbed (zero hidden states) and the head returning a recording tensor. Raises
-    NotImplementedError unless the returned logits are the end of one chain of ops on the head output."""
-    lm = next(m for m in model.modules() if any(c is head for c in m.children()))
-    chain: dict = {"ops": [], "last": None}
+    * lm_head_multiplier, Gemma2's tanh soft-cap, ...). The module that owns the head runs its forward once with every
+    other child answering zero hidden states and the head answering zero logits, under a _ChainProbe that follows
+    those logits to the forward's result. NotImplementedError unless that result is the end of one chain of ops on
+    them (a further submodule, an in-place write or a fork is not)."""
+    owner = next((m for m in model.modules() if any(c is head for c in m.children())), None)
+    if owner is None:
+        raise NotImplementedError("the head is not a submodule of the model")
     V, H = head.weight.shape
-
-    def recording_head(*_, **__):
-        tail = torch.zeros(1, 1, V, dtype=head.weight.dtype).as_subclass(_Tail)
-        tail.chain = chain
-        chain["last"] = tail
-        return tail
-
+    dtype = head.weight.dtype
     from transformers.modeling_outputs import MoeModelOutputWithPast
-    hidden = MoeModelOutputWithPast(last_hidden_state=torch.zeros(1, 1, H, dtype=head.weight.dtype))
-    stubs = {c: (lambda *_, **__: hidden) for c in lm.children() if c is not head}
-    stubs[head] = recording_head
-    saved = {c: vars(c).get("forward") for c in stubs}
-    try:
-        for c, f in stubs.items():
-            c.forward = f
-        out = type(lm).forward(lm, input_ids=torch.zeros(1, 1, dtype=torch.long), use_cache=False)
-    finally:
-        for c, f in saved.items():
-            if f is None:
-                del c.forward
-            else:
-                c.forward = f
-    if chain["last"] is None or out.logits is not chain["last"]:
-        raise NotImplementedError(f"{type(lm).__name__}: its logits are not one chain of ops on its lm_head "
-                                  "output; the chunked head cannot reproduce them")
-    return chain["ops"]
+    zero_states = MoeModelOutputWithPast(last_hidden_state=torch.zeros(1, 1, H, dtype=dtype))
+    probe = _ChainProbe()
+
+    def zero_logits(*_, **__):
+        z = torch.zeros(1, 1, V, dtype=dtype)
+        probe.start(z)
+        return z
+
+    stand_ins = {c: (zero_logits if c is head else (lambda *_, **__: zero_states)) for c in owner.children()}
+    with _forwards(stand_ins), probe:
+        result = type(owner).forward(owner, input_ids=torch.zeros(1, 1, dtype=torch.long), use_cache=False)
+    if not probe.lineage or getattr(result, "logits", None) is not probe.lineage[-1]:
+        raise NotImplementedError(f"{type(owner).__name__}: its logits are not its lm_head output after one chain of "
+                                  "ops; the chunked head cannot reproduce them")
+    return probe.ops
 
 
 _DIV = {torch.Tensor.__truediv__, torch.Tensor.div, torch.div, torch.true_divide, torch.Tensor.true_divide}

@@ -42,15 +42,28 @@ def _checkpoint(fn, *args):
     return checkpoint(fn, *args, use_reentrant=False) if _INNER else fn(*args)
 
 
+_REFERENCE_TILES = "octopus.rl.seq_tiles"  # the trainer's own module, whose flag its patched decoder layers read
+
+
 @contextlib.contextmanager
 def no_inner():
-    """Tiles run without their own checkpoints (a caller's checkpoint recomputes them instead)."""
+    """Tiles run without their own checkpoints (a caller's checkpoint recomputes them instead). The decoder layers the
+    trainer patches read the flag of the trainer's own seq_tiles module (octopus/rl/seq_tiles.py:35, 92), so when that
+    module is loaded its flag is switched as well (and restored after): chunk_major's reverse-chunk recompute
+    (chunk_major.py:356) then plans the same activations whichever of the two modules it imports no_inner from."""
+    import sys
     global _INNER
+    ref = sys.modules.get(_REFERENCE_TILES)
+    ref_before = getattr(ref, "_INNER", None)
     _INNER = False
+    if ref is not None:
+        ref._INNER = False
     try:
         yield
     finally:
         _INNER = True
+        if ref is not None:
+            ref._INNER = ref_before
 
 
 def tiled(fn, *xs):

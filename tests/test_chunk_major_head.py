@@ -8,8 +8,9 @@ between forward and backward (FSDP's unsharded tensor) is the one used and the o
 (lm_head.py:116-117).
 
 Checked: the chunked forward equals tree_head_output over the whole tree, and the reverse-chunk backward gives the
-same hidden and weight gradients as one backward through it; the HIP path on the GPU, the composite path on the
-CPU."""
+same hidden and weight gradients as one backward through it; and both against the fp64 oracle on the same inputs
+(the pair rows' columns expanded by oracle.head.tree_output; the gradients of the loss whose dL/dlogprob per pair is
+the folded flat gradient), at the path's bars. The HIP path on the GPU, the composite path on the CPU."""
 
 import functools
 
@@ -19,6 +20,7 @@ import torch
 
 from octopus_amd.rl.lm_head import _chunked_rows, bind_head
 from octopus_amd.rl.prefix_tree import TreeMeta, build_tree, tree_head_output
+from oracle import head as ohead
 
 SMALL = dict(vocab_size=300, hidden_size=64, intermediate_size=64, num_hidden_layers=1, num_attention_heads=2,
              num_key_value_heads=1, head_dim=32)
@@ -82,6 +84,22 @@ def _run(dev, dtype, tol_out, tol_grad):
 
     assert rel(head.weight.grad, gw_all) <= tol_grad
     assert rel(h_cm.grad, gh_all) <= tol_grad
+
+    # against the fp64 oracle on the same inputs: the pair rows' columns expanded to the flat positions, and the
+    # gradients of the loss whose dL/dlogprob per pair is grad_pairs[:, 0] (the entropy column is detached), the hidden
+    # gradient folded back onto the tree rows the pairs read (chunk_major.py:339-363)
+    rows = hidden[0].index_select(0, meta.pair_pos).cpu()
+    W = old.detach().cpu()
+    labels = meta.pair_label.cpu()
+    lp, ent, _ = ohead.head_forward(rows, W, labels, 0.8)
+    want_out = ohead.tree_output(torch.stack([lp, ent], 1), meta.flat_pair.cpu())
+    tol_oracle = 1e-5 if dtype == torch.float32 else 2e-3
+    assert (out_cm[0].cpu().double() - want_out).abs().max().item() <= tol_oracle
+    gh_pairs, gw_want = ohead.head_backward(rows, W, labels, 0.8, grad_pairs[:P, 0].cpu())
+    gh_want = torch.zeros(hidden.shape[1], hidden.shape[2], dtype=torch.float64).index_add_(
+        0, meta.pair_pos.cpu(), gh_pairs)
+    bar = 1e-4 if dtype == torch.float32 else 1e-2
+    assert rel(h_cm.grad[0].cpu(), gh_want) <= bar and rel(head.weight.grad.cpu(), gw_want) <= bar
 
 
 def test_chunk_major_head_cpu():

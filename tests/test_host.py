@@ -1,6 +1,7 @@
-"""Host-side logic of the product on the CPU: the prefix-tree pairs against the oracle's trie, the reference's
-own CPU head tests (tests/test_lm_head.py of the reference) through octopus_amd.rl.lm_head, the post-head
-chain parsing the fused epilogue relies on, and the seq-tile entry points."""
+"""Host-side logic of the product on the CPU: the prefix-tree pairs against the oracle's trie, the properties the
+reference's CPU head tests check (tests/test_lm_head.py:11-75, tests/test_prefix_tree.py:165-176 of the reference)
+restated through octopus_amd.rl.lm_head, the post-head chain parsing the fused epilogue relies on, and the seq-tile
+entry points."""
 
 import numpy as np
 import pytest
@@ -62,18 +63,41 @@ def test_build_tree_reference_cases():
         build_tree(flat, cu, mounts={1: [(1, 0, 0, 2)]})
 
 
-def test_tree_head_output_expands_pairs_to_flat_positions():
-    """Reference tests/test_prefix_tree.py:165-176 through the product's tree_head_output."""
-    flat, cu = _flat([np.array([1, 2, 3, 4]), np.array([1, 2, 9])])
-    meta = TreeMeta(build_tree(flat, cu), "cpu")
-    hidden = torch.arange(5, dtype=torch.float32)[None, :, None]
+def _next_token_expectation(flat, cu, scored, f2t, fn):
+    """[T_flat, C] by definition: position p that asks (scored, and not its sequence's last) gets fn(tree position
+    of p, flat[p + 1]); every other position a zero row."""
+    rows = []
+    ends = set(int(e) - 1 for e in cu[1:])
+    for p in range(len(flat)):
+        asks = p not in ends and (scored is None or bool(scored[p]))
+        rows.append(fn(int(f2t[p]), int(flat[p + 1])) if asks else [0.0, 0.0])
+    return torch.tensor(rows, dtype=torch.float64)
 
-    def head(rows, labels):
-        return torch.stack([rows[:, 0] * 10 + labels, labels.float()], -1)
+
+@pytest.mark.parametrize("case", [0, 1, 2, 3])
+def test_tree_head_output_gives_each_position_its_own_next_token(case):
+    """The expansion of reference tests/test_prefix_tree.py:165-176, stated as a property: through tree_head_output,
+    every flat position that asks gets the head's value at (its own tree row, its own next flat token), shared
+    prefixes with different continuations included, and every other position exactly zero. Cases: the reference's
+    hand-built forests and a random deduplicated one (tests/golden/prefix_pairs.json)."""
+    import json
+    import os
+    fx = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "prefix_pairs.json")))[case]
+    flat, cu = np.array(fx["flat"], dtype=np.int64), np.array(fx["cu"], dtype=np.int64)
+    scored = None if fx["scored"] is None else np.array(fx["scored"], dtype=bool)
+    tree = build_tree(flat, cu, scored=scored)
+    meta = TreeMeta(tree, "cpu")
+    T_tree = len(tree.tokens)
+    hidden = (torch.arange(T_tree, dtype=torch.float64) * 0.5 + 1.0)[None, :, None]  # row value of tree row i
+
+    def head(rows, labels):  # (row value + 1000 * label, -label): both columns name the pair
+        lab = labels.to(torch.float64)
+        return torch.stack([rows[:, 0] + 1000.0 * lab, -lab], -1)
 
     out = tree_head_output(head, hidden, meta)[0]
-    assert out[1, 1] == 3 and out[5, 1] == 9 and out[1, 0] == 1 * 10 + 3 and out[5, 0] == 1 * 10 + 9
-    assert (out[[3, 6]] == 0).all()
+    want = _next_token_expectation(flat, cu, scored, tree.flat_to_tree,
+                                   lambda pos, nxt: [pos * 0.5 + 1.0 + 1000.0 * nxt, -float(nxt)])
+    assert torch.equal(out.to(torch.float64), want)
 
 
 def _families():
@@ -93,73 +117,111 @@ EXPECTED_POST = [dict(pre=1.0, post=1.0, tanh=False), dict(pre=1 / 3.0, post=1.0
 
 
 @pytest.mark.parametrize("k", range(4), ids=["llama", "granitemoehybrid", "gemma2", "falcon_h1"])
-def test_chunked_head_matches_the_models_own_logits(k):
-    """Reference tests/test_lm_head.py:11-34 (CPU, fp32, atol 1e-5), and the fused epilogue's reading of the
-    recorded post-head chain."""
+def test_bound_head_reproduces_each_familys_softmax(k):
+    """The property of reference tests/test_lm_head.py:11-34: once bound, the model returns for each position the
+    log-probability of its next token and the entropy of the softmax of its OWN logits (post-head ops included) at
+    temperature T, to 1e-5 on the CPU; here the expected columns come from torch.distributions.Categorical over the
+    unbound model's logits in fp64, at T 1.0, 0.7 and 1.6. The fused epilogue's reading of each family's recorded
+    chain is checked beside it."""
     from transformers import AutoModelForCausalLM
     config = _families()[k]
-    torch.manual_seed(0)
+    torch.manual_seed(40 + k)
     model = AutoModelForCausalLM.from_config(config, attn_implementation="eager").eval()
-    ids = torch.randint(0, config.vocab_size, (1, 12))
-    labels = torch.roll(ids, -1, -1).reshape(-1)
+    ids = torch.randint(0, config.vocab_size, (1, 15), generator=torch.Generator().manual_seed(50 + k))
+    nxt = ids[0].roll(-1)
     with torch.no_grad():
-        own = model(input_ids=ids).logits[0].float()
-    for temperature in (1.0, 0.7):
+        own = model(input_ids=ids).logits[0].double()
+    for temperature in (1.0, 0.7, 1.6):
         head = bind_head(model, temperature)
-        head.octopus_labels, head.octopus_tree = labels, None
+        head.octopus_labels, head.octopus_tree = nxt, None
         with torch.no_grad():
-            out = model(input_ids=ids).logits[0]
-        logp = torch.log_softmax(own / temperature, -1)
-        assert torch.allclose(out[:, 0], logp.gather(-1, labels[:, None])[:, 0], atol=1e-5)
-        assert torch.allclose(out[:, 1], -(logp.exp() * logp).sum(-1), atol=1e-5)
-    assert bool(head.octopus_post) == (config.model_type != "llama")
-    post = _fused_post(head.octopus_post)
-    exp = EXPECTED_POST[k]
+            cols = model(input_ids=ids).logits[0].double()
+        want = torch.distributions.Categorical(logits=own / temperature)
+        assert (cols[:, 0] - want.log_prob(nxt)).abs().max().item() <= 1e-5, temperature
+        assert (cols[:, 1] - want.entropy()).abs().max().item() <= 1e-5, temperature
+    assert (len(head.octopus_post) > 0) == (config.model_type != "llama")
+    post, exp = _fused_post(head.octopus_post), EXPECTED_POST[k]
     assert abs(post.pre - exp["pre"]) < 1e-12 and abs(post.post - exp["post"]) < 1e-12 and post.tanh == exp["tanh"]
 
 
-@pytest.mark.parametrize("tail", [
-    lambda m, logits: (logits.__setitem__((..., 0), 0.0), logits)[1],  # masked in place
-    lambda m, logits: (logits * 2, logits / 3)[1],  # an op on an earlier result
-    lambda m, logits: m.extra(logits),  # a submodule after the head
-], ids=["setitem", "fork", "submodule"])
-def test_unreproducible_post_head_logits_fail_loudly(tail):
-    """Reference tests/test_lm_head.py:37-55."""
+def _llama_with_tail(after_head):
+    """A Llama whose forward returns after_head(model, lm_head output) as its logits, with one extra Linear child."""
     from transformers import LlamaConfig
     from transformers.modeling_outputs import CausalLMOutput
     from transformers.models.llama.modeling_llama import LlamaForCausalLM
 
-    class Model(LlamaForCausalLM):
+    class TailedLlama(LlamaForCausalLM):
         def __init__(self, config):
             super().__init__(config)
             self.extra = torch.nn.Linear(config.vocab_size, config.vocab_size)
 
         def forward(self, input_ids=None, **kwargs):
-            return CausalLMOutput(logits=tail(self, self.lm_head(self.model(input_ids=input_ids).last_hidden_state)))
+            states = self.model(input_ids=input_ids).last_hidden_state
+            return CausalLMOutput(logits=after_head(self, self.lm_head(states)))
 
+    torch.manual_seed(7)
+    return TailedLlama(LlamaConfig(**SMALL))
+
+
+def _set_first(x):
+    x[..., 0] = -1.0
+    return x
+
+
+@pytest.mark.parametrize("after_head", [
+    lambda m, x: x.clamp_(min=-4.0),                 # a write into the head's output
+    lambda m, x: _set_first(x),                      # an indexed write
+    lambda m, x: torch.maximum(x * 2.0, x),          # the flow forks: the earlier result is read again
+    lambda m, x: m.extra(x),                         # a further submodule
+], ids=["inplace", "setitem", "fork", "submodule"])
+def test_post_head_flows_one_chain_cannot_replay_are_refused(after_head):
+    """The refusals of reference tests/test_lm_head.py:37-55: bind_head raises NotImplementedError for logits that no
+    chain of ops on the head's output reproduces."""
     with pytest.raises(NotImplementedError):
-        bind_head(Model(LlamaConfig(**SMALL)), 1.0)
+        bind_head(_llama_with_tail(after_head), 1.0)
 
 
-def test_flat_head_runs_only_the_scored_positions():
-    """Reference tests/test_lm_head.py:58-75 (fp64, exact)."""
+def test_a_replayable_post_head_chain_is_bound_and_fused():
+    """A chain of the kinds the fused epilogue takes (a divide, tanh, a multiply) is recorded, read as
+    4 tanh(z / 4), and the bound head reproduces the tailed model's own softmax."""
+    model = _llama_with_tail(lambda m, x: torch.tanh(x / 4.0) * 4.0).eval()
+    ids = torch.randint(0, SMALL["vocab_size"], (1, 9), generator=torch.Generator().manual_seed(8))
+    with torch.no_grad():
+        own = model(input_ids=ids).logits[0].double()
+    head = bind_head(model, 0.9)
+    assert _fused_post(head.octopus_post) == (0.25, 4.0, True)
+    head.octopus_labels, head.octopus_tree = ids[0].roll(-1), None
+    with torch.no_grad():
+        cols = model(input_ids=ids).logits[0].double()
+    want = torch.distributions.Categorical(logits=own / 0.9)
+    assert (cols[:, 0] - want.log_prob(ids[0].roll(-1))).abs().max().item() <= 1e-5
+    assert (cols[:, 1] - want.entropy()).abs().max().item() <= 1e-5
+
+
+def test_scored_positions_alone_give_the_same_values_and_gradients():
+    """The property of reference tests/test_lm_head.py:58-75 in fp64: with octopus_scored set, the scored positions'
+    columns equal those of the unscored head exactly, the others are exactly 0, and the gradient of any loss over the
+    scored positions is exactly the same for every parameter (torch.autograd.grad of both runs)."""
     from transformers import AutoModelForCausalLM, LlamaConfig
-    torch.manual_seed(0)
+    torch.manual_seed(11)
     model = AutoModelForCausalLM.from_config(LlamaConfig(**SMALL), attn_implementation="eager").double()
-    ids = torch.randint(0, SMALL["vocab_size"], (1, 12))
-    head = bind_head(model, 0.7)
-    head.octopus_labels, head.octopus_tree = torch.roll(ids, -1, -1).reshape(-1), None
-    scored = torch.rand(12) < 0.4
-    w = torch.randn(1, 12, 2, dtype=torch.float64) * scored[None, :, None]
-    outs, grads = [], []
-    for head.octopus_scored in (None, scored):
-        model.zero_grad(set_to_none=True)
-        out = model(input_ids=ids).logits
-        (out * w).sum().backward()
-        outs.append(out.detach()[0])
-        grads.append([p.grad for p in model.parameters()])
-    assert torch.equal(outs[1][scored], outs[0][scored]) and (outs[1][~scored] == 0).all()
-    assert all(torch.equal(a, b) for a, b in zip(*grads))
+    ids = torch.randint(0, SMALL["vocab_size"], (1, 14), generator=torch.Generator().manual_seed(12))
+    head = bind_head(model, 0.8)
+    head.octopus_labels, head.octopus_tree = ids[0].roll(-1), None
+    keep = torch.rand(14, generator=torch.Generator().manual_seed(13)) < 0.5
+    weight = torch.randn(14, 2, dtype=torch.float64, generator=torch.Generator().manual_seed(14)) * keep[:, None]
+    params = list(model.parameters())
+
+    def run(scored):
+        head.octopus_scored = scored
+        cols = model(input_ids=ids).logits[0]
+        return cols.detach(), torch.autograd.grad((cols * weight).sum(), params, allow_unused=True)
+
+    cols_all, grads_all = run(None)
+    cols_sel, grads_sel = run(keep)
+    assert torch.equal(cols_sel[keep], cols_all[keep]) and bool((cols_sel[~keep] == 0).all())
+    for a, b in zip(grads_all, grads_sel):
+        assert (a is None and b is None) or torch.equal(a, b)
 
 
 def test_fused_post_rejects_chains_without_an_epilogue():
@@ -196,6 +258,18 @@ def test_tiled_and_no_inner():
         with seq_tiles.no_inner():
             assert seq_tiles._INNER is False
         assert seq_tiles._INNER is True
+        # with the trainer's own seq_tiles module loaded, its flag (the one its decoder layers read) follows too
+        import sys
+        import types
+        ref = types.ModuleType("octopus.rl.seq_tiles")
+        ref._INNER = True
+        sys.modules["octopus.rl.seq_tiles"] = ref
+        try:
+            with seq_tiles.no_inner():
+                assert ref._INNER is False and seq_tiles._INNER is False
+            assert ref._INNER is True
+        finally:
+            del sys.modules["octopus.rl.seq_tiles"]
         a, b = seq_tiles.tiled(lambda p, q: (p + 1, q), x, None if False else x)
         assert a.shape == x.shape and torch.equal(b, x)
     finally:

@@ -155,6 +155,31 @@ def test_trie_pairs_expand_to_flat_positions():
     assert fp[0] == fp[4]  # "1" -> "2" in both sequences: one pair
 
 
+@pytest.mark.parametrize("case", [0, 1, 2, 3])
+def test_tree_output_gives_each_flat_position_its_pairs_row(case):
+    """oracle.head.tree_output (prefix_tree.py:419-421: a zero row appended, then index_select by flat_pair) pinned by
+    definition on the reference's hand-built forests and a random deduplicated one (tests/golden/prefix_pairs.json,
+    the case of tests/test_prefix_tree.py:165-176 first): with each pair row made to name its pair, the position p
+    that asks receives the row of (tree position of p, flat[p + 1]), every other position zeros. A wrong index, a
+    missing zero row or a pair mixed up with its neighbour fails it."""
+    import json
+    import os
+    fx = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "prefix_pairs.json")))[case]
+    flat, cu = np.array(fx["flat"], dtype=np.int64), np.array(fx["cu"], dtype=np.int64)
+    scored = None if fx["scored"] is None else np.array(fx["scored"], dtype=bool)
+    tokens, f2t, _ = opairs.tree_positions(flat, cu)
+    pos, lab, fp = opairs.pairs(flat, cu, scored)
+    pair_rows = torch.stack([torch.as_tensor(pos, dtype=F64), torch.as_tensor(lab, dtype=F64)], 1)
+    for none_marker in (-1, len(pos)):  # -1, or the appended zero row's index P (TreeMeta's form)
+        fpx = np.where(fp < 0, none_marker, fp)
+        out = ohead.tree_output(pair_rows, fpx)
+        ends = set(int(e) - 1 for e in cu[1:])
+        for p in range(len(flat)):
+            asks = p not in ends and (scored is None or bool(scored[p]))
+            want = [float(f2t[p]), float(flat[p + 1])] if asks else [0.0, 0.0]
+            assert out[p].tolist() == want, (case, p)
+
+
 def test_trie_pairs_of_scored_positions():
     """Reference tests/test_prefix_tree.py:179-188."""
     flat, cu = _flat([np.array([1, 2, 3, 4]), np.array([1, 2, 3, 5]), np.array([1, 2, 9])])
