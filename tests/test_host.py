@@ -280,6 +280,28 @@ def test_prefix_tree_module_exports():
     assert callable(prefix_tree.build_tree) and callable(prefix_tree.tree_head_output)
 
 
+def test_the_head_op_saves_no_weight_for_backward():
+    """An activation-offload pack hook (saved_tensors_hooks, as the actor's host_activations) sees the rows, labels and
+    per-row state the head op saves, never the [V, d] weight: the backward reads the weight the op holds by reference
+    (meta tensors through the op's fake kernels; no GPU). The backward still returns a [V, d] weight gradient."""
+    from octopus_amd import head_op
+    V, d, n = 1000, 64, 32
+    rows = torch.empty(n, d, device="meta", dtype=torch.bfloat16, requires_grad=True)
+    W = torch.empty(V, d, device="meta", dtype=torch.bfloat16, requires_grad=True)
+    labels = torch.empty(n, device="meta", dtype=torch.int64)
+    packed = []
+
+    def pack(t):
+        packed.append(tuple(t.shape))
+        return t
+
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+        out = head_op.fused_head(rows, W, labels, 0.9)
+    assert packed and (V, d) not in packed, packed
+    out[:, 0].sum().backward()
+    assert W.grad.shape == (V, d) and rows.grad.shape == (n, d)
+
+
 def test_gather_flag_asks_for_the_row_copy_only_past_2_gib_through_idx():
     """The torch op requests OCTO_WS_GATHER exactly when rows are read through idx from a matrix whose rows x row
     stride x element bytes reach 2^31 - 1, the C ABI's own test (meta tensors: shapes and strides, no memory)."""
