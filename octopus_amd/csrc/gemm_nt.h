@@ -56,16 +56,18 @@ struct GemmShape {
   int64_t count_off;
 };
 
-// Block -> (mt, nt). Blocks run on XCD b % 8. The tiles are ordered in groups of group_m M-tiles across all N-tiles
-// (M fastest within a group), and that order is cut into 8 contiguous segments of equal length (+-1), one per XCD:
-// the ~32 workgroups resident on an XCD run neighbouring tiles of its segment (4 M-tiles x 8 N-tiles) and share A
-// and B K-slices in its L2, and every XCD holds the same number of tiles whatever the shape. (Dealing whole M-tile
-// rows to the XCDs instead left the XCDs with one more row a whole extra round of tiles whenever M-tiles were not a
-// multiple of 8: 99 M-tiles x 10 N-tiles ran 5 rounds of 32 tiles on three XCDs against 4 on the others.)
-// A device-side row count that bounds M or N shrinks the tile grid the segments are cut from (read once per block),
-// so the idle blocks all come after the working ones instead of between them: interleaved idle blocks retire
-// instantly and stagger the working workgroups at every group start, which breaks their L2 sharing. The grid is
-// 8 * ceil(bound-free tiles / 8); blocks past their XCD's segment return false.
+// Block -> (mt, nt). Blocks run on XCD b % 8. The first 8 * floor(M-tiles / 8) M-tiles are dealt to the XCDs
+// round-robin (XCD x owns mt = x, x + 8, ...), and each XCD walks its own in groups of group_m across all N-tiles, so
+// the ~32 workgroups resident on an XCD run 4 M-tiles x 8 N-tiles and share A and B K-slices in its L2, while the 8
+// XCDs sweep the N-tiles in step (at 114,688 hidden rows, 0.59 GB, more than the 256 MB Infinity Cache, XCDs out of
+// step made the forward 6% slower). The tiles of the last M-tiles % 8 M-tiles are cut into 8 contiguous segments of
+// equal length (+-1), one per XCD, so every XCD holds the same number of tiles whatever the shape (whole M-tile rows
+// for those too gave an XCD with one more row a whole extra round: 99 M-tiles x 10 N-tiles ran 5 rounds of 32 tiles on
+// three XCDs against 4 on the others). Per XCD that is floor(M / 8) N + ceil((M % 8) N / 8) = ceil(M N / 8) tiles.
+// A device-side row count that bounds M or N shrinks the tile grid (read once per block), so the idle blocks all come
+// after the working ones instead of between them: interleaved idle blocks retire instantly and stagger the working
+// workgroups at every group start, which breaks their L2 sharing. The grid is 8 * ceil(bound-free tiles / 8); blocks
+// past their XCD's tiles return false.
 __host__ __device__ inline int64_t tile_grid(int mtiles, int ntiles) {
   return 8 * (((int64_t)mtiles * ntiles + 7) / 8);
 }
@@ -76,17 +78,23 @@ __device__ __forceinline__ bool tile_of(const GemmShape &s, int &mt, int &nt) {
   int64_t mtiles = s.mtiles, ntiles = s.ntiles;
   if (s.count_on == 1) mtiles = min(mtiles, cdiv(dev_count(s.count, s.count_off, s.M), (int64_t)TM));
   if (s.count_on == 2) ntiles = min(ntiles, cdiv(dev_count(s.count, s.count_off, s.N), (int64_t)TN));
-  const int64_t T = mtiles * ntiles;
-  const int64_t lo = x * T / 8, hi = (x + 1) * T / 8;  // XCD x's segment of the tile order
-  const int64_t L = lo + k;
-  if (L >= hi) return false;
-  const int64_t span = (int64_t)s.group_m * ntiles;
-  const int64_t gid = L / span;
-  const int64_t first = gid * s.group_m;
-  const int64_t gsize = (mtiles - first) < s.group_m ? (mtiles - first) : s.group_m;
-  const int64_t local = L - gid * span;
-  mt = (int)(first + local % gsize);
-  nt = (int)(local / gsize);
+  const int64_t mfull = mtiles / 8;  // M-tiles every XCD owns: x, x + 8, ..., x + 8 (mfull - 1)
+  const int64_t main = mfull * ntiles;
+  if (k < main) {
+    const int64_t span = (int64_t)s.group_m * ntiles;
+    const int64_t gid = k / span;
+    const int64_t first = gid * s.group_m;
+    const int64_t gsize = (mfull - first) < s.group_m ? (mfull - first) : s.group_m;
+    const int64_t local = k - gid * span;
+    mt = (int)(x + 8 * (first + local % gsize));
+    nt = (int)(local / gsize);
+    return true;
+  }
+  const int64_t r = mtiles - 8 * mfull, T = r * ntiles;  // the last r M-tiles, M fastest, cut into 8 segments
+  const int64_t L = x * T / 8 + (k - main);
+  if (L >= (x + 1) * T / 8) return false;
+  mt = (int)(8 * mfull + L % r);
+  nt = (int)(L / r);
   return true;
 }
 

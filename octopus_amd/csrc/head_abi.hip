@@ -100,6 +100,35 @@ void vocab_chunks(int64_t V_pad, int64_t vmax, int64_t &Vc, int64_t &chunks) {
   chunks = cdiv(V_pad, Vc);
 }
 
+// Rounds of tiles (32 CUs per XCD, tiles dealt evenly to the 8 XCDs) that grad_W = dz^T . h takes over the chunks: a
+// chunk of m vocabulary tiles has m x d/256 tiles of K = all the pass's rows each, so its last round, when partial,
+// idles CUs for a whole long tile.
+int64_t gradw_rounds(int64_t V_pad, int d, int64_t Vc) {
+  const int64_t nd = cdiv(d, TN);
+  int64_t rounds = 0;
+  for (int64_t v0 = 0; v0 < V_pad; v0 += Vc) {
+    const int64_t m = ((V_pad - v0) < Vc ? (V_pad - v0) : Vc) / TM;
+    rounds += cdiv(cdiv(m * nd, 8), 32);
+  }
+  return rounds;
+}
+// With grad_W asked for: of the chunk counts from the fewest that fit up to 3 more, the one whose grad_W takes the
+// fewest rounds (the fewest chunks on a tie). At d 4096, V 128,256: 8 chunks of 63 vocabulary tiles, 32 rounds, where
+// 5 chunks of 101 take 35 (202 tiles per XCD in each: 6.3 rounds of 32).
+void gradw_rounds_chunks(int64_t V_pad, int d, int64_t &Vc, int64_t &chunks) {
+  int64_t best = gradw_rounds(V_pad, d, Vc);
+  const int64_t c0 = chunks;
+  for (int64_t c = c0 + 1; c <= c0 + 3; ++c) {
+    const int64_t vc = round_up(cdiv(V_pad, c), TM);
+    const int64_t r = gradw_rounds(V_pad, d, vc);
+    if (r < best) {
+      best = r;
+      Vc = vc;
+      chunks = cdiv(V_pad, vc);
+    }
+  }
+}
+
 struct FwdLayout {
   int64_t mtiles, Vc, chunks;
   size_t part, wide, z, rows, total;
@@ -177,6 +206,7 @@ bool bwd_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_
         if (budget > hb) {
           const int64_t vmax = (int64_t)((budget - hb) / per_col) / TM * TM;
           if (vmax >= TM) vocab_chunks(L.V_pad, vmax, Vc, chunks);
+          if (vmax >= TM && need_gw) gradw_rounds_chunks(L.V_pad, d, Vc, chunks);
         }
       }
       if (chunks > 0) {
@@ -771,7 +801,7 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
         const GemmShape s3 = shape(vc, d, rows, kGroupM, 3, count, r0);
         StoreArgs o;
         const bool acc_out = flags & OCTO_GRADW_ACCUMULATE;
-        if (L.gacc_on && !last_pass) {  // fp32 partial sums of the passes so far
+        if (L.gacc_on && !last_pass && !count) {  // fp32 partial sums of the passes so far
           o.C = gacc + v0 * d;
           o.addend = nullptr;
           o.dtype = OCTO_F32;
@@ -781,6 +811,20 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
           o.addend = (L.gacc_on && p > 0) ? gacc + v0 * d : nullptr;
           o.dtype = gw_dtype;
           o.accumulate = (acc_out || (!L.gacc_on && p > 0)) ? 1 : 0;
+        }
+        if (count && p > 0) {  // passes at or past the device row count store nothing
+          o.pass_count = count;
+          o.pass_r0 = r0;
+          o.pass_end = r0 + rows;
+        }
+        if (count && L.gacc_on && !last_pass) {
+          // the device count decides: the pass that reaches it stores grad_W (adding the earlier passes' partials),
+          // an earlier one stores its fp32 partials
+          o.pass_count = count;
+          o.pass_r0 = r0;
+          o.pass_end = r0 + rows;
+          o.part = gacc + v0 * d;
+          o.part_accumulate = p > 0 ? 1 : 0;
         }
         o.ldc = d;
         o.ld_add = d;

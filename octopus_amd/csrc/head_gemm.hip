@@ -472,6 +472,28 @@ __device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::N
   }
 }
 
+// Which store a row pass's GEMM makes (StoreArgs pass_count / part): 0 none, 1 the final C, 2 the fp32 partials.
+__device__ __forceinline__ int pass_store(const StoreArgs &e) {
+  if (!e.pass_count) return 1;
+  const int64_t c = *e.pass_count;
+  if (e.pass_r0 > 0 && c <= e.pass_r0) return 0;
+  return (e.part && c > e.pass_end) ? 2 : 1;
+}
+
+template <class L, typename OT>
+__device__ __forceinline__ void store_pass(const typename L::V (&acc)[L::NI][L::NJ], const StoreArgs &e, int which,
+                                           int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid) {
+  if (which == 1) {
+    store_any<L, OT>(acc, e, m0, n0, mvalid, nvalid);
+  } else {
+    StoreArgs p = e;
+    p.C = e.part;
+    p.addend = nullptr;
+    p.accumulate = e.part_accumulate;
+    store_any<L, float>(acc, p, m0, n0, mvalid, nvalid);
+  }
+}
+
 // fp32 gradient GEMMs (4-stage loop, 32 x 32 MFMAs).
 template <int DT, int OT>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
@@ -480,6 +502,8 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
+  const int which = pass_store(e);
+  if (which == 0) return;
   const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
   int64_t mvalid = s.M - m0, nvalid = s.N - n0, K_eff = s.K;
   if (s.count_on == 1) mvalid = dev_count(s.count, s.count_off + m0, mvalid);
@@ -487,7 +511,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   if (mvalid <= 0 || nvalid <= 0) return;
   f32x16 acc[4][4];
   mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
-  store_any<Acc32, typename Elem<OT>::T>(acc, e, m0, n0, mvalid, nvalid);
+  store_pass<Acc32, typename Elem<OT>::T>(acc, e, which, m0, n0, mvalid, nvalid);
 }
 
 // The 16-bit gradient GEMMs' 8-wave form: 512 threads, two waves per SIMD, each 128 x 64 of the tile; the second
@@ -503,6 +527,8 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   lds_char *smem = (lds_char *)smem_;
   int mt, nt;
   if (!tile_of(s, mt, nt)) return;
+  const int which = pass_store(e);
+  if (which == 0) return;
   const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
   int64_t mvalid = s.M - m0, nvalid = s.N - n0, K_eff = s.K;
   if (s.count_on == 1) mvalid = dev_count(s.count, s.count_off + m0, mvalid);
@@ -512,7 +538,7 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   if constexpr (KM == KM_A) mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
   else if constexpr (KM == KM_B) mainloop_ring5<DT, OpRowsN<8, 128>, OpColsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
   else mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
-  store_any<Acc16N<4>, typename Elem<OT>::T>(acc, e, m0, n0, mvalid, nvalid);
+  store_pass<Acc16N<4>, typename Elem<OT>::T>(acc, e, which, m0, n0, mvalid, nvalid);
 }
 
 // The logits-shaped GEMMs on the 8-wave loop (16-bit operands): 512 threads, two waves per SIMD, each 128 x 64, with

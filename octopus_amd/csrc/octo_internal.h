@@ -82,12 +82,21 @@ struct HitArgs {
 int launch_hit(const HitArgs &a, hipStream_t st);
 
 struct StoreArgs {
-  void *C;
-  const float *addend;  // optional fp32 term added before the store, [M, ld_add]
-  int64_t ldc;          // elements
-  int64_t ld_add;       // elements
-  int dtype;
-  int accumulate;
+  void *C = nullptr;
+  const float *addend = nullptr;  // optional fp32 term added before the store, [M, ld_add]
+  int64_t ldc = 0;                // elements
+  int64_t ld_add = 0;             // elements
+  int dtype = OCTO_F32;
+  int accumulate = 0;
+  // A GEMM of one row pass of several (K = the pass's rows), with the row count on the device (pass_count != NULL):
+  // a pass that starts at or past the count (pass_r0 > 0) stores nothing. With fp32 partials (part != NULL, laid out
+  // as C with row stride ldc), the pass whose end reaches the count (count <= pass_end) stores the final C as above
+  // (addend = the earlier passes' partials); an earlier pass stores its sum to part instead (= or += by
+  // part_accumulate). No count: C as above, the host having chosen the destination.
+  const int32_t *pass_count = nullptr;
+  int64_t pass_r0 = 0, pass_end = 0;
+  float *part = nullptr;
+  int part_accumulate = 0;
 };
 
 int launch_gemm_stats(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,

@@ -77,13 +77,28 @@ def test_backward_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     assert ws <= BUDGET + extra + (1 << 20), (ws, extra)
     whole_dz = n * Vp * esz
     assert ws < whole_dz  # the [rows, V] staging of a whole pass would not fit
-    # as few chunks as the budget allows: with one chunk fewer the staging would not fit
+    # the staging of a chunk fits the budget; the chunk count is the fewest that fit or, with grad_W, up to 3 more when
+    # that takes grad_W fewer rounds of tiles
     per_col = P * esz * (1 + (esz == 4 and need_gw)) + (d * esz if (V % 64 or d % 256 or esz == 4) else 0) + \
         (d * 2 if w == _lib.FP8E4M3 else 0)
-    assert per_col * Vc + P * d * 4 <= BUDGET
-    if chunks > 1:
-        wider = -(-(-(-Vp // (chunks - 1))) // 256) * 256
-        assert per_col * wider + (P * d * 4 if chunks > 2 else 0) > BUDGET or per_col * Vp > BUDGET
+    assert per_col * Vc + (P * d * 4 if chunks > 1 else 0) <= BUDGET
+
+    def width(c):
+        return -(-(-(-Vp // c)) // 256) * 256
+
+    fewest = next(c for c in range(1, Vp // 256 + 1)
+                  if per_col * width(c) + (P * d * 4 if c > 1 else 0) <= BUDGET)
+    if need_gw:
+        assert fewest <= chunks <= fewest + 3
+        assert _gradw_rounds(Vp, d, Vc) <= _gradw_rounds(Vp, d, width(fewest))
+    else:
+        assert chunks == fewest
+
+
+def _gradw_rounds(Vp, d, Vc):
+    """Rounds of 32 tiles per XCD (tiles dealt evenly to 8 XCDs) of grad_W = dz^T . h over the vocabulary chunks."""
+    nd = -(-d // 256)
+    return sum(-(-(-(-(min(Vc, Vp - v0) // 256) * nd // 8)) // 32) for v0 in range(0, Vp, Vc))
 
 
 def test_backward_plan_follows_the_workspace():
