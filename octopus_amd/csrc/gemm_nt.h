@@ -71,13 +71,21 @@ struct GemmShape {
 __host__ __device__ inline int64_t tile_grid(int mtiles, int ntiles) {
   return 8 * (((int64_t)mtiles * ntiles + 7) / 8);
 }
-__device__ __forceinline__ bool tile_of(const GemmShape &s, int &mt, int &nt) {
-  const int64_t b = blockIdx.x;
-  const int x = (int)(b & 7);
-  const int64_t k = b >> 3;
-  int64_t mtiles = s.mtiles, ntiles = s.ntiles;
+// The tile grid after a device-side row count's bound (read from memory).
+__device__ __forceinline__ void bounded_tiles(const GemmShape &s, int64_t &mtiles, int64_t &ntiles) {
+  mtiles = s.mtiles;
+  ntiles = s.ntiles;
   if (s.count_on == 1) mtiles = min(mtiles, cdiv(dev_count(s.count, s.count_off, s.M), (int64_t)TM));
   if (s.count_on == 2) ntiles = min(ntiles, cdiv(dev_count(s.count, s.count_off, s.N), (int64_t)TN));
+}
+// Tiles XCD x holds in the order below.
+__device__ __forceinline__ int64_t xcd_tiles(int x, int64_t mtiles, int64_t ntiles) {
+  const int64_t T = (mtiles % 8) * ntiles;
+  return (mtiles / 8) * ntiles + (x + 1) * T / 8 - x * T / 8;
+}
+// XCD x's k-th tile; false past its tiles.
+__device__ __forceinline__ bool tile_at(const GemmShape &s, int x, int64_t k, int64_t mtiles, int64_t ntiles, int &mt,
+                                        int &nt) {
   const int64_t mfull = mtiles / 8;  // M-tiles every XCD owns: x, x + 8, ..., x + 8 (mfull - 1)
   const int64_t main = mfull * ntiles;
   if (k < main) {
@@ -96,6 +104,12 @@ __device__ __forceinline__ bool tile_of(const GemmShape &s, int &mt, int &nt) {
   mt = (int)(8 * mfull + L % r);
   nt = (int)(L / r);
   return true;
+}
+// The one-shot grid's block -> (mt, nt): block b is XCD b % 8's (b / 8)-th tile.
+__device__ __forceinline__ bool tile_of(const GemmShape &s, int &mt, int &nt) {
+  int64_t mtiles, ntiles;
+  bounded_tiles(s, mtiles, ntiles);
+  return tile_at(s, (int)(blockIdx.x & 7), (int64_t)(blockIdx.x >> 3), mtiles, ntiles, mt, nt);
 }
 
 template <int DT> struct Mfma;
@@ -528,67 +542,86 @@ __device__ __forceinline__ void ring5_stage(const OA &opa, const OB &opb, int kd
   }
 }
 
-// smem: SMEM_RING5 bytes. 16-bit types only.
-template <int DT, typename OA, typename OB, bool SPLIT = false>
-__device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &B, int64_t m0, int64_t n0,
-                                               int64_t K_eff, lds_char *smem, f32x4 (&acc)[OA::NB][OB::NB]) {
-  static_assert(DT == OCTO_BF16 || DT == OCTO_F16, "16-bit operands");
-  static_assert(OA::NI == OB::NI, "one workgroup shape");
-  constexpr int NI = OA::NI, NWN = TN / (16 * OB::NB);  // waves along N
-  const int w = threadIdx.x >> 6;
-  const int wm = w / NWN, wn = w % NWN;
+__device__ __forceinline__ int ring_slot(int s) { return s >= ENSLOT ? s - ENSLOT : s; }
+
+// The ring loop's prologue: stage 0 into slots (sa0, sa0 + 1), stage 1 (when nk > 1) into (sa0 + 2, sa0 + 3), mod 5.
+template <typename OA, typename OB>
+__device__ __forceinline__ void ring5_prologue(const OA &opa, const OB &opb, int sa0, uint32_t kbytes, int nk,
+                                               lds_char *smem) {
+  constexpr int NI = OA::NI;
+#pragma unroll
+  for (int q = 0; q < NI; ++q) opa.dma(0, q, kbytes, smem + ring_slot(sa0) * ESLICE);
+#pragma unroll
+  for (int q = 0; q < NI; ++q) opb.dma(0, q, kbytes, smem + ring_slot(sa0 + 1) * ESLICE);
+  if (nk > 1) {
+#pragma unroll
+    for (int q = 0; q < NI; ++q) opa.dma(1, q, kbytes, smem + ring_slot(sa0 + 2) * ESLICE);
+#pragma unroll
+    for (int q = 0; q < NI; ++q) opb.dma(1, q, kbytes, smem + ring_slot(sa0 + 3) * ESLICE);
+  }
+}
+
+// The ring loop after its prologue, stage j of the tile in slots (sa0 + 2 j, sa0 + 2 j + 1) mod 5; acc is zeroed
+// here. Ends with every DMA landed and every wave past its last LDS read (the slots are free), and returns the slot
+// that continues the ring, (sa0 + 2 nk) mod 5. VMEM instructions issued after the prologue's (a previous tile's
+// epilogue stores) are fine: loads complete in order among themselves, so at most 2 NI outstanding means stage 0 in.
+template <int DT, typename OA, typename OB, bool SPLIT>
+__device__ __forceinline__ int ring5_run(const OA &opa, const OB &opb, int sa0, uint32_t kbytes, int nk,
+                                         lds_char *smem, f32x4 (&acc)[OA::NB][OB::NB]) {
+  constexpr int NI = OA::NI;
 #pragma unroll
   for (int i = 0; i < OA::NB; ++i)
 #pragma unroll
     for (int j = 0; j < OB::NB; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[i][j][v] = 0.f;
-
-  const uint32_t kbytes = (uint32_t)(K_eff * 2);
-  const int nk = (int)((kbytes + EKB - 1) / EKB);
-  if (nk == 0) return;
-
-  OA opa;
-  OB opb;
-  opa.init(A, m0, wm, (uint32_t)K_eff);
-  opb.init(B, n0, wn, (uint32_t)K_eff);
-
-  // prologue: stages 0 and 1 into slots 0..3
-#pragma unroll
-  for (int q = 0; q < NI; ++q) opa.dma(0, q, kbytes, smem);
-#pragma unroll
-  for (int q = 0; q < NI; ++q) opb.dma(0, q, kbytes, smem + ESLICE);
-  if (nk > 1) {
-#pragma unroll
-    for (int q = 0; q < NI; ++q) opa.dma(1, q, kbytes, smem + 2 * ESLICE);
-#pragma unroll
-    for (int q = 0; q < NI; ++q) opb.dma(1, q, kbytes, smem + 3 * ESLICE);
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NI));  // stage 0 landed
-  } else {
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  }
+  if (nk == 0) return sa0;
+  if (nk > 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NI));  // stage 0 landed
+  else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   __builtin_amdgcn_s_barrier();
 
   typename OA::F fa[2][OA::NB];
   typename OB::F fb[2][OB::NB];
 #pragma unroll
-  for (int b = 0; b < OA::NB; ++b) fa[0][b] = opa.frag(smem, 0, b);
+  for (int b = 0; b < OA::NB; ++b) fa[0][b] = opa.frag(smem + ring_slot(sa0) * ESLICE, 0, b);
 #pragma unroll
-  for (int b = 0; b < OB::NB; ++b) fb[0][b] = opb.frag(smem + ESLICE, 0, b);
-  int sa = 0;  // slot of stage k's A slice: 2 k mod 5
+  for (int b = 0; b < OB::NB; ++b) fb[0][b] = opb.frag(smem + ring_slot(sa0 + 1) * ESLICE, 0, b);
+  int sa = sa0;  // slot of stage k's A slice: sa0 + 2 k mod 5
   int k = 0;
   for (; k + 2 < nk; ++k) {
     ring5_stage<DT, OA, OB, true, true, true, SPLIT>(opa, opb, k + 2, sa, kbytes, smem, fa, fb, acc);
-    sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
+    sa = ring_slot(sa + 2);
   }
   if (k + 1 < nk) {
     ring5_stage<DT, OA, OB, false, true, true, SPLIT>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
-    sa = (sa + 2 >= ENSLOT) ? sa + 2 - ENSLOT : sa + 2;
+    sa = ring_slot(sa + 2);
     ++k;
   }
   ring5_stage<DT, OA, OB, false, false, false, SPLIT>(opa, opb, k, sa, kbytes, smem, fa, fb, acc);
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0) & WAIT_LGKM0);
   __builtin_amdgcn_s_barrier();
+  return ring_slot(sa + 2);
+}
+
+// smem: SMEM_RING5 bytes. 16-bit types only.
+template <int DT, typename OA, typename OB, bool SPLIT = false>
+__device__ __forceinline__ void mainloop_ring5(const Operand &A, const Operand &B, int64_t m0, int64_t n0,
+                                               int64_t K_eff, lds_char *smem, f32x4 (&acc)[OA::NB][OB::NB]) {
+  static_assert(DT == OCTO_BF16 || DT == OCTO_F16, "16-bit operands");
+  static_assert(OA::NI == OB::NI, "one workgroup shape");
+  constexpr int NWN = TN / (16 * OB::NB);  // waves along N
+  const int w = threadIdx.x >> 6;
+  const int wm = w / NWN, wn = w % NWN;
+  const uint32_t kbytes = (uint32_t)(K_eff * 2);
+  const int nk = (int)((kbytes + EKB - 1) / EKB);
+  OA opa;
+  OB opb;
+  if (nk > 0) {
+    opa.init(A, m0, wm, (uint32_t)K_eff);
+    opb.init(B, n0, wn, (uint32_t)K_eff);
+    ring5_prologue(opa, opb, 0, kbytes, nk, smem);
+  }
+  ring5_run<DT, OA, OB, SPLIT>(opa, opb, 0, kbytes, nk, smem, acc);
 }
 
 // ---- accumulator layouts of a wave's 128 x 128 sub-tile --------------------------------------------
