@@ -2,10 +2,12 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg3] [--no-cpu-baseline]
 
-A step is one pass of the path over one packed micro-batch, inputs resident in HBM:
-  compaction of the scored rows -> fused forward (MFMA GEMM + softmax epilogue; merge with target gather and the
-  GRPO weight g of each compact row) -> fused backward (recompute dz, grad_hidden and grad_W GEMMs, row scatter,
-  grad_W to bf16).
+A step is one pass of the path over one packed micro-batch, inputs resident in HBM: compaction of the scored rows,
+then the head's GRPO step in one call (octo_head_step_grpo), row pass by row pass: the logits GEMM with the softmax
+statistics and each element's tile-relative exponential in its epilogue; the merge (logprob, entropy, target gather,
+GRPO weight g and loss); the exponentials scaled into dz; the grad_hidden and grad_W GEMMs; row scatter, grad_W to
+bf16. --two-call runs the forward and the backward as the autograd route calls them instead (octo_head_fwd_grpo,
+then octo_head_bwd, which recomputes the logits); the default run also times that route for context.
 Default workload cfg3: N = 32,768 packed tree tokens (an 8,192-token root shared by 12 branches of 2,048,
 root masked: 24,576 scored rows), d = 2560, V = 151,936, bf16, T = 1.0 (octopus_amd.workloads).
 Prints one JSON line: packed tokens/s; per GEMM kernel, its average launch time from HIP events recorded around
@@ -68,17 +70,19 @@ def cpu_baseline(cfg, scored_rows: int, target_s: float = 4.0) -> dict:
                       f"scored rows (extrapolated); {r['threads']} threads = os.cpu_count(); host: {model}"}
 
 
-GEMM_KERNELS = ("gemm_stats", "gemm_dz", "gemm_store_grad_h", "gemm_store_grad_w")
+GEMM_KERNELS = ("gemm_stats", "gemm_dz", "gemm_store_grad_h", "gemm_store_grad_w", "gemm_grads", "dz_scale")
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 
-def recorded_traffic(kernel: str, workload: str):
+def recorded_traffic(kernel: str, workload: str, fused: bool = False):
     """HBM bytes per launch of `kernel` at `workload` as recorded from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-    in profiles/gemm_kernels_<workload>_counters.md (line `traffic <kernel>: <bytes>`), or None."""
+    in profiles/gemm_kernels_<workload>_counters.md (line `traffic <kernel>: <bytes>`, or `traffic step <kernel>:`
+    for the fused step's launches), or None."""
     path = os.path.join(PROFILES, f"gemm_kernels_{workload}_counters.md")
+    key = f"traffic step {kernel}:" if fused else f"traffic {kernel}:"
     try:
         for line in open(path):
-            if line.startswith(f"traffic {kernel}:"):
+            if line.startswith(key):
                 return float(line.split(":", 1)[1].split()[0])
     except OSError:
         pass
@@ -231,6 +235,9 @@ def main() -> int:
     ap.add_argument("--bwd-workspace-mib", type=int, default=0,
                     help="give the backward this much workspace instead of the queried size (its plan of row passes "
                          "and vocabulary chunks follows the workspace)")
+    ap.add_argument("--two-call", action="store_true",
+                    help="run the forward and the backward as two calls (octo_head_fwd_grpo, octo_head_bwd: the "
+                         "autograd route, logits recomputed in the backward) instead of the fused step")
     ap.add_argument("--hipblaslt", action="store_true",
                     help="only time torch.matmul (hipBLASLt) on the four plain GEMMs of the workload's step, "
                          "without any epilogue, for context; then exit")
@@ -270,6 +277,7 @@ def main() -> int:
     from octopus_amd.workloads import CONFIGS, make_batch
     if args.bwd_workspace_mib:
         head_op.BWD_WORKSPACE_BYTES = args.bwd_workspace_mib << 20
+        head_op.STEP_WORKSPACE_BYTES = args.bwd_workspace_mib << 20
 
     cfg = CONFIGS[args.workload]
     dev = torch.device("cuda", 0)
@@ -305,11 +313,22 @@ def main() -> int:
         return head_op.head_bwd(h, W, b.w_scale, y, idx, count, lse, g, inv_T, 1.0, 1.0, False, True, True,
                                 need_w)
 
+    def two_call():
+        idx, count, out, lse, g = forward_grpo()
+        return backward(idx, count, lse, g)
+
+    def fused_step():
+        # forward, GRPO weight and loss, grad_hidden and grad_W in one call, the logits computed once per row pass
+        idx, count = head_op.compact_rows(b.scored)
+        return head_op.head_step_grpo(h, W, b.w_scale, y, idx, count, inv_T, 1.0, 1.0, False, True, True, old,
+                                      None, b.adv, mask_f, 0.2, 0.28, 5.0, True, need_w)
+
+    fused = cfg.backward != "none" and not args.two_call
+
     def step():
         if cfg.backward == "none":  # a forward-only workload: logprob and entropy of every scored row
             return forward()[2]
-        idx, count, out, lse, g = forward_grpo()
-        return backward(idx, count, lse, g)
+        return fused_step() if fused else two_call()
 
     for _ in range(args.warmup):
         step()
@@ -330,9 +349,13 @@ def main() -> int:
                              "ms_per_step": total / args.steps}
     _lib.call("octo_timing_enable", 0)
 
-    # per-phase HIP-event timing on the launch stream (torch's current stream carries every launch)
+    # per-phase HIP-event timing on the launch stream (torch's current stream carries every launch): the forward
+    # and the backward of the two-call route (for the fused step: context beside its own time)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     fwd_ms, bwd_ms, reps = [], [], 3
+    if fused:
+        two_call()
+        torch.cuda.synchronize()
     for _ in range(reps):
         ev[0].record()
         if cfg.backward == "none":
@@ -352,18 +375,28 @@ def main() -> int:
 
     n, d, V = scored_rows, cfg.d, cfg.V
     alg_flop = {"full": 6, "hidden": 4, "none": 2}[cfg.backward] * n * d * V
-    exe_flop = {"full": 8, "hidden": 6, "none": 2}[cfg.backward] * n * d * V
+    # executed: the fused step computes the logits once (as the forward-only workload), the two-call route twice
+    exe_flop = ({"full": 6, "hidden": 4, "none": 2} if fused or cfg.backward == "none"
+                else {"full": 8, "hidden": 6})[cfg.backward] * n * d * V
     peak = PEAK_BF16 if cfg.dtype != torch.float32 else PEAK_F32
     step_s = ms / 1e3
     # every GEMM kernel of the path is one dense contraction of 2 * n * d * V FLOP per step: logits
-    # (gemm_stats), logits again -> dz (gemm_dz), dz . W (gemm_store_grad_h), dz^T . h (gemm_store_grad_w);
-    # a kernel launched in several row passes does 2 * n * d * V / launches per launch on average
+    # (gemm_stats), logits again -> dz (gemm_dz, two-call route only), dz . W (gemm_store_grad_h), dz^T . h
+    # (gemm_store_grad_w); a kernel launched in several row passes does 2 * n * d * V / launches per launch on
+    # average. dz_scale (fused step) is HBM-bound: 4 bytes per element of the scored rows' [n, V_pad] (an f16
+    # exponential read, a 16-bit dz written)
     flop_step = 2 * n * d * V
-    for k in kernels.values():
-        k["flop_per_launch"] = flop_step / k["launches_per_step"]
+    V_pad = -(-V // 256) * 256
+    for name, k in kernels.items():
+        if name == "dz_scale":
+            k["bytes_per_launch"] = 4 * n * V_pad / k["launches_per_step"]
+            k["GBps"] = k["bytes_per_launch"] / (k["avg_ms"] / 1e3) / 1e9
+            continue
+        # gemm_grads (fused step) runs both gradient GEMMs of a row pass in one launch
+        k["flop_per_launch"] = flop_step * (2 if name == "gemm_grads" else 1) / k["launches_per_step"]
         k["tflops"] = k["flop_per_launch"] / (k["avg_ms"] / 1e3) / 1e12
     for name, k in kernels.items():  # fabric (HBM side of L2) bytes per launch from the recorded rocprof counters
-        t = recorded_traffic(name, cfg.name)
+        t = recorded_traffic(name, cfg.name, fused)
         k["traffic_GBps"] = t / (k["avg_ms"] / 1e3) / 1e9 if t else None
     # the weight stream: the logits GEMM reads W (its MFMA operand: bf16, fp8 weights widened) once per launch
     w_bytes = V * d * (4 if cfg.dtype == torch.float32 else 2)
@@ -376,7 +409,7 @@ def main() -> int:
     # The roofline kernel: the one with the most time per step among those whose FLOP are algorithmic work of the
     # metric (the forward logits GEMM and the two gradient GEMMs); gemm_dz recomputes the logits (executed, not
     # algorithmic work) and is never credited. The whole path's algorithmic and executed fractions sit beside it.
-    algorithmic = [k for k in ("gemm_stats", "gemm_store_grad_h", "gemm_store_grad_w") if k in kernels]
+    algorithmic = [k for k in ("gemm_stats", "gemm_store_grad_h", "gemm_store_grad_w", "gemm_grads") if k in kernels]
     dom = max(algorithmic, key=lambda k: kernels[k]["ms_per_step"])
     flop_launch = kernels[dom]["flop_per_launch"]
     dom_achieved = flop_launch / (kernels[dom]["avg_ms"] / 1e3)
@@ -393,19 +426,24 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16" if cfg.dtype == torch.bfloat16 else str(cfg.dtype).replace("torch.", ""),
         "data": "synthetic (seeded: hidden N(0,1) RMS-normalised, W N(0,0.02), Zipf(1.1) targets)",
-        "config": {"workload": f"{cfg.name}: packed tree micro-batch, fused fwd+bwd GRPO logprob head",
+        "config": {"workload": f"{cfg.name}: packed tree micro-batch, "
+                               + ("fused fwd+bwd GRPO logprob head (one call)" if fused else
+                                  "GRPO logprob head, forward then backward (two calls)" if cfg.backward != "none"
+                                  else "logprob head forward"),
                    "N_packed": cfg.N, "scored_rows": n, "d": d, "V": V, "temperature": cfg.temperature,
                    "backward": cfg.backward, "weight": "fp8 e4m3 + row scales" if cfg.fp8_weight else "as hidden",
                    "parallelism": "single GPU"},
         "mfma_frac_algorithmic": alg_flop / step_s / peak,
         "mfma_frac_executed": exe_flop / step_s / peak,
-        "phase_ms": {"forward": fwd_ms, "backward": bwd_ms},
+        "phase_ms": ({"two_call_forward": fwd_ms, "two_call_backward": bwd_ms, "two_call_step": fwd_ms + bwd_ms}
+                     if fused else {"forward": fwd_ms, "backward": bwd_ms}),
         "kernels": kernels,
         "weight_stream": weight_stream,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": dom_achieved / 1e12, "peak": peak / 1e12,
                      "unit": "TFLOP/s", "frac": dom_achieved / peak,
-                     "traffic": recorded_traffic(dom, cfg.name),
-                     "per_launch": f"2*n*d*V / launches = {flop_launch:.4g} algorithmic FLOP (n={n} scored rows, "
+                     "traffic": recorded_traffic(dom, cfg.name, fused),
+                     "per_launch": f"{'4' if dom == 'gemm_grads' else '2'}*n*d*V / launches = {flop_launch:.4g} "
+                                   f"algorithmic FLOP (n={n} scored rows, "
                                    f"{kernels[dom]['launches_per_step']:g} launches per step), HIP events "
                                    f"around each launch over the timed steps",
                      "path_frac_algorithmic": alg_flop / step_s / peak,

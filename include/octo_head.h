@@ -33,6 +33,10 @@
  *   AReaL grpo_loss_fn (cited by docs/rl-plan-episodes.md:496-497, constants grpo.yaml:103-118)
  *                                                  -> octo_grpo_grad, or fused into the forward's
  *                                                     last step: octo_head_fwd_grpo
+ *   octopus/rl/actor.py:343-347 (AReaL's grpo_loss_fn reads the head's columns, then loss.backward()
+ *     runs lm_head.py:115-121's checkpoint recompute) -> octo_head_step_grpo (forward, GRPO loss and
+ *                                                     backward in one call, the logits computed once per
+ *                                                     row pass)
  */
 #ifndef OCTO_HEAD_H
 #define OCTO_HEAD_H
@@ -69,14 +73,16 @@ extern "C" {
                                  /* base-2 maximum of s log2(e) and log2 of the shifted sum, lse =       */
                                  /* (m2 + l2S) ln 2; the backward then repeats the forward's rounding    */
                                  /* (exact dz row sums when the logits sit far from zero)                */
+#define OCTO_WS_STEP        128  /* octo_head_workspace_bytes / octo_head_bwd_plan: for octo_head_step_grpo */
 #define OCTO_PAIRS_NONE_AS_COUNT 1 /* octo_label_pairs: positions without a pair get the pair count  */
 
 const char *octo_version(void);
 const char *octo_last_error(void);
 
 /* Kernel timing hook (no counterpart in the reference: a measurement aid for benchmarks). While enabled,
- * every GEMM launch of octo_head_fwd / octo_head_bwd is bracketed by HIP events on its stream, under the
- * names "gemm_stats", "gemm_dz", "gemm_store_grad_h" and "gemm_store_grad_w". octo_timing_read waits for
+ * every GEMM launch of octo_head_fwd / octo_head_bwd / octo_head_step_grpo is bracketed by HIP events on its
+ * stream, under the names "gemm_stats", "gemm_dz", "gemm_store_grad_h" and "gemm_store_grad_w" (and the step's
+ * "dz_scale"). octo_timing_read waits for
  * the recorded launches of one name and returns their count and summed duration. octo_timing_enable
  * (either value) discards what was recorded. Off by default; enabling it creates events (allocates). */
 int octo_timing_enable(int on);
@@ -239,6 +245,33 @@ int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                        float inv_T, float pre, float post, int use_tanh,
                        float *logp, float *ent, float *lse, float *out2, int64_t ld_out2,
                        const octo_grpo_tail *grpo, void *ws, size_t ws_bytes, void *stream);
+
+/* The GRPO training step of the head in one call: octo_head_fwd_grpo's outputs (logp, ent, lse, out2, grpo->g,
+ * grpo->loss, with the same arguments and meaning) and octo_head_bwd's gradients for g = grpo->g (grad_h, grad_w,
+ * ld_gh, gh_dtype, gw_dtype and OCTO_GRADW_ACCUMULATE as there; NULL skips one). lse must not be NULL (the pair
+ * form under OCTO_LSE_PAIR, as for the backward). The gradients are those of grpo->loss; a caller whose loss is
+ * c L scales them by c.
+ * The rows run in passes of at most 32,768 (as many as the staging budget holds, balanced). The forward GEMM of a
+ * pass stores each element's exponential relative to its 256-column tile's maximum, exp2(s log2 e - m_tile) x
+ * post'(z) (x the fp8 row scale), as [rows, V rounded up to 256] in the MFMA type; once the merge has the rows'
+ * (m2, l2S) and g, each tile is scaled by -g exp2(m_tile - m2 - l2S) / T into dz (the label entry written from the
+ * fp32 target logit), and grad_h = dz . W, grad_W = dz^T . h run as in octo_head_bwd: the logits are computed
+ * once instead of twice. dz differs from octo_head_bwd's by one more rounding to the MFMA type (the exponential's).
+ * Workspace: octo_head_workspace_bytes with OCTO_WS_STEP [| OCTO_WS_NO_GRADW | OCTO_WS_GATHER], the plan at a
+ * 2 GiB staging budget ([rows, V] of one pass); outside the staging are the pass's (m, S, U) per vocabulary tile,
+ * h^T of a pass, fp32 grad_w partials [V, d] over several passes, and once per call W widened to bf16 (fp8 weights)
+ * or W^T (16-bit weights with V % 64 or d % 256 not 0). A smaller workspace is accepted down to the plan at a
+ * 1 MiB budget; octo_head_bwd_plan with OCTO_WS_STEP gives {rows per pass, passes, V rounded up to 256, 1}.
+ * fp32 operands run octo_head_fwd_grpo, then octo_head_bwd, in the same workspace. */
+int octo_head_step_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
+                        const void *w, int64_t ldw, int w_dtype, const float *w_scale,
+                        const int64_t *labels, const int64_t *idx, const int32_t *count,
+                        int64_t n_max, int d, int V, int flags,
+                        float inv_T, float pre, float post, int use_tanh,
+                        float *logp, float *ent, float *lse, float *out2, int64_t ld_out2,
+                        const octo_grpo_tail *grpo,
+                        void *grad_h, int64_t ld_gh, int gh_dtype, void *grad_w, int gw_dtype,
+                        void *ws, size_t ws_bytes, void *stream);
 
 /* GRPO/PPO policy-gradient weight per token (AReaL grpo_loss_fn semantics):
  *   ratio r = exp(logp - prox)          (prox == NULL: prox = logp, i.e. reuse_train_logp)

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(HERE, "libocto_head.so")
 OK, EINVAL, EWORKSPACE, EUNSUPPORTED, EHIP = 0, -1, -2, -3, -4
 BF16, F16, F32, FP8E4M3 = 0, 1, 2, 3
 ROWS_VIA_IDX, OUT_SCATTER, GRADW_ACCUMULATE, WS_BACKWARD, WS_NO_GRADW, WS_GATHER, LSE_PAIR = 1, 2, 4, 8, 16, 32, 64
+WS_STEP = 128
 PAIRS_NONE_AS_COUNT = 1
 
 _p = ctypes.c_void_p
@@ -52,6 +53,9 @@ SIGNATURES = {
                               _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, _p],
     "octo_head_bwd": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                       _f32, _f32, _f32, _i32, _p, _p, _p, _i64, _i32, _p, _i32, _p, _sz, _p],
+    "octo_head_step_grpo": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                            _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, ctypes.POINTER(GrpoTail),
+                            _p, _i64, _i32, _p, _i32, _p, _sz, _p],
     "octo_columns_fwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p],
     "octo_columns_bwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p, _i64, _p],
     "octo_pairs_expand": [_p, _i64, _i32, _p, _i64, _p, _p],
@@ -117,7 +121,8 @@ def workspace_bytes(n_max: int, d: int, V: int, w_dtype: int, flags: int) -> int
 
 
 def bwd_plan(n_max: int, d: int, V: int, w_dtype: int, flags: int, ws_bytes: int) -> tuple[int, int, int, int]:
-    """(rows per pass, passes, vocabulary columns per chunk, chunks) that octo_head_bwd runs in ws_bytes."""
+    """(rows per pass, passes, vocabulary columns per chunk, chunks) that octo_head_bwd runs in ws_bytes; with
+    WS_STEP in flags, octo_head_step_grpo's (rows per pass, passes, V rounded up to 256, 1)."""
     out = (_i64 * 4)()
     call("octo_head_bwd_plan", n_max, d, V, w_dtype, flags, ws_bytes, out)
     return tuple(out)

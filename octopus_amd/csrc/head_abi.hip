@@ -265,6 +265,102 @@ bool bwd_plan_for(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool n
   return false;
 }
 
+// ---- the fused GRPO step's plan (octo_head_step_grpo) ----------------------------------------------------
+// The step runs the rows in passes of P; per pass its forward GEMM stores, besides the statistics, every element's
+// tile-relative exponential (StatsArgs::ex) into a [P, V_pad] staging area in the MFMA type, which launch_dz_scale
+// turns into dz once the merge has the rows' (m2, l2S) and g; the gradient GEMMs read it as the backward's read
+// their dz. Rows per pass: the most that fit the staging budget (at most kPassRowsMax), balanced over the passes.
+// The staging is the only part that grows with the budget; outside it sit the pass's statistics [P, V / 256], h^T
+// [d, P], the label entries [P], fp32 grad_W partials [V, d] over several passes, and, once per call, W widened to
+// bf16 (fp8 weights) or staged as W^T (16-bit weights that grad_h cannot read K-major as stored).
+struct StepLayout {
+  int64_t P, passes, mtiles, V_pad;
+  int esz;
+  bool gacc_on, wide_on, wt_on;
+  size_t part, z, hit, ht, dz, wide, wt, gacc, rows, total;
+};
+
+// Rows per pass for a step without grad_W: each pass's grad_h launch is one tile per CU per round of long tiles (K =
+// V), so a pass whose tiles overrun a multiple of the 256 CUs pays a whole extra round for the overrun. Of the pass
+// sizes up to pmax (multiples of 256), the one whose passes take the fewest grad_h rounds in total, the largest on a
+// tie: at d 2560 and 131,072 rows, 25 x 256 rows (250 tiles, 21 passes, 21 rounds) against 27 x 256 (270 tiles,
+// 19 passes, 38 rounds). With grad_W the two gradients share one launch, whose short grad_W tiles fill those rounds.
+int64_t gradh_pass_rows(int64_t n_max, int d, int64_t pmax) {
+  const int64_t nt = cdiv(n_max, TN), nd = cdiv(d, TN), cus = 256;
+  int64_t best_p = 0, best_r = 0;
+  for (int64_t p = pmax / TN; p >= 1; --p) {
+    const int64_t passes = cdiv(nt, p), last = nt - (passes - 1) * p;
+    const int64_t r = (passes - 1) * cdiv(p * nd, cus) + cdiv(last * nd, cus);
+    if (!best_p || r < best_r) {
+      best_p = p;
+      best_r = r;
+    }
+  }
+  return best_p * TN;
+}
+
+// False when the budget holds fewer than 256 rows, or for fp32 operands (the step then runs the forward and the
+// backward: step_fallback).
+bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw, bool gather, size_t budget,
+               StepLayout &L) {
+  L.esz = elem_bytes(staged_dtype(w_dtype));
+  if (L.esz != 2) return false;
+  L.mtiles = cdiv(V, TM);
+  L.V_pad = L.mtiles * TM;
+  int64_t pmax = kPassRowsMax;
+  if (budget) {
+    const int64_t fit = (int64_t)(budget / ((size_t)L.V_pad * L.esz)) / TN * TN;
+    if (fit < TN) return false;
+    if (fit < pmax) pmax = fit;
+  }
+  L.passes = n_max > 0 ? cdiv(n_max, pmax) : 0;
+  L.P = n_max > 0 ? round_up(cdiv(n_max, L.passes), TN) : 0;
+  if (n_max > 0 && need_gh && !need_gw) L.P = gradh_pass_rows(n_max, d, pmax);
+  L.passes = n_max > 0 ? cdiv(n_max, L.P) : 0;
+  L.gacc_on = need_gw && L.passes > 1;
+  L.wide_on = w_dtype == OCTO_FP8E4M3;
+  L.wt_on = need_gh && !gh_reads_w(d, V, w_dtype);
+  size_t off = 0;
+  L.part = off;  // (m, S, U) per (row of the pass, vocabulary tile)
+  off += align_up((size_t)L.P * L.mtiles * sizeof(f32x4));
+  L.z = off;  // the GRPO tail's token count
+  off += kAlign;
+  L.hit = off;  // dz at each row's label [P] fp32
+  off += align_up((size_t)L.P * sizeof(float));
+  L.ht = off;  // h^T [d, P] of the pass's rows (grad_W)
+  if (need_gw) off += align_up((size_t)d * L.P * L.esz);
+  L.dz = off;  // the exponentials, then dz [P, V_pad], token-major
+  off += align_up((size_t)L.P * L.V_pad * L.esz);
+  L.wide = off;  // fp8 weights widened to bf16 [V, d]
+  if (L.wide_on) off += align_up((size_t)V * d * 2);
+  L.wt = off;  // W^T [d, V_pad] (grad_h, when it cannot read W K-major)
+  if (L.wt_on) off += align_up((size_t)d * L.V_pad * L.esz);
+  L.gacc = off;  // fp32 grad_W partial sums across passes
+  if (L.gacc_on) off += align_up((size_t)V * d * sizeof(float));
+  L.rows = off;  // the gathered hidden rows (OCTO_WS_GATHER), last
+  if (gather) off += gather_bytes(n_max, d, w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_dtype);
+  L.total = off;
+  return true;
+}
+
+// The plan the step runs in ws_bytes: unbounded if it fits, else the largest candidate staging budget that fits.
+bool step_plan_for(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw, bool gather,
+                   size_t ws_bytes, StepLayout &L) {
+  if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, 0, L) && L.total <= ws_bytes) return true;
+  for (int q = kBudgetQMax; q >= kBudgetQMin; --q)
+    if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, staging_candidate(q), L) && L.total <= ws_bytes)
+      return true;
+  return false;
+}
+
+// Workspace of the step for fp32 operands: the forward's, then the backward's (at the default budget), in turn.
+size_t step_fallback_bytes(int64_t n_max, int d, int V, int w_dtype, bool need_gw, bool gather) {
+  const size_t f = fwd_layout(n_max, d, V, w_dtype, gather).total;
+  BwdLayout B;
+  const size_t b = bwd_plan(n_max, d, V, w_dtype, true, need_gw, gather, kStagingBudget, B) ? B.total : 0;
+  return f > b ? f : b;
+}
+
 struct Common {
   int hesz, wesz, dt;
   bool fp8;
@@ -402,6 +498,99 @@ GemmShape shape(int64_t M, int64_t N, int64_t K, int group_m, int count_on, cons
   return s;
 }
 
+// grad_W[v0 .. v0 + vc) of row pass p (rows r0 .. r0 + rows, K = rows) from the pass's dz A3 and h^T B3: stored in
+// gw_dtype when the pass is the only one or the last (adding the fp32 partials of the earlier passes when gacc_on),
+// else as fp32 partials (gacc_on) or added to the output. With a device row count the count decides which pass is
+// the last (passes at or past it store nothing). gacc and gw point at row v0.
+StoreArgs grad_w_store(int d, int64_t r0, int64_t rows, int64_t p, int64_t passes, bool gacc_on, float *gacc, void *gw,
+                       int gw_dtype, int flags, const int32_t *count) {
+  const bool last_pass = p + 1 == passes;
+  StoreArgs o;
+  const bool acc_out = flags & OCTO_GRADW_ACCUMULATE;
+  if (gacc_on && !last_pass && !count) {  // fp32 partial sums of the passes so far
+    o.C = gacc;
+    o.addend = nullptr;
+    o.dtype = OCTO_F32;
+    o.accumulate = p > 0 ? 1 : 0;
+  } else {
+    o.C = gw;
+    o.addend = (gacc_on && p > 0) ? gacc : nullptr;
+    o.dtype = gw_dtype;
+    o.accumulate = (acc_out || (!gacc_on && p > 0)) ? 1 : 0;
+  }
+  if (count && p > 0) {  // passes at or past the device row count store nothing
+    o.pass_count = count;
+    o.pass_r0 = r0;
+    o.pass_end = r0 + rows;
+  }
+  if (count && gacc_on && !last_pass) {
+    // the device count decides: the pass that reaches it stores grad_W (adding the earlier passes' partials), an
+    // earlier one stores its fp32 partials
+    o.pass_count = count;
+    o.pass_r0 = r0;
+    o.pass_end = r0 + rows;
+    o.part = gacc;
+    o.part_accumulate = p > 0 ? 1 : 0;
+  }
+  o.ldc = d;
+  o.ld_add = d;
+  return o;
+}
+int grad_w_pass(int dt, const Operand &A3, int kmajor, const Operand &B3, int64_t vc, int d, int64_t r0, int64_t rows,
+                int64_t p, int64_t passes, bool gacc_on, float *gacc, void *gw, int gw_dtype, int flags,
+                const int32_t *count, hipStream_t st) {
+  const StoreArgs o = grad_w_store(d, r0, rows, p, passes, gacc_on, gacc, gw, gw_dtype, flags, count);
+  TimedLaunch t("gemm_store_grad_w", st);
+  return launch_gemm_store(dt, A3, B3, shape(vc, d, rows, kGroupM, 3, count, r0), o, st, kmajor);
+}
+
+// The merge's arguments for every row of the call (row_off 0, all n_max rows) with the GRPO tail gt, if any.
+MergeArgs merge_args(const f32x4 *part, int64_t mtiles, const void *h, int64_t ldh, int h_dtype, const void *w,
+                     int64_t ldw, int w_dtype, const float *w_scale, const int64_t *labels, const int64_t *idx,
+                     const int32_t *count, int64_t n_max, int d, int V, int flags, float inv_T, float pre, float post,
+                     int use_tanh, float *logp, float *ent, float *lse, float *out2, int64_t ld_out2,
+                     const octo_grpo_tail *gt, const float *z) {
+  MergeArgs m;
+  m.part = part;
+  m.mtiles = mtiles;
+  m.h = h;
+  m.ldh = ldh;
+  m.h_dtype = h_dtype;
+  m.w = w;
+  m.ldw = ldw;
+  m.w_dtype = w_dtype;
+  m.wscale = w_scale;
+  m.labels = labels;
+  m.idx = idx;
+  m.count = count;
+  m.n_max = n_max;
+  m.d = d;
+  m.V = V;
+  m.flags = flags;
+  m.inv_T = inv_T;
+  m.pre = pre;
+  m.post = post;
+  m.use_tanh = use_tanh;
+  m.logp = logp;
+  m.ent = ent;
+  m.lse = lse;
+  m.lse_pair = (flags & OCTO_LSE_PAIR) != 0;
+  m.out2 = out2;
+  m.ld_out2 = ld_out2;
+  m.gprox = gt ? gt->prox : nullptr;
+  m.gold = gt ? gt->old : nullptr;
+  m.gadv = gt ? gt->adv : nullptr;
+  m.gmask = gt ? gt->mask : nullptr;
+  m.n_tokens = gt ? gt->n_tokens : 0;
+  m.eps_lo = gt ? gt->eps_lo : 0.f;
+  m.eps_hi = gt ? gt->eps_hi : 0.f;
+  m.reject_upper = gt ? gt->reject_upper : 0.f;
+  m.z = z;
+  m.g = gt ? gt->g : nullptr;
+  m.loss = gt ? gt->loss : nullptr;
+  return m;
+}
+
 int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
              const float *w_scale, const int64_t *labels, const int64_t *idx, const int32_t *count, int64_t n_max,
              int d, int V, int flags, float inv_T, float pre, float post, int use_tanh, float *logp, float *ent,
@@ -454,45 +643,181 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
     if (rc) return rc;
   }
 
-  MergeArgs m;
-  m.part = e.part;
-  m.mtiles = L.mtiles;
-  m.h = h;
-  m.ldh = ldh;
-  m.h_dtype = h_dtype;
-  m.w = w;
-  m.ldw = ldw;
-  m.w_dtype = w_dtype;
-  m.wscale = w_scale;
-  m.labels = labels;
-  m.idx = idx;
-  m.count = count;
-  m.n_max = n_max;
-  m.d = d;
-  m.V = V;
-  m.flags = flags;
-  m.inv_T = inv_T;
-  m.pre = pre;
-  m.post = post;
-  m.use_tanh = use_tanh;
-  m.logp = logp;
-  m.ent = ent;
-  m.lse = lse;
-  m.lse_pair = (flags & OCTO_LSE_PAIR) != 0;
-  m.out2 = out2;
-  m.ld_out2 = ld_out2;
-  m.gprox = gt ? gt->prox : nullptr;
-  m.gold = gt ? gt->old : nullptr;
-  m.gadv = gt ? gt->adv : nullptr;
-  m.gmask = gt ? gt->mask : nullptr;
-  m.n_tokens = gt ? gt->n_tokens : 0;
-  m.eps_lo = gt ? gt->eps_lo : 0.f;
-  m.eps_hi = gt ? gt->eps_hi : 0.f;
-  m.reject_upper = gt ? gt->reject_upper : 0.f;
-  m.z = z;
-  m.g = gt ? gt->g : nullptr;
-  m.loss = gt ? gt->loss : nullptr;
+  const MergeArgs m = merge_args(e.part, L.mtiles, h, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count,
+                                 n_max, d, V, flags, inv_T, pre, post, use_tanh, logp, ent, lse, out2, ld_out2, gt, z);
   return launch_merge(m, st);
+}
+
+
+// ---- the fused GRPO step (octo_head_step_grpo) ---------------------------------------------------------
+// Forward, GRPO weight and backward of the compact rows in one call, pass by pass (StepLayout). The logits are
+// computed once per pass: the forward GEMM leaves each element's tile-relative exponential in the staging area, the
+// merge gives the rows' outputs, row state, g and label entry, launch_dz_scale scales the exponentials into dz, and
+// grad_h = dz . W, grad_W = dz^T . h follow as in the backward. fp32 operands run head_fwd, then octo_head_bwd.
+int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
+              const float *w_scale, const int64_t *labels, const int64_t *idx, const int32_t *count, int64_t n_max,
+              int d, int V, int flags, float inv_T, float pre, float post, int use_tanh, float *logp, float *ent,
+              float *lse, float *out2, int64_t ld_out2, const octo_grpo_tail *gt, void *grad_h, int64_t ld_gh,
+              int gh_dtype, void *grad_w, int gw_dtype, void *ws, size_t ws_bytes, void *stream) {
+  Common cm;
+  int rc = check_common(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, n_max, d, V, flags, inv_T,
+                        pre, post, use_tanh, cm);
+  if (rc) return rc;
+  OCTO_CHECK_ARG(gt != nullptr, "head_step_grpo: null grpo");
+  OCTO_CHECK_ARG(gt->n_tokens >= 0, "head_step_grpo: n_tokens < 0");
+  OCTO_CHECK_ARG(gt->g && gt->adv && gt->mask, "head_step_grpo: null g, adv or mask");
+  OCTO_CHECK_ARG(lse != nullptr, "head_step_grpo: null lse");
+  OCTO_CHECK_ARG(!out2 || ld_out2 >= 2, "head_step_grpo: ld_out2 < 2");
+  if (grad_h) {
+    OCTO_CHECK_ARG(gh_dtype == OCTO_BF16 || gh_dtype == OCTO_F16 || gh_dtype == OCTO_F32, "head_step_grpo: grad_h dtype");
+    OCTO_CHECK_ARG(ld_gh >= d, "head_step_grpo: ld_gh < d");
+  }
+  if (grad_w) {
+    if (cm.fp8) return octo_fail(OCTO_EUNSUPPORTED, "head_step_grpo: grad_w of fp8 weights");
+    OCTO_CHECK_ARG(gw_dtype == OCTO_BF16 || gw_dtype == OCTO_F16 || gw_dtype == OCTO_F32, "head_step_grpo: grad_w dtype");
+  }
+  const bool need_gh = grad_h != nullptr, need_gw = grad_w != nullptr;
+  if (n_max == 0) return OCTO_OK;
+  if (cm.dt == OCTO_F32) {  // fp32: the forward, then the backward
+    if (!ws || ws_bytes < step_fallback_bytes(n_max, d, V, w_dtype, need_gw, cm.gather))
+      return octo_fail(OCTO_EWORKSPACE, "head_step_grpo: workspace %zu < %zu bytes", ws ? ws_bytes : (size_t)0,
+                       step_fallback_bytes(n_max, d, V, w_dtype, need_gw, cm.gather));
+    rc = head_fwd(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
+                  pre, post, use_tanh, logp, ent, lse, out2, ld_out2, gt, ws, ws_bytes, stream);
+    if (rc || (!need_gh && !need_gw)) return rc;
+    return octo_head_bwd(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags,
+                         inv_T, pre, post, use_tanh, lse, gt->g, grad_h, ld_gh, gh_dtype, grad_w, gw_dtype, ws,
+                         ws_bytes, stream);
+  }
+  StepLayout L;
+  if (!ws || !step_plan_for(n_max, d, V, w_dtype, need_gh, need_gw, cm.gather, ws_bytes, L)) {
+    StepLayout Lmin;
+    size_t least = 0;
+    for (int q = kBudgetQMin; q <= kBudgetQMax && !least; ++q)
+      if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, cm.gather, staging_candidate(q), Lmin)) least = Lmin.total;
+    return octo_fail(OCTO_EWORKSPACE, "head_step_grpo: workspace %zu bytes, below the smallest plan's %zu%s",
+                     ws ? ws_bytes : (size_t)0, least,
+                     cm.gather ? " (hidden of 2 GiB or more through idx: query with OCTO_WS_GATHER)" : "");
+  }
+  hipStream_t st = (hipStream_t)stream;
+  char *wsb = (char *)ws;
+  f32x4 *part = (f32x4 *)(wsb + L.part);
+  float *z = (float *)(wsb + L.z), *hit = (float *)(wsb + L.hit), *gacc = (float *)(wsb + L.gacc);
+  void *ht = wsb + L.ht, *dz = wsb + L.dz, *wt = wsb + L.wt;
+  const int esz = L.esz;
+
+  rc = launch_grpo_count(gt->mask, gt->n_tokens, z, gt->loss, st);  // Z, and the loss zeroed
+  if (rc) return rc;
+  void *gathered = cm.gather ? wsb + L.rows : nullptr;
+  if (gathered) {
+    rc = launch_rows_gather(h, ldh * cm.hesz, idx, count, n_max, (int64_t)d * cm.hesz, gathered, st);
+    if (rc) return rc;
+  }
+  // the GEMMs' weight operand: W as stored, or fp8 weights widened to bf16 once for every pass
+  Operand Aw = weight_operand(w, ldw, cm, V);
+  if (L.wide_on) {
+    rc = launch_widen_fp8(w, ldw, V, d, wsb + L.wide, st);
+    if (rc) return rc;
+    Aw = weight_operand(wsb + L.wide, d, cm, V);
+    Aw.ld = (int64_t)d * 2;
+  }
+  if (L.wt_on) {  // W^T [d, V_pad] in the staged type, zero past V
+    rc = launch_transpose(Aw.base, Aw.ld / esz, cm.dt, nullptr, nullptr, nullptr, 0, V, L.V_pad, d, wt, L.V_pad,
+                          cm.dt, st);
+    if (rc) return rc;
+  }
+
+  for (int64_t p = 0; p < L.passes; ++p) {
+    const int64_t r0 = p * L.P;
+    const int64_t rows = (n_max - r0) < L.P ? (n_max - r0) : L.P;
+    const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm, gathered, d);
+
+    // logits once: statistics per (row, vocabulary tile) and the tile-relative exponentials
+    StatsArgs e;
+    e.part = part;
+    e.mtiles = L.mtiles;
+    e.v0 = 0;
+    e.V = V;
+    e.wscale = w_scale;
+    e.c = cm.c;
+    e.pre = cm.pre;
+    e.ex = dz;
+    e.ldx = L.V_pad;
+    {
+      TimedLaunch t("gemm_stats", st);
+      rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, Aw, Bh, shape(V, rows, d, kGroupM, 2, count, r0), e, st);
+    }
+    if (rc) return rc;
+
+    // the pass's outputs, row state, GRPO weight g (the loss summed) and dz at each label
+    MergeArgs m = merge_args(part, L.mtiles, h, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max,
+                             d, V, flags, inv_T, pre, post, use_tanh, logp, ent, lse, out2, ld_out2, gt, z);
+    m.row_off = r0;
+    m.rows = rows;
+    m.c = cm.c;
+    m.gmul = cm.gmul;
+    m.hit = hit;
+    rc = launch_merge(m, st);
+    if (rc) return rc;
+
+    DzScaleArgs sa;
+    sa.dz = dz;
+    sa.ld = L.V_pad;
+    sa.V_pad = L.V_pad;
+    sa.dtype = cm.dt;
+    sa.part = part;
+    sa.mtiles = L.mtiles;
+    sa.lse = lse;
+    sa.lse_pair = (flags & OCTO_LSE_PAIR) != 0;
+    sa.g = gt->g;
+    sa.gmul = cm.gmul;
+    sa.wscale = cm.fp8 ? w_scale : nullptr;
+    sa.labels = labels;
+    sa.label_idx = (flags & OCTO_ROWS_VIA_IDX) ? idx : nullptr;
+    sa.hit = hit;
+    sa.count = count;
+    sa.r0 = r0;
+    sa.rows = rows;
+    sa.n_max = n_max;
+    sa.V = V;
+    {
+      TimedLaunch t("dz_scale", st);
+      rc = launch_dz_scale(sa, st);
+    }
+    if (rc) return rc;
+
+    // grad_h[rows] = dz . W   (K = V, or V_pad through the staged W^T)
+    const Operand A2 = plain_operand(dz, L.V_pad * esz, rows, count, r0);
+    const Operand B2 = L.wt_on ? plain_operand(wt, L.V_pad * esz, d, nullptr, 0) : plain_operand(Aw.base, Aw.ld, d, nullptr, 0);
+    const GemmShape s2 = shape(rows, d, L.wt_on ? L.V_pad : V, kGroupM, 1, count, r0);
+    StoreArgs o2;
+    o2.C = (char *)grad_h + r0 * ld_gh * elem_bytes(gh_dtype);
+    o2.ldc = ld_gh;
+    o2.dtype = gh_dtype;
+    // grad_W (+)= dz^T . h   (K = this pass's rows)
+    const Operand A3 = plain_operand(dz, L.V_pad * esz, L.P, nullptr, 0);
+    const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
+    if (need_gw) {  // h^T [d, P] of the pass's rows, zero past the count
+      const int64_t rows_pad = round_up(rows, TN);
+      rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, nullptr,
+                            idx ? idx + r0 : nullptr, count, r0, rows, rows_pad, d, ht, L.P, cm.dt, st);
+      if (rc) return rc;
+    }
+    if (need_gh && need_gw) {  // both in one launch
+      const StoreArgs o3 = grad_w_store(d, r0, rows, p, L.passes, L.gacc_on, gacc, grad_w, gw_dtype, flags, count);
+      TimedLaunch t("gemm_grads", st);
+      rc = launch_gemm_grads(cm.dt, A2, B2, s2, o2, !L.wt_on, A3, B3, shape(V, d, rows, kGroupM, 3, count, r0), o3,
+                             st);
+    } else if (need_gh) {
+      TimedLaunch t("gemm_store_grad_h", st);
+      rc = launch_gemm_store(cm.dt, A2, B2, s2, o2, st, L.wt_on ? KM_NONE : KM_B);
+    } else {
+      rc = grad_w_pass(cm.dt, A3, KM_A, B3, V, d, r0, rows, p, L.passes, L.gacc_on, gacc, grad_w, gw_dtype, flags,
+                       count, st);
+    }
+    if (rc) return rc;
+  }
+  return OCTO_OK;
 }
 
 // ---- the allocation-free forward (octo_head_fwd_noalloc) ----------------------------------------
@@ -595,7 +920,17 @@ int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flag
   OCTO_CHECK_ARG(bytes != nullptr, "workspace_bytes: null pointer");
   OCTO_CHECK_ARG(n_max >= 0 && d > 0 && V > 0, "workspace_bytes: bad sizes");
   OCTO_CHECK_ARG(w_dtype >= OCTO_BF16 && w_dtype <= OCTO_FP8E4M3, "workspace_bytes: dtype %d", w_dtype);
-  if (flags & OCTO_WS_BACKWARD) {
+  if (flags & OCTO_WS_STEP) {
+    const bool need_gw = !(flags & OCTO_WS_NO_GRADW), gather = flags & OCTO_WS_GATHER;
+    StepLayout L;
+    if (step_plan(n_max, d, V, w_dtype, true, need_gw, gather, kStagingBudget, L)) {
+      *bytes = L.total;
+    } else {
+      if (elem_bytes(staged_dtype(w_dtype)) == 2)
+        return octo_fail(OCTO_EINVAL, "workspace_bytes: no step plan for V=%d in the default budget", V);
+      *bytes = step_fallback_bytes(n_max, d, V, w_dtype, need_gw, gather);
+    }
+  } else if (flags & OCTO_WS_BACKWARD) {
     BwdLayout L;
     if (!bwd_plan(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW), flags & OCTO_WS_GATHER, kStagingBudget, L))
       return octo_fail(OCTO_EINVAL, "workspace_bytes: no backward plan for d=%d", d);
@@ -610,6 +945,16 @@ int octo_head_bwd_plan(int64_t n_max, int d, int V, int w_dtype, int flags, size
   OCTO_CHECK_ARG(plan != nullptr, "bwd_plan: null pointer");
   OCTO_CHECK_ARG(n_max >= 0 && d > 0 && V > 0, "bwd_plan: bad sizes");
   OCTO_CHECK_ARG(w_dtype >= OCTO_BF16 && w_dtype <= OCTO_FP8E4M3, "bwd_plan: dtype %d", w_dtype);
+  if ((flags & OCTO_WS_STEP) && elem_bytes(staged_dtype(w_dtype)) == 2) {
+    StepLayout S;
+    if (!step_plan_for(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW), flags & OCTO_WS_GATHER, ws_bytes, S))
+      return octo_fail(OCTO_EWORKSPACE, "bwd_plan: no step plan fits %zu bytes", ws_bytes);
+    plan[0] = S.P;
+    plan[1] = S.passes;
+    plan[2] = S.V_pad;
+    plan[3] = 1;
+    return OCTO_OK;
+  }
   BwdLayout L;
   if (!bwd_plan_for(n_max, d, V, w_dtype, true, !(flags & OCTO_WS_NO_GRADW), flags & OCTO_WS_GATHER, ws_bytes, L))
     return octo_fail(OCTO_EWORKSPACE, "bwd_plan: no plan fits %zu bytes", ws_bytes);
@@ -637,6 +982,17 @@ int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, 
   OCTO_CHECK_ARG(grpo != nullptr, "head_fwd_grpo: null grpo");
   return head_fwd(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
                   pre, post, use_tanh, logp, ent, lse, out2, ld_out2, grpo, ws, ws_bytes, stream);
+}
+
+int octo_head_step_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw,
+                        int w_dtype, const float *w_scale, const int64_t *labels, const int64_t *idx,
+                        const int32_t *count, int64_t n_max, int d, int V, int flags, float inv_T, float pre,
+                        float post, int use_tanh, float *logp, float *ent, float *lse, float *out2, int64_t ld_out2,
+                        const octo_grpo_tail *grpo, void *grad_h, int64_t ld_gh, int gh_dtype, void *grad_w,
+                        int gw_dtype, void *ws, size_t ws_bytes, void *stream) {
+  return head_step(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
+                   pre, post, use_tanh, logp, ent, lse, out2, ld_out2, grpo, grad_h, ld_gh, gh_dtype, grad_w,
+                   gw_dtype, ws, ws_bytes, stream);
 }
 
 int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
@@ -690,7 +1046,6 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
   for (int64_t p = 0; p < L.passes; ++p) {
     const int64_t r0 = p * L.P;
     const int64_t rows = (n_max - r0) < L.P ? (n_max - r0) : L.P;
-    const bool last_pass = p + 1 == L.passes;
 
     const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm, gathered, d);
     DzArgs e;
@@ -798,40 +1153,8 @@ int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const
         const Operand A3 = kmajor ? plain_operand(dza, L.Vc * esz, L.P, nullptr, 0)
                                   : plain_operand(dzb, L.P * esz, L.Vc, nullptr, 0);
         const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
-        const GemmShape s3 = shape(vc, d, rows, kGroupM, 3, count, r0);
-        StoreArgs o;
-        const bool acc_out = flags & OCTO_GRADW_ACCUMULATE;
-        if (L.gacc_on && !last_pass && !count) {  // fp32 partial sums of the passes so far
-          o.C = gacc + v0 * d;
-          o.addend = nullptr;
-          o.dtype = OCTO_F32;
-          o.accumulate = p > 0 ? 1 : 0;
-        } else {
-          o.C = (char *)grad_w + v0 * d * elem_bytes(gw_dtype);
-          o.addend = (L.gacc_on && p > 0) ? gacc + v0 * d : nullptr;
-          o.dtype = gw_dtype;
-          o.accumulate = (acc_out || (!L.gacc_on && p > 0)) ? 1 : 0;
-        }
-        if (count && p > 0) {  // passes at or past the device row count store nothing
-          o.pass_count = count;
-          o.pass_r0 = r0;
-          o.pass_end = r0 + rows;
-        }
-        if (count && L.gacc_on && !last_pass) {
-          // the device count decides: the pass that reaches it stores grad_W (adding the earlier passes' partials),
-          // an earlier one stores its fp32 partials
-          o.pass_count = count;
-          o.pass_r0 = r0;
-          o.pass_end = r0 + rows;
-          o.part = gacc + v0 * d;
-          o.part_accumulate = p > 0 ? 1 : 0;
-        }
-        o.ldc = d;
-        o.ld_add = d;
-        {
-          TimedLaunch t("gemm_store_grad_w", st);
-          rc = launch_gemm_store(cm.dt, A3, B3, s3, o, st, kmajor);
-        }
+        rc = grad_w_pass(cm.dt, A3, kmajor, B3, vc, d, r0, rows, p, L.passes, L.gacc_on, gacc + v0 * d,
+                         (char *)grad_w + v0 * d * elem_bytes(gw_dtype), gw_dtype, flags, count, st);
         if (rc) return rc;
       }
     }

@@ -95,16 +95,18 @@ constexpr int kMergeRows = 16;
 __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
   __shared__ float loss_part[kMergeRows];
   const int wave = threadIdx.x >> 6;
-  const int64_t r = (int64_t)blockIdx.x * kMergeRows + wave;
+  const int64_t rl = (int64_t)blockIdx.x * kMergeRows + wave;  // row of this launch
+  const int64_t r = a.row_off + rl;                              // compact row
   const int lane = threadIdx.x & 63;
   const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
+  const int64_t rows = a.rows < 0 ? a.n_max : a.rows;
   float lt = 0.f;
-  if (r < cnt) {
+  if (rl < rows && r < cnt) {
     const int64_t hrow = a.idx ? a.idx[r] : r;
     const int64_t y = a.labels[(a.flags & OCTO_ROWS_VIA_IDX) ? hrow : r];
 
     Stat3 st{-INFINITY, 0.f, 0.f};
-    const f32x4 *pr = a.part + r * a.mtiles;
+    const f32x4 *pr = a.part + rl * a.mtiles;
     for (int64_t mt = lane; mt < a.mtiles; mt += 64) {
       const f32x4 p = pr[mt];
       st = stat_merge(st, Stat3{p[0], p[1], p[2]});
@@ -116,6 +118,7 @@ __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
     if (y_ok) dot = row_dot(a.h, a.h_dtype, hrow * a.ldh, a.w, a.w_dtype, y * a.ldw, a.d, lane);
     dot = wave_sum(dot);
     if (lane == 0) {
+      const float raw = dot;  // h . W_y as stored (fp8: before the row scale)
       if (a.w_dtype == OCTO_FP8E4M3 && y_ok) dot *= a.wscale[y];
       const float zt = a.use_tanh ? a.post * tanhf(a.pre * dot) : a.post * a.pre * dot;
       const float sy = zt * a.inv_T;
@@ -144,8 +147,26 @@ __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
           grpo_token(lp, a.gprox ? a.gprox + hrow : nullptr, a.gold ? a.gold + hrow : nullptr, a.gadv[hrow],
                      a.eps_lo, a.eps_hi, a.reject_upper, 1.f / a.z[0], gt, lt);
         a.g[r] = gt;
+        if (a.hit) {  // launch_hit's formula, from the same target logit and row state
+          float v = 0.f;
+          if (y_ok) {
+            const bool f8 = a.w_dtype == OCTO_FP8E4M3;
+            const float x = f8 ? raw * a.wscale[y] : raw;
+            const float gs = gt * a.gmul;
+            if (a.use_tanh) {
+              const float th = ftanh(a.pre * x);
+              v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(th, a.c, -st.m) - l2S), gs) * (1.f - th * th);
+            } else {
+              v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(x, a.c, -st.m) - l2S), gs);
+            }
+            if (f8) v *= a.wscale[y];
+          }
+          a.hit[rl] = v;
+        }
       }
     }
+  } else if (a.hit && lane == 0 && rl < rows) {
+    a.hit[rl] = 0.f;
   }
   if (!a.loss) return;  // uniform across the workgroup: no barrier below is skipped by part of it
   if (lane == 0) loss_part[wave] = lt;
@@ -159,8 +180,9 @@ __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
 }
 
 int launch_merge(const MergeArgs &a, hipStream_t st) {
-  if (a.n_max == 0) return OCTO_OK;
-  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)cdiv(a.n_max, kMergeRows)), dim3(64 * kMergeRows), 0, st, a);
+  const int64_t rows = a.rows < 0 ? a.n_max : a.rows;
+  if (rows == 0) return OCTO_OK;
+  hipLaunchKernelGGL(merge_kernel, dim3((unsigned)cdiv(rows, kMergeRows)), dim3(64 * kMergeRows), 0, st, a);
   OCTO_CHECK_LAUNCH("merge");
   return OCTO_OK;
 }
@@ -204,6 +226,71 @@ int launch_hit(const HitArgs &a, hipStream_t st) {
   if (a.rows == 0) return OCTO_OK;
   hipLaunchKernelGGL(hit_kernel, dim3((unsigned)cdiv(a.rows, 4)), dim3(256), 0, st, a);
   OCTO_CHECK_LAUNCH("hit");
+  return OCTO_OK;
+}
+
+// ---- dz from the stored exponentials (the fused step) ---------------------------------------------------
+// One workgroup per (row, 8,192 columns): 4 x 16 bytes per thread, loaded together, scaled by the row's factor for
+// their vocabulary tile (8 columns never straddle a 256-column tile), the label entry replaced, stored back. The
+// row's state is uniform over the workgroup (scalar loads). Non-temporal: the rows are read back only by the
+// gradient GEMMs, after the rest of the pass's [rows, V] has streamed through.
+constexpr int kScaleChunks = 4;  // 16-byte chunks per thread
+
+__global__ __launch_bounds__(256) void dz_scale_kernel(DzScaleArgs a) {
+  const int64_t i = blockIdx.y;  // row of the pass
+  const int64_t r = a.r0 + i;
+  const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
+  if (r >= cnt) return;
+  float m2, l2s;
+  row_state(a.lse, a.lse_pair, r, m2, l2s);
+  const float ngs = -(a.g[r] * a.gmul);
+  const int64_t y = a.labels[a.label_idx ? a.label_idx[r] : r];
+  const bool f16 = a.dtype == OCTO_F16;
+  const f32x4 *pr = a.part + i * a.mtiles;
+  char *row = (char *)a.dz + i * a.ld * 2;
+  const int64_t chunk0 = (int64_t)blockIdx.x * (256 * kScaleChunks) + threadIdx.x;
+  i32x4 v[kScaleChunks];
+#pragma unroll
+  for (int k = 0; k < kScaleChunks; ++k) {
+    const int64_t c0 = (chunk0 + 256 * k) * 8;
+    if (c0 < a.V_pad) v[k] = __builtin_nontemporal_load((const i32x4 *)(row + c0 * 2));
+  }
+#pragma unroll
+  for (int k = 0; k < kScaleChunks; ++k) {
+    const int64_t c0 = (chunk0 + 256 * k) * 8;
+    if (c0 >= a.V_pad) continue;
+    const float s = ngs * fexp2(pr[c0 >> 8][0] - m2 - l2s);
+    float x[8];
+    unpack8(v[k], true, x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] *= s;
+    if (a.wscale) {  // fp8 weights: each column's row scale (the chain rule through z = scale x raw product)
+      if (c0 + 8 <= a.V) {  // two aligned 16-byte loads (c0 is a multiple of 8, the scales 16-byte aligned)
+        const f32x4 s0 = *(const f32x4 *)(a.wscale + c0), s1 = *(const f32x4 *)(a.wscale + c0 + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[e] *= s0[e];
+          x[e + 4] *= s1[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= (c0 + e < a.V) ? a.wscale[c0 + e] : 0.f;
+      }
+    }
+    if (y >= c0 && y < c0 + 8 && y < a.V) x[y - c0] = a.hit[i];
+    __builtin_nontemporal_store(pack8(x, f16), (i32x4 *)(row + c0 * 2));
+  }
+}
+
+int launch_dz_scale(const DzScaleArgs &a, hipStream_t st) {
+  if (a.rows == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(a.dtype == OCTO_BF16 || a.dtype == OCTO_F16, "dz_scale: dtype %d", a.dtype);
+  OCTO_CHECK_ARG(a.V_pad % 8 == 0 && a.ld % 8 == 0 && a.ld >= a.V_pad && ((uintptr_t)a.dz) % 16 == 0,
+                 "dz_scale: rows of 16-byte chunks");
+  OCTO_CHECK_ARG(a.rows <= 65535, "dz_scale: %lld rows in one launch", (long long)a.rows);
+  const unsigned bx = (unsigned)cdiv(a.V_pad / 8, 256 * kScaleChunks);
+  hipLaunchKernelGGL(dz_scale_kernel, dim3(bx, (unsigned)a.rows), dim3(256), 0, st, a);
+  OCTO_CHECK_LAUNCH("dz_scale");
   return OCTO_OK;
 }
 

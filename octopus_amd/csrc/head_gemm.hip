@@ -376,6 +376,48 @@ __device__ __forceinline__ void dz_stage(const typename L::V (&acc)[L::NI][L::NJ
   }
 }
 
+// The stats epilogue's tile-relative exponentials (StatsArgs::ex) into the LDS staging tile, laid out as dz_stage
+// lays out dz: ex = exp2(c t - m_tile) x post'(z), zero past V and past the tile's valid tokens. acc holds t's
+// argument after pre_transform (z, or tanh(pre z) under the softcap, whose derivative is 1 - t^2); m_tile of each token
+// column is the larger of its two waves' maxima in red, as stat_merge keeps it in part. (fp8 row scales are applied
+// by launch_dz_scale: in f16 here they would push the values into its subnormal range.)
+template <class L, typename P2, bool TANH, bool EDGE>
+__device__ __forceinline__ void ex_stage(const typename L::V (&acc)[L::NI][L::NJ], const StatsArgs &e, int64_t ma,
+                                         int64_t nvalid, int wm, int wn, int lane, const lds_f32x4 *red,
+                                         lds_char *tile) {
+  float mt[L::NJ];
+  int tt[L::NJ], sw[L::NJ];
+#pragma unroll
+  for (int j = 0; j < L::NJ; ++j) {
+    tt[j] = L::col(wn, j, lane);
+    const f32x4 a = red[tt[j]], b = red[256 + tt[j]];
+    mt[j] = fmaxf(a[0], b[0]);
+    sw[j] = DzSwz<L>::at(tt[j]);
+  }
+#pragma unroll
+  for (int i = 0; i < L::NI; ++i)
+#pragma unroll
+    for (int g4 = 0; g4 < L::NV / 4; ++g4) {
+      const int rl = L::row(wm, i, 4 * g4, lane);  // first of this lane's 4 vocab rows in the tile
+#pragma unroll
+      for (int j = 0; j < L::NJ; ++j) {
+        float x4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float x = acc[i][j][4 * g4 + u];
+          float ev = fexp2(__builtin_fmaf(x, e.c, -mt[j]));
+          if constexpr (TANH) ev *= 1.f - x * x;
+          if constexpr (EDGE) ev = (ma + rl + u < e.V) ? ev : 0.f;
+          x4[u] = tt[j] < nvalid ? ev : 0.f;
+        }
+        i32x2 pk;
+        pk[0] = (int)pack2(x4[0], x4[1], (P2 *)nullptr);
+        pk[1] = (int)pack2(x4[2], x4[3], (P2 *)nullptr);
+        *(lds_i32x2 *)(tile + tt[j] * 512 + (((rl >> 2) ^ sw[j]) << 3)) = pk;
+      }
+    }
+}
+
 // ma: the tile's first vocabulary row; m0: its first dz column (ma - v0)
 template <class L, typename P2, int NT = NTHREADS>
 __device__ __forceinline__ void dz_write(const DzArgs &e, int64_t ma, int64_t m0, int64_t n0, int64_t nvalid,
@@ -520,15 +562,10 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 // as stored, so no W^T is staged), wait for the next stage half-way through the K-step (SPLIT). Same box, 24,576
 // rows, d 2560, V 151,936: grad_W 13.6 against 14.1 ms and grad_h 13.9 against 14.4 ms for the 4-wave form; grad_h
 // reading W K-major without SPLIT 15.0 against 14.15 ms.
+// One tile (mt, nt) of the 8-wave gradient GEMM; OT < 0: the output type is e.dtype, chosen after the mainloop.
 template <int DT, int OT, int KM>
-__global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_store8_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
-  static_assert(ring5_ok(DT), "16-bit operands");
-  __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
-  lds_char *smem = (lds_char *)smem_;
-  int mt, nt;
-  if (!tile_of(s, mt, nt)) return;
-  const int which = pass_store(e);
-  if (which == 0) return;
+__device__ __forceinline__ void store8_tile(const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
+                                            int mt, int nt, int which, lds_char *smem) {
   const int64_t m0 = (int64_t)mt * TM, n0 = (int64_t)nt * TN;
   int64_t mvalid = s.M - m0, nvalid = s.N - n0, K_eff = s.K;
   if (s.count_on == 1) mvalid = dev_count(s.count, s.count_off + m0, mvalid);
@@ -538,16 +575,66 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   if constexpr (KM == KM_A) mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
   else if constexpr (KM == KM_B) mainloop_ring5<DT, OpRowsN<8, 128>, OpColsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
   else mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
-  store_pass<Acc16N<4>, typename Elem<OT>::T>(acc, e, which, m0, n0, mvalid, nvalid);
+  if constexpr (OT >= 0) {
+    store_pass<Acc16N<4>, typename Elem<OT>::T>(acc, e, which, m0, n0, mvalid, nvalid);
+  } else {
+    switch (e.dtype) {
+      case OCTO_BF16: store_pass<Acc16N<4>, __bf16>(acc, e, which, m0, n0, mvalid, nvalid); break;
+      case OCTO_F16: store_pass<Acc16N<4>, _Float16>(acc, e, which, m0, n0, mvalid, nvalid); break;
+      default: store_pass<Acc16N<4>, float>(acc, e, which, m0, n0, mvalid, nvalid); break;
+    }
+  }
+}
+
+template <int DT, int OT, int KM>
+__global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_store8_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
+  static_assert(ring5_ok(DT), "16-bit operands");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
+  lds_char *smem = (lds_char *)smem_;
+  int mt, nt;
+  if (!tile_of(s, mt, nt)) return;
+  const int which = pass_store(e);
+  if (which == 0) return;
+  store8_tile<DT, OT, KM>(A, B, s, e, mt, nt, which, smem);
+}
+
+// Both gradient GEMMs of one row pass in one launch (the fused step): blocks [0, nh) run grad_h = dz . W (nh = its
+// tile grid, a multiple of 8, so block b still runs on XCD b % 8 in either part), the rest grad_W = dz^T . h. The
+// grad_h tiles, K = V long, are dispatched first; grad_W's, K = the pass's rows, fill the CUs its grid leaves idle
+// and the rest of its last round (a pass of 6,656 rows at d 2560 has 260 grad_h tiles: alone, a second round for 4
+// of them). KMH: grad_h reads W K-major as stored (KM_B) or a staged W^T (KM_NONE); grad_W reads dz K-major.
+template <int DT, int KMH>
+__global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_grads8_kernel(Operand Ah, Operand Bh, GemmShape sh, StoreArgs eh, Operand Aw, Operand Bw, GemmShape sw, StoreArgs ew, unsigned nh) {
+  static_assert(ring5_ok(DT), "16-bit operands");
+  __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
+  lds_char *smem = (lds_char *)smem_;
+  const unsigned b = blockIdx.x;
+  int64_t mtiles, ntiles;
+  int mt, nt;
+  if (b < nh) {
+    bounded_tiles(sh, mtiles, ntiles);
+    if (!tile_at(sh, (int)(b & 7), (int64_t)(b >> 3), mtiles, ntiles, mt, nt)) return;
+    store8_tile<DT, -1, KMH>(Ah, Bh, sh, eh, mt, nt, 1, smem);
+  } else {
+    const unsigned c = b - nh;
+    bounded_tiles(sw, mtiles, ntiles);
+    if (!tile_at(sw, (int)(c & 7), (int64_t)(c >> 3), mtiles, ntiles, mt, nt)) return;
+    const int which = pass_store(ew);
+    if (which == 0) return;
+    store8_tile<DT, -1, KM_A>(Aw, Bw, sw, ew, mt, nt, which, smem);
+  }
 }
 
 // The logits-shaped GEMMs on the 8-wave loop (16-bit operands): 512 threads, two waves per SIMD, each 128 x 64, with
 // the split stage barrier. Same box, 24,576 rows, d 2560, V 151,936 (against the 4-wave loop): gemm_stats 14.3
 // against 15.1 ms, gemm_dz 15.3 against 16.5 ms; without the split barrier gemm_dz was 0.4 ms slower than the 4-wave
 // loop.
-template <int DT, bool A_FP8, bool TANH>
+// EX: also store the tile-relative exponentials (StatsArgs::ex) through the LDS staging tile, as gemm_dz8 stores dz;
+// the per-wave statistics then sit past that tile.
+template <int DT, bool A_FP8, bool TANH, bool EX>
 __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_stats8_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
   static_assert(ring5_ok(DT), "16-bit operands");
+  static_assert(256 * 512 + 512 * 16 <= SMEM_RING5, "staging tile and statistics fit the ring's LDS");
   typedef Acc16N<4> L;
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
   lds_char *smem = (lds_char *)smem_;
@@ -557,7 +644,7 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   const int64_t nvalid = min(dev_count(s.count, s.count_off + n0, s.N - n0), (int64_t)TN);  // this tile's tokens
   if (nvalid <= 0) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = L::wm(w), wn = L::wn(w);
-  lds_f32x4 *red = (lds_f32x4 *)smem;
+  lds_f32x4 *red = (lds_f32x4 *)(smem + (EX ? 256 * 512 : 0));
   f32x4 acc[8][4];
   mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, s.K, smem, acc);
   const int64_t ma = e.v0 + m0;  // first vocabulary row of the tile
@@ -565,6 +652,10 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   if (ma + TM > e.V) stats_cols<L, true>(acc, ma, wm, wn, lane, e.V, e.c, red);
   else stats_cols<L, false>(acc, ma, wm, wn, lane, e.V, e.c, red);
   __syncthreads();
+  if constexpr (EX) {  // f16 whatever the MFMA type: the values lie in [0, 1]
+    if (ma + TM > e.V) ex_stage<L, f16x2_t, TANH, true>(acc, e, ma, nvalid, wm, wn, lane, red, smem);
+    else ex_stage<L, f16x2_t, TANH, false>(acc, e, ma, nvalid, wm, wn, lane, red, smem);
+  }
   const int t = threadIdx.x;
   if (t < nvalid) {
     const f32x4 a = red[t], b = red[256 + t];
@@ -573,6 +664,11 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
     f32x4 o;
     o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
     e.part[(n0 + t) * e.mtiles + e.v0 / TM + mt] = o;
+  }
+  if constexpr (EX) {
+    __syncthreads();  // staging tile written
+    lds_tile_to_global<2 * NTHREADS>(smem, (char *)e.ex + (n0 * e.ldx + ma) * 2, e.ldx * 2,
+                                     [](int row) { return DzSwz<L>::at(row); });
   }
 }
 
@@ -608,10 +704,15 @@ static inline dim3 grid_of(const GemmShape &s) { return dim3((unsigned)tile_grid
 
 template <int DT, bool F8, bool TH>
 static int go_stats(const Operand &A, const Operand &B, const GemmShape &s, const StatsArgs &e, hipStream_t st) {
-  if constexpr (ring5_ok(DT))
-    hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
-  else
+  if constexpr (ring5_ok(DT)) {
+    if (e.ex)
+      hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH, true>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
+    else
+      hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH, false>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
+  } else {
+    if (e.ex) return octo_fail(OCTO_EUNSUPPORTED, "gemm_stats: exponentials of fp32 operands");
     hipLaunchKernelGGL((gemm_stats_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);
+  }
   OCTO_CHECK_LAUNCH("gemm_stats");
   return OCTO_OK;
 }
@@ -675,10 +776,40 @@ static int go_store(const Operand &A, const Operand &B, const GemmShape &s, cons
   return OCTO_OK;
 }
 
+template <int DT>
+static int go_grads(const Operand &Ah, const Operand &Bh, const GemmShape &sh, const StoreArgs &eh, bool wh_kmajor,
+                    const Operand &Aw, const Operand &Bw, const GemmShape &sw, const StoreArgs &ew, hipStream_t st) {
+  const int64_t nh = tile_grid(sh.mtiles, sh.ntiles), nw = tile_grid(sw.mtiles, sw.ntiles);
+  if (nh + nw > 0x7fffffffLL) return octo_fail(OCTO_EINVAL, "gemm_grads: %lld tiles", (long long)(nh + nw));
+  const dim3 grid((unsigned)(nh + nw));
+  if (wh_kmajor)
+    hipLaunchKernelGGL((gemm_grads8_kernel<DT, KM_B>), grid, dim3(2 * NTHREADS), 0, st, Ah, Bh, sh, eh, Aw, Bw, sw, ew,
+                       (unsigned)nh);
+  else
+    hipLaunchKernelGGL((gemm_grads8_kernel<DT, KM_NONE>), grid, dim3(2 * NTHREADS), 0, st, Ah, Bh, sh, eh, Aw, Bw, sw,
+                       ew, (unsigned)nh);
+  OCTO_CHECK_LAUNCH("gemm_grads");
+  return OCTO_OK;
+}
+
 // The K-major loader (OpColsN) reads whole 512-byte rows of the tile's 256 columns of a plain (unmapped) matrix,
 // up to the next multiple of 64 K-rows: the caller guarantees those rows exist.
 static bool kmajor_layout_ok(const Operand &X) {
   return !X.map && !(X.ld & 15) && X.ld >= 512 && X.ld <= 0xffffffffLL / 64 && (uintptr_t)X.base % 16 == 0;
+}
+
+int launch_gemm_grads(int dt, const Operand &Ah, const Operand &Bh, const GemmShape &sh, const StoreArgs &eh,
+                      bool wh_kmajor, const Operand &Aw, const Operand &Bw, const GemmShape &sw, const StoreArgs &ew,
+                      hipStream_t st) {
+  if (wh_kmajor && !kmajor_layout_ok(Bh)) return octo_fail(OCTO_EINVAL, "gemm_grads: K-major W layout");
+  if (!kmajor_layout_ok(Aw)) return octo_fail(OCTO_EINVAL, "gemm_grads: K-major dz layout");
+  for (int t : {eh.dtype, ew.dtype})
+    if (t != OCTO_BF16 && t != OCTO_F16 && t != OCTO_F32) return octo_fail(OCTO_EUNSUPPORTED, "gemm_grads: output dtype %d", t);
+  switch (dt) {
+    case OCTO_BF16: return go_grads<OCTO_BF16>(Ah, Bh, sh, eh, wh_kmajor, Aw, Bw, sw, ew, st);
+    case OCTO_F16: return go_grads<OCTO_F16>(Ah, Bh, sh, eh, wh_kmajor, Aw, Bw, sw, ew, st);
+  }
+  return octo_fail(OCTO_EUNSUPPORTED, "gemm_grads: dtype %d", dt);
 }
 
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,

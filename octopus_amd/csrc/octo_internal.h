@@ -11,6 +11,14 @@ struct GemmShape;
 // gemm_stats epilogue arguments: part[row * mtiles + mt] = (m, S, U) of row over vocab tile mt. The GEMM's first
 // operand holds the vocabulary rows v0 .. (a chunk of W starting at row v0, a multiple of 256): its tile mt is vocab
 // tile v0 / 256 + mt.
+//
+// With ex != NULL (16-bit operands) the epilogue also stores, per element, the tile-relative exponential
+//   ex[token][v] = exp2(c t - m_tile) x post'(z)
+// token-major in f16 (columns v of the vocabulary, rows = the GEMM's tokens, ldx elements apart; zero past V and past
+// the tile's valid tokens), where m_tile is the tile's base-2 maximum as part stores it. Once the row's (m2, l2S) and
+// g are known, dz = -g gmul exp2(m_tile - m2 - l2S) ex x (fp8 row scale) (the fused step, launch_dz_scale). f16 for
+// any MFMA type: the values lie in [0, 1], where f16 keeps 11 bits to bf16's 8; what it rounds in its subnormal range,
+// below 2^-14 of the tile's largest probability, errs by at most 2^-25 of it per element.
 struct StatsArgs {
   f32x4 *part;
   int64_t mtiles;
@@ -19,6 +27,8 @@ struct StatsArgs {
   const float *wscale;  // per-vocab-row scale (fp8 weights) or NULL
   float c;              // base-2 softmax scale of the (transformed) logit
   float pre;            // tanh argument scale (softcap)
+  void *ex = nullptr;
+  int64_t ldx = 0;
 };
 
 // The backward's per-row softmax state. Paired (OCTO_LSE_PAIR): lse[2 r] = m2, the row's base-2 maximum exactly as
@@ -107,6 +117,11 @@ int launch_gemm_dz(int dt, bool a_fp8, bool tanh, const Operand &A, const Operan
 enum { KM_NONE = 0, KM_A = 1, KM_B = 2 };
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
                       hipStream_t st, int kmajor = KM_NONE);
+// grad_h (Ah = dz K-contiguous, Bh = W K-major as stored when wh_kmajor, else W^T K-contiguous) and grad_W (Aw = dz
+// K-major, Bw = h^T) of one row pass in one launch, each with its own shape and store (16-bit operands).
+int launch_gemm_grads(int dt, const Operand &Ah, const Operand &Bh, const GemmShape &sh, const StoreArgs &eh,
+                      bool wh_kmajor, const Operand &Aw, const Operand &Bw, const GemmShape &sw, const StoreArgs &ew,
+                      hipStream_t st);
 
 // ---- small kernels (head_aux.hip) ---------------------------------------------------------------
 struct MergeArgs {
@@ -137,8 +152,38 @@ struct MergeArgs {
   float eps_lo, eps_hi, reject_upper;
   const float *z;  // max(1, masked-token count), from launch_grpo_count
   float *g, *loss;
+  // Rows row_off .. row_off + rows of the compact order (rows < 0: all n_max), part indexed from row_off. With hit
+  // != NULL (and g), hit[r - row_off] = the row's dz at its label, g gmul (1 - p_y) post'(z_y) x (fp8 row scale), as
+  // launch_hit computes it; 0 past the count or for a label outside [0, V).
+  int64_t row_off = 0, rows = -1;
+  float c = 0.f, gmul = 0.f;
+  float *hit = nullptr;
 };
 int launch_merge(const MergeArgs &a, hipStream_t st);
+
+// dz of compact rows r0 .. r0 + rows (local row i = r - r0) from the tile-relative exponentials a stats GEMM stored
+// (StatsArgs::ex, f16), in place: dz[i][v] = -g[r] gmul exp2(part[i][v / 256].m - m2 - l2S) ex[i][v] (x wscale[v]
+// for fp8 weights, 0 past V) for v < V_pad, then dz[i][y] = hit[i], in the MFMA type. Rows at or past the count are
+// left as they are (the GEMMs that read dz stop at the count).
+struct DzScaleArgs {
+  void *dz;  // [rows, ld] 16-bit: f16 exponentials in, dz in dtype (bf16 / f16) out
+  int64_t ld, V_pad;
+  int dtype;
+  const f32x4 *part;  // [rows, mtiles], local rows
+  int64_t mtiles;
+  const float *lse;  // (m2, l2S) pairs or lse, global rows
+  int lse_pair;
+  const float *g;  // global rows
+  float gmul;
+  const float *wscale;  // [V] fp8 row scales, or NULL
+  const int64_t *labels;
+  const int64_t *label_idx;  // labels[label_idx[r]] when set
+  const float *hit;          // local rows
+  const int32_t *count;
+  int64_t r0, rows, n_max;
+  int64_t V;
+};
+int launch_dz_scale(const DzScaleArgs &a, hipStream_t st);
 // dst row r (row_bytes, contiguous) = src row idx[r] (ld_src_bytes apart) for r < *count; 16-byte aligned rows
 int launch_rows_gather(const void *src, int64_t ld_src_bytes, const int64_t *idx, const int32_t *count,
                        int64_t n_max, int64_t row_bytes, void *dst, hipStream_t st);

@@ -201,6 +201,73 @@ def _(rows, weight, w_scale, labels, idx, count, lse, g, inv_T, pre, post, use_t
             torch.empty_like(weight) if need_weight else weight.new_empty(0))
 
 
+# Bytes of workspace head_step_grpo gives the library (None: octo_head_workspace_bytes with OCTO_WS_STEP, the plan at
+# a 2 GiB staging budget).
+STEP_WORKSPACE_BYTES: Optional[int] = None
+
+
+@torch.library.custom_op("octohead::head_step_grpo", mutates_args=(), device_types="cuda")
+def head_step_grpo(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Tensor, idx: Optional[Tensor],
+                   count: Optional[Tensor], inv_T: float, pre: float, post: float, use_tanh: bool,
+                   labels_via_idx: bool, scatter: bool, prox: Optional[Tensor], old: Optional[Tensor], adv: Tensor,
+                   mask: Tensor, eps_lo: float, eps_hi: float, reject_upper: float, need_rows: bool,
+                   need_weight: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """The GRPO step of the head in one call (octo_head_step_grpo): head_fwd_grpo's (out, lse, g, loss), then
+    head_bwd's (grad_rows, grad_weight) of that loss, with the logits computed once per row pass. grad_rows is
+    [rows, d] in rows' dtype (compact rows scattered to idx, as head_bwd), grad_weight [V, d] in weight's dtype; an
+    output not asked for is an empty tensor."""
+    rows2, weight2 = _rows2d(rows), _rows2d(weight)
+    labels, idx = _index(labels), _index(idx)
+    n_max = idx.numel() if idx is not None else rows2.shape[0]
+    V, d = weight2.shape
+    dev = rows2.device
+    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | (_lib.OUT_SCATTER if scatter else 0) | _lib.LSE_PAIR
+    out = torch.zeros(rows2.shape[0] if scatter else n_max, 2, dtype=torch.float32, device=dev)
+    lse = torch.zeros(n_max, 2, dtype=torch.float32, device=dev)
+    g = torch.zeros(n_max, dtype=torch.float32, device=dev)
+    loss = torch.zeros((), dtype=torch.float32, device=dev)
+    grad_rows = torch.zeros_like(rows) if need_rows else rows.new_empty(0)
+    grad_w = (torch.zeros_like(weight) if n_max == 0 else torch.empty_like(weight)) if need_weight \
+        else weight.new_empty(0)
+    if n_max == 0:
+        return out, lse, g, loss, grad_rows, grad_w
+    f = lambda t: None if t is None else t.float().contiguous().reshape(-1)  # noqa: E731
+    prox_, old_, adv_, mask_ = f(prox), f(old), f(adv), f(mask)
+    tail = _lib.GrpoTail(_p(prox_), _p(old_), _p(adv_), _p(mask_), adv_.numel(), eps_lo, eps_hi, reject_upper,
+                         _p(g), _p(loss))
+    w_code = _dtype_code(weight2)
+    ws_flags = _lib.WS_STEP | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, idx)
+    nbytes = _lib.workspace_bytes(n_max, d, V, w_code, ws_flags)
+    if STEP_WORKSPACE_BYTES is not None:
+        nbytes = int(STEP_WORKSPACE_BYTES)
+    ws = _workspace(nbytes, rows2)
+    gh = None
+    if need_rows:  # compact-order rows; scattered into grad_rows below
+        gh = grad_rows if idx is None else torch.empty(n_max, d, dtype=rows2.dtype, device=dev)
+    _lib.call("octo_head_step_grpo", _p(rows2), rows2.shape[0], rows2.stride(0), _dtype_code(rows2),
+              _p(weight2), weight2.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
+              n_max, d, V, flags, inv_T, pre, post, int(use_tanh),
+              None, None, _p(lse), _p(out), 2, ctypes.byref(tail),
+              _p(gh), d, _dtype_code(rows2) if need_rows else _lib.F32,
+              _p(grad_w if need_weight else None), _dtype_code(grad_w) if need_weight else _lib.F32,
+              _p(ws), ws.numel(), _stream(rows2))
+    if need_rows and idx is not None:
+        _lib.call("octo_rows_scatter", _p(gh), d, _dtype_code(gh), _p(idx), _p(count), n_max, d,
+                  _p(grad_rows), grad_rows.stride(0), _dtype_code(grad_rows), 0, _stream(rows2))
+    return out, lse, g, loss, grad_rows, grad_w
+
+
+@head_step_grpo.register_fake
+def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, labels_via_idx, scatter, prox, old, adv,
+      mask, eps_lo, eps_hi, reject_upper, need_rows, need_weight):
+    n_max = idx.shape[0] if idx is not None else rows.shape[0]
+    out = rows.new_empty(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32)
+    return (out, rows.new_empty(n_max, 2, dtype=torch.float32), rows.new_empty(n_max, dtype=torch.float32),
+            rows.new_empty((), dtype=torch.float32),
+            torch.empty_like(rows) if need_rows else rows.new_empty(0),
+            torch.empty_like(weight) if need_weight else weight.new_empty(0))
+
+
 def _head_setup(ctx, inputs, output):
     rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, labels_via_idx, scatter = inputs
     # The weight is held by reference, not saved: the backward reads the weight the module holds, as the reference's

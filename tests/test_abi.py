@@ -126,6 +126,65 @@ def test_backward_plan_follows_the_workspace():
         _lib.bwd_plan(n, d, V, _lib.BF16, 0, 1 << 16)
 
 
+def _gradh_rounds(n, d, p_tiles):
+    """grad_h rounds (one long tile per CU, 256 CUs) over the passes of p_tiles x 256 rows covering n rows."""
+    nt, nd = -(-n // 256), -(-d // 256)
+    passes = -(-nt // p_tiles)
+    last = nt - (passes - 1) * p_tiles
+    return (passes - 1) * -(-(p_tiles * nd) // 256) + -(-(last * nd) // 256)
+
+
+@pytest.mark.parametrize("n,d,V,w,flags", [
+    (32768, 2560, 151936, _lib.BF16, 0),                     # 32,768 packed rows, grad_h + grad_W: five passes
+    (65536, 4096, 128256, _lib.BF16, 0),                     # d 4096, V 128,256: eight passes of 8,192
+    (131072, 2560, 151936, _lib.FP8E4M3, _lib.WS_NO_GRADW),  # fp8 weights, grad_h only
+    (32768, 2560, 151937, _lib.F16, _lib.WS_NO_GRADW),       # V not a multiple of 64: W^T staged once
+])
+def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
+    """The fused step's workspace at the default plan: one pass's [rows, V_pad] exponentials (then dz) within the
+    2 GiB staging budget, plus that pass's statistics, h^T and label entries, fp32 grad_W partials over several
+    passes, and once per call the widened fp8 weights or W^T. Rows per pass: the most the budget holds, balanced;
+    without grad_W, the size whose passes take the fewest grad_h rounds."""
+    ws = _lib.workspace_bytes(n, d, V, w, _lib.WS_STEP | flags)
+    P, passes, Vp, one = _lib.bwd_plan(n, d, V, w, _lib.WS_STEP | flags, ws)
+    assert Vp == (V + 255) // 256 * 256 and one == 1
+    assert P % 256 == 0 and P * Vp * 2 <= BUDGET and passes == -(-n // P)
+    need_gw = not flags & _lib.WS_NO_GRADW
+    pmax = min(32768, BUDGET // (Vp * 2) // 256 * 256)
+    if need_gw:
+        assert P == -(-(-(-n // -(-n // pmax))) // 256) * 256
+    else:
+        best = min(_gradh_rounds(n, d, p) for p in range(1, pmax // 256 + 1))
+        assert _gradh_rounds(n, d, P // 256) == best
+        assert all(_gradh_rounds(n, d, p) > best for p in range(P // 256 + 1, pmax // 256 + 1))
+    extra = (P * ((V + 255) // 256) * 16 + P * 4 + (d * P * 2 if need_gw else 0) +
+             (V * d * 4 if need_gw and passes > 1 else 0) + (V * d * 2 if w == _lib.FP8E4M3 else 0) +
+             (d * Vp * 2 if V % 64 or d % 256 else 0))
+    assert P * Vp * 2 <= ws <= P * Vp * 2 + extra + (1 << 20), (ws, extra)
+    if n == 131072:
+        assert (P, passes) == (6400, 21)  # 21 grad_h rounds, against 38 for 27 x 256 rows
+
+
+def test_step_plan_follows_the_workspace_and_fp32_falls_back():
+    n, d, V = 3000, 256, 5120
+    big = _lib.workspace_bytes(n, d, V, _lib.BF16, _lib.WS_STEP)
+    assert _lib.bwd_plan(n, d, V, _lib.BF16, _lib.WS_STEP, big) == (3072, 1, 5120, 1)
+    last = 1
+    for ws in (big, big // 2, big // 4, 8 << 20):
+        P, passes, _, _ = _lib.bwd_plan(n, d, V, _lib.BF16, _lib.WS_STEP, ws)
+        assert P * passes >= n > P * (passes - 1) and passes >= last
+        last = passes
+    assert last > 1
+    # several passes add the fp32 grad_W partials [V, d] (5 MiB here): below them nothing fits
+    with pytest.raises(ValueError):
+        _lib.bwd_plan(n, d, V, _lib.BF16, _lib.WS_STEP, 4 << 20)
+    assert _lib.bwd_plan(n, d, V, _lib.BF16, _lib.WS_STEP | _lib.WS_NO_GRADW, 4 << 20)[1] > 1
+    # fp32 operands run the forward and then the backward in the same workspace
+    f32 = _lib.workspace_bytes(n, d, V, _lib.F32, _lib.WS_STEP)
+    assert f32 == max(_lib.workspace_bytes(n, d, V, _lib.F32, 0),
+                      _lib.workspace_bytes(n, d, V, _lib.F32, _lib.WS_BACKWARD))
+
+
 P = ctypes.c_void_p(256)  # never dereferenced: every call below fails its host-side checks first
 
 

@@ -1,0 +1,259 @@
+"""octo_head_step_grpo: the head's GRPO step (forward, GRPO weight and loss, backward) in one call, the logits
+computed once per row pass.
+
+The forward half runs the forward's own statistics and merge per row, so its outputs (logprob, entropy, row state,
+g) must equal octo_head_fwd_grpo's bit for bit and its loss up to summation order. The backward half builds dz from
+the stored exponentials instead of a recompute, so its gradients must match octo_head_bwd's for the same g to the
+16-bit rounding of dz, and the fp64 oracle (oracle/head.py, with g from oracle/grpo.py on the same logprobs) within
+the relative Frobenius bar 1e-2 (16-bit; 1e-4 for fp32, which runs the forward and the backward). The cases cover
+the plan's branches: one pass and several (fp32 grad_W partials, passes past the device row count), W read K-major
+as stored and W^T staged (V not a multiple of 64), the softcap, fp8 weights (grad_h only), the compacted rows read
+through idx with labels per hidden row, and OCTO_GRADW_ACCUMULATE through the C ABI."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from octopus_amd import _lib, head_op
+from oracle import grpo as ogrpo
+from oracle import head as ohead
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+CODE = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
+EPS = (0.2, 0.28, 5.0)
+
+
+def _rel(a, b):
+    return ((a.double() - b.double()).norm() / b.double().norm()).item()
+
+
+def _batch(N, d, V, dtype, seed, scored_frac=0.6, wscale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(N, d, generator=g)
+    h = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype)
+    W = (torch.randn(V, d, generator=g) * 0.02 * wscale).to(dtype)
+    y = torch.randint(0, V, (N,), generator=g)
+    scored = torch.rand(N, generator=g) < scored_frac
+    mask = (scored & (torch.rand(N, generator=g) < 0.85)).float()
+    adv = torch.randn(N, generator=g)
+    noise = 0.05 * torch.randn(N, generator=g)
+    return h, W, y, scored, mask, adv, noise
+
+
+def _step_ws(n, d, V, code, flags, want):
+    """The largest workspace (shrinking by 10% steps from the queried size) whose step plan satisfies want(plan)."""
+    ws = _lib.workspace_bytes(n, d, V, code, _lib.WS_STEP | flags)
+    while ws > (1 << 16):
+        try:
+            plan = _lib.bwd_plan(n, d, V, code, _lib.WS_STEP | flags, ws)
+        except ValueError:
+            plan = None
+        if plan is not None and want(plan):
+            return ws, plan
+        ws = ws * 9 // 10
+    raise AssertionError("no workspace gives the wanted plan")
+
+
+def _run(h, W, y, scored, mask, adv, old, T, post=(1.0, 1.0, False), w_scale=None, need_w=True, ws=None):
+    """(step outputs, two-call outputs) on the GPU, both through compaction of the scored rows."""
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    idx, count = head_op.compact_rows(scored.to(DEV))
+    sc = None if w_scale is None else w_scale.to(DEV)
+    pre, pst, tanh = post
+    args = (hd, Wd, sc, yd, idx, count, 1.0 / T, pre, pst, tanh, True, True, old.to(DEV), None, adv.to(DEV),
+            mask.to(DEV), *EPS)
+    head_op.STEP_WORKSPACE_BYTES = ws
+    try:
+        step = head_op.head_step_grpo(*args, True, need_w)
+    finally:
+        head_op.STEP_WORKSPACE_BYTES = None
+    out, lse, g, loss = head_op.head_fwd_grpo(*args)
+    grads = head_op.head_bwd(hd, Wd, sc, yd, idx, count, lse, g, 1.0 / T, pre, pst, tanh, True, True, need_w)
+    torch.cuda.synchronize()
+    return idx, count, step, (out, lse, g, loss) + tuple(grads)
+
+
+def _check(h, W32, y, scored, mask, adv, old, T, post, step, two, need_w, bar, vs_two):
+    out_s, lse_s, g_s, loss_s, gh_s, gw_s = step
+    out_t, lse_t, g_t, loss_t, gh_t, gw_t = two
+    # the forward half: the forward's own outputs
+    assert torch.equal(out_s, out_t) and torch.equal(lse_s, lse_t) and torch.equal(g_s, g_t)
+    assert abs(loss_s.item() - loss_t.item()) <= 1e-5 * max(1.0, abs(loss_t.item()))
+    sel = scored.nonzero()[:, 0]
+    n = sel.numel()
+    # g and the loss against the oracle's GRPO on the same logprobs
+    lp = out_s[:, 0].cpu().double().numpy()
+    lo, go = ogrpo.grpo(lp, adv.numpy(), mask.numpy(), prox=old.double().numpy(), eps_lo=EPS[0], eps_hi=EPS[1],
+                        reject_upper=EPS[2])
+    assert np.abs(g_s[:n].cpu().double().numpy() - go[sel.numpy()]).max() <= 1e-6
+    assert abs(loss_s.item() - lo) <= 1e-5 * max(1.0, abs(lo))
+    # the backward half: against the two-call backward and the oracle on the scored rows
+    gh_ref, gw_ref = ohead.head_backward(h[sel], W32, y[sel], T, g_s[:n].cpu(), *post, want_w=need_w)
+    gh_s = gh_s.cpu()
+    assert (gh_s[~scored] == 0).all()
+    assert _rel(gh_s[sel], gh_ref) <= bar
+    assert _rel(gh_s, gh_t.cpu()) <= vs_two
+    if need_w:
+        assert _rel(gw_s.cpu(), gw_ref) <= bar
+        assert _rel(gw_s.cpu(), gw_t.cpu()) <= vs_two
+    assert torch.isfinite(gh_s).all()
+
+
+# (1500, 256, 5120): grad_h reads W K-major as stored; (1500, 136, 3001): V not a multiple of 64, W^T staged
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=["bf16", "f16", "f32"])
+@pytest.mark.parametrize("shape", [(1500, 256, 5120), (1500, 136, 3001)], ids=str)
+def test_step_matches_forward_backward_and_oracle(dtype, shape):
+    N, d, V = shape
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, dtype, seed=91)
+    bar = 1e-4 if dtype == torch.float32 else 1e-2
+    # 16-bit: dz differs from the backward's by the rounding of the f16 exponential (at most 2^-11 relative)
+    vs_two = 1e-6 if dtype == torch.float32 else 4e-3
+    for T, post in ((1.0, (1.0, 1.0, False)), (0.7, (0.5, 2.0, True))):
+        lp0 = head_op.head_fwd(h.to(DEV), W.to(DEV), None, y.to(DEV), None, None, 1.0 / T, *post, False, False)[0]
+        old = lp0[:, 0].cpu() + noise
+        idx, count, step, two = _run(h, W, y, scored, mask, adv, old, T, post)
+        _check(h, W.float(), y, scored, mask, adv, old, T, post, step, two, True, bar, vs_two)
+
+
+def test_step_over_passes_with_grad_w_partials_and_the_device_count():
+    """Three passes of a third of the rows each, with 60% of the rows scored: the first pass holds every scored row
+    and part of the second, and the third starts past the device count, so its grad_W launch stores nothing and the
+    second one's writes grad_W (adding the fp32 partials of the first)."""
+    N, d, V = 6000, 256, 5120
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, torch.bfloat16, seed=92)
+    ws, plan = _step_ws(N, d, V, _lib.BF16, 0, lambda p: p[1] == 3)
+    assert plan[0] == 2048, plan
+    n = int(scored.sum())
+    assert plan[0] < n < 2 * plan[0], (plan, n)
+    lp0 = head_op.head_fwd(h.to(DEV), W.to(DEV), None, y.to(DEV), None, None, 1.0, 1.0, 1.0, False, False, False)[0]
+    old = lp0[:, 0].cpu() + noise
+    idx, count, step, two = _run(h, W, y, scored, mask, adv, old, 1.0, ws=ws)
+    _check(h, W.float(), y, scored, mask, adv, old, 1.0, (1.0, 1.0, False), step, two, True, 1e-2, 4e-3)
+
+
+def test_step_passes_against_the_fp32_reference():
+    """Two passes of 20,224 rows without compaction, grad_W summed in fp32 across them: against the chunked fp32 torch
+    reference on the GPU, and its second pass's rows on their own."""
+    from tests.gpu_reference import head_fp32
+    N, d, V = 40000, 128, 3000
+    gen = torch.Generator(device=DEV).manual_seed(93)
+    h = torch.randn(N, d, device=DEV, generator=gen).to(torch.bfloat16)
+    W = (torch.randn(V, d, device=DEV, generator=gen) * 0.05).to(torch.bfloat16)
+    y = torch.randint(0, V, (N,), device=DEV, generator=gen)
+    adv = torch.randn(N, device=DEV, generator=gen)
+    mask = torch.ones(N, device=DEV)
+    ws, plan = _step_ws(N, d, V, _lib.BF16, 0, lambda p: p[1] == 2)
+    old = head_op.head_fwd(h, W, None, y, None, None, 1 / 0.7, 1.0, 1.0, False, False, False)[0][:, 0] + 0.01
+    head_op.STEP_WORKSPACE_BYTES = ws
+    try:
+        out, lse, g, loss, gh, gw = head_op.head_step_grpo(h, W, None, y, None, None, 1 / 0.7, 1.0, 1.0, False,
+                                                           False, False, old, None, adv, mask, *EPS, True, True)
+    finally:
+        head_op.STEP_WORKSPACE_BYTES = None
+    lp, ent, gr, gwr = head_fp32(h, W.float(), y, 0.7, g=g)
+    assert (out[:, 0] - lp).abs().max() <= 2e-3 and (out[:, 1] - ent).abs().max() <= 2e-3
+    assert _rel(gh, gr) <= 1e-2 and _rel(gw, gwr) <= 1e-2, plan
+    assert _rel(gh[plan[0]:], gr[plan[0]:]) <= 1e-2
+
+
+def test_step_fp8_weights_to_hidden():
+    """fp8 weights with per-row scales, backward to the hidden rows only (no grad_W for fp8): the row scales enter dz
+    in the scaling kernel; against the two-call path and the oracle on the dequantised weights."""
+    from octopus_amd.workloads import quantise_fp8_rows
+    N, d, V = 1200, 512, 8192
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, torch.bfloat16, seed=94, wscale=3.0)
+    Wq, scale = quantise_fp8_rows(W)
+    W32 = Wq.float() * scale[:, None]
+    lp0 = head_op.head_fwd(h.to(DEV), Wq.to(DEV), scale.to(DEV), y.to(DEV), None, None, 1.0, 1.0, 1.0, False, False,
+                           False)[0]
+    old = lp0[:, 0].cpu() + noise
+    with pytest.raises(NotImplementedError):
+        _run(h, Wq, y, scored, mask, adv, old, 1.0, w_scale=scale, need_w=True)
+    idx, count, step, two = _run(h, Wq, y, scored, mask, adv, old, 1.0, w_scale=scale, need_w=False)
+    _check(h, W32, y, scored, mask, adv, old, 1.0, (1.0, 1.0, False), step, two, False, 1e-2, 4e-3)
+
+
+def test_step_extreme_logits():
+    """Every row's hidden vector is e_0, so logit j is W[j, 0]: a 600-nat peak in the last vocabulary tile against
+    logits in [-50, 50] (the other tiles' exponentials scale to exact zeros), and logits near -1,000 at T 0.7 (each
+    tile's maximum far from zero). The gradients against the two-call backward's, whose own agreement with the
+    oracle at these logits is bounded in tests/test_gpu_head.py."""
+    N, d, V = 300, 64, 1000
+    h = torch.zeros(N, d, dtype=torch.bfloat16)
+    h[:, 0] = 1.0
+    gen = torch.Generator().manual_seed(95)
+    base = torch.randint(-50, 51, (V,), generator=gen).to(torch.float32)
+    y = torch.randint(0, V, (N,), generator=gen)
+    y[::2] = 777
+    scored = torch.ones(N, dtype=torch.bool)
+    mask = torch.ones(N)
+    adv = torch.randn(N, generator=gen)
+    for T, col in ((1.0, base.clone().index_fill_(0, torch.tensor([777]), 600.0)), (0.7, base / 10 - 1000.0)):
+        W = torch.zeros(V, d)
+        W[:, 0] = col
+        W = W.to(torch.bfloat16)
+        lp0 = head_op.head_fwd(h.to(DEV), W.to(DEV), None, y.to(DEV), None, None, 1.0 / T, 1.0, 1.0, False, False,
+                               False)[0]
+        old = lp0[:, 0].cpu() + 0.05 * torch.randn(N, generator=gen)
+        idx, count, step, two = _run(h, W, y, scored, mask, adv, old, T)
+        out_s, lse_s, g_s, loss_s, gh_s, gw_s = step
+        out_t, lse_t, g_t, loss_t, gh_t, gw_t = two
+        assert torch.equal(out_s, out_t) and torch.equal(g_s, g_t)
+        assert torch.isfinite(gh_s).all() and torch.isfinite(gw_s).all()
+        # grad_W has no cancellation: the step's dz against the backward's to their 16-bit rounding
+        assert _rel(gw_s, gw_t) <= 4e-3, T
+        # grad_h at logits near -1,000 is a sum of large cancelling terms (the weights share a -1,000 component): the
+        # 16-bit rounding of dz dominates either way (2^-9 relative per element, about 0.7 of the result in the
+        # two-call backward, tests/test_gpu_head.py); the step's extra f16 rounding adds at most a quarter of that
+        gh_ref, _ = ohead.head_backward(h, W, y, T, g_s.cpu(), want_w=False)
+        e_two = _rel(gh_t.cpu(), gh_ref)
+        assert _rel(gh_s.cpu(), gh_ref) <= 1e-2 + 1.5 * e_two, (T, e_two)
+
+
+def test_step_with_no_scored_rows():
+    N, d, V = 512, 64, 1024
+    h, W, y, _, _, adv, noise = _batch(N, d, V, torch.bfloat16, seed=96)
+    scored = torch.zeros(N, dtype=torch.bool)
+    mask = torch.zeros(N)
+    idx, count, step, two = _run(h, W, y, scored, mask, adv, noise, 1.0)
+    out_s, lse_s, g_s, loss_s, gh_s, gw_s = step
+    assert (out_s == 0).all() and loss_s.item() == 0.0
+    assert (gh_s == 0).all() and (gw_s == 0).all()
+
+
+def test_step_grad_w_accumulate_through_the_c_abi():
+    """OCTO_GRADW_ACCUMULATE and fp32 gradient outputs through the C ABI, over two passes: grad_w += the step's
+    grad_W; grad_h in fp32."""
+    n, d, V, T = 3000, 256, 4096, 0.8
+    h, W, y, _, _, adv, noise = _batch(n, d, V, torch.bfloat16, seed=97)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    old = (head_op.head_fwd(hd, Wd, None, yd, None, None, 1.0 / T, 1.0, 1.0, False, False, False)[0][:, 0].cpu()
+           + noise).to(DEV)
+    advd, maskd = adv.to(DEV), torch.ones(n, device=DEV)
+    out = torch.zeros(n, 2, device=DEV)
+    lse = torch.zeros(n, 2, device=DEV)
+    g = torch.zeros(n, device=DEV)
+    loss = torch.zeros((), device=DEV)
+    tail = _lib.GrpoTail(P(old), None, P(advd), P(maskd), n, *EPS, P(g), P(loss))
+    wsb, plan = _step_ws(n, d, V, _lib.BF16, 0, lambda p: p[1] == 2)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    gh = torch.empty(n, d, dtype=torch.float32, device=DEV)
+    base = (torch.randn(V, d, generator=torch.Generator().manual_seed(98)) * 1e-3).to(torch.float32)
+    gw = base.to(DEV).clone()
+    _lib.call("octo_head_step_grpo", P(hd), n, hd.stride(0), _lib.BF16, P(Wd), Wd.stride(0), _lib.BF16, None, P(yd),
+              None, None, n, d, V, _lib.LSE_PAIR | _lib.GRADW_ACCUMULATE, 1.0 / T, 1.0, 1.0, 0, None, None, P(lse),
+              P(out), 2, ctypes.byref(tail), P(gh), d, _lib.F32, P(gw), _lib.F32, P(ws), ws.numel(), st)
+    torch.cuda.synchronize()
+    gh_ref, gw_ref = ohead.head_backward(h, W, y, T, g.cpu())
+    assert _rel(gh.cpu(), gh_ref) <= 1e-2, plan
+    assert _rel(gw.cpu() - base, gw_ref) <= 1e-2, plan
+    # a workspace below the smallest plan is refused before anything is queued
+    with pytest.raises(ValueError):
+        _lib.call("octo_head_step_grpo", P(hd), n, hd.stride(0), _lib.BF16, P(Wd), Wd.stride(0), _lib.BF16, None,
+                  P(yd), None, None, n, d, V, _lib.LSE_PAIR, 1.0 / T, 1.0, 1.0, 0, None, None, P(lse), P(out), 2,
+                  ctypes.byref(tail), P(gh), d, _lib.F32, P(gw), _lib.F32, P(ws), 1 << 20, st)
