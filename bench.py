@@ -238,6 +238,8 @@ def main() -> int:
     ap.add_argument("--two-call", action="store_true",
                     help="run the forward and the backward as two calls (octo_head_fwd_grpo, octo_head_bwd: the "
                          "autograd route, logits recomputed in the backward) instead of the fused step")
+    ap.add_argument("--no-context", action="store_true",
+                    help="skip the two-call route's timing after the fused step's (profiling runs)")
     ap.add_argument("--hipblaslt", action="store_true",
                     help="only time torch.matmul (hipBLASLt) on the four plain GEMMs of the workload's step, "
                          "without any epilogue, for context; then exit")
@@ -352,8 +354,8 @@ def main() -> int:
     # per-phase HIP-event timing on the launch stream (torch's current stream carries every launch): the forward
     # and the backward of the two-call route (for the fused step: context beside its own time)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-    fwd_ms, bwd_ms, reps = [], [], 3
-    if fused:
+    fwd_ms, bwd_ms, reps = [], [], 0 if fused and args.no_context else 3
+    if fused and reps:
         two_call()
         torch.cuda.synchronize()
     for _ in range(reps):
@@ -370,8 +372,8 @@ def main() -> int:
         torch.cuda.synchronize()
         fwd_ms.append(ev[0].elapsed_time(ev[1]))
         bwd_ms.append(ev[2].elapsed_time(ev[3]))
-    fwd_ms = sorted(fwd_ms)[reps // 2]
-    bwd_ms = sorted(bwd_ms)[reps // 2]
+    fwd_ms = sorted(fwd_ms)[reps // 2] if reps else None
+    bwd_ms = sorted(bwd_ms)[reps // 2] if reps else None
 
     n, d, V = scored_rows, cfg.d, cfg.V
     alg_flop = {"full": 6, "hidden": 4, "none": 2}[cfg.backward] * n * d * V
@@ -436,7 +438,7 @@ def main() -> int:
         "mfma_frac_algorithmic": alg_flop / step_s / peak,
         "mfma_frac_executed": exe_flop / step_s / peak,
         "phase_ms": ({"two_call_forward": fwd_ms, "two_call_backward": bwd_ms, "two_call_step": fwd_ms + bwd_ms}
-                     if fused else {"forward": fwd_ms, "backward": bwd_ms}),
+                     if fused and reps else {} if fused else {"forward": fwd_ms, "backward": bwd_ms}),
         "kernels": kernels,
         "weight_stream": weight_stream,
         "roofline": {"kernel": dom, "bound": "mfma", "achieved": dom_achieved / 1e12, "peak": peak / 1e12,

@@ -262,7 +262,8 @@ int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
  * h^T of a pass, fp32 grad_w partials [V, d] over several passes, and once per call W widened to bf16 (fp8 weights)
  * or W^T (16-bit weights with V % 64 or d % 256 not 0). A smaller workspace is accepted down to the plan at a
  * 1 MiB budget; octo_head_bwd_plan with OCTO_WS_STEP gives {rows per pass, passes, V rounded up to 256, 1}.
- * fp32 operands run octo_head_fwd_grpo, then octo_head_bwd, in the same workspace. */
+ * fp32 operands run octo_head_fwd_grpo, then octo_head_bwd, in the same workspace. With grad_h and grad_w both
+ * NULL the call is octo_head_fwd_grpo (whose workspace size then suffices). */
 int octo_head_step_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                         const void *w, int64_t ldw, int w_dtype, const float *w_scale,
                         const int64_t *labels, const int64_t *idx, const int32_t *count,

@@ -678,6 +678,9 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
   }
   const bool need_gh = grad_h != nullptr, need_gw = grad_w != nullptr;
   if (n_max == 0) return OCTO_OK;
+  if (!need_gh && !need_gw)  // no gradient asked for: the forward with its GRPO tail (its own workspace size)
+    return head_fwd(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
+                    pre, post, use_tanh, logp, ent, lse, out2, ld_out2, gt, ws, ws_bytes, stream);
   if (cm.dt == OCTO_F32) {  // fp32: the forward, then the backward
     if (!ws || ws_bytes < step_fallback_bytes(n_max, d, V, w_dtype, need_gw, cm.gather))
       return octo_fail(OCTO_EWORKSPACE, "head_step_grpo: workspace %zu < %zu bytes", ws ? ws_bytes : (size_t)0,
@@ -811,7 +814,7 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     } else if (need_gh) {
       TimedLaunch t("gemm_store_grad_h", st);
       rc = launch_gemm_store(cm.dt, A2, B2, s2, o2, st, L.wt_on ? KM_NONE : KM_B);
-    } else {
+    } else if (need_gw) {
       rc = grad_w_pass(cm.dt, A3, KM_A, B3, V, d, r0, rows, p, L.passes, L.gacc_on, gacc, grad_w, gw_dtype, flags,
                        count, st);
     }

@@ -801,6 +801,8 @@ static bool kmajor_layout_ok(const Operand &X) {
 int launch_gemm_grads(int dt, const Operand &Ah, const Operand &Bh, const GemmShape &sh, const StoreArgs &eh,
                       bool wh_kmajor, const Operand &Aw, const Operand &Bw, const GemmShape &sw, const StoreArgs &ew,
                       hipStream_t st) {
+  if (!eh.C || !ew.C || !Ah.base || !Bh.base || !Aw.base || !Bw.base)
+    return octo_fail(OCTO_EINVAL, "gemm_grads: null operand or output");
   if (wh_kmajor && !kmajor_layout_ok(Bh)) return octo_fail(OCTO_EINVAL, "gemm_grads: K-major W layout");
   if (!kmajor_layout_ok(Aw)) return octo_fail(OCTO_EINVAL, "gemm_grads: K-major dz layout");
   for (int t : {eh.dtype, ew.dtype})
@@ -814,6 +816,7 @@ int launch_gemm_grads(int dt, const Operand &Ah, const Operand &Bh, const GemmSh
 
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
                       hipStream_t st, int kmajor) {
+  if (!e.C || !A.base || !B.base) return octo_fail(OCTO_EINVAL, "gemm_store: null operand or output");
   if (kmajor != KM_NONE) {
     if (!kmajor_layout_ok(kmajor == KM_A ? A : B)) return octo_fail(OCTO_EINVAL, "gemm_store: K-major operand layout");
     switch (dt) {

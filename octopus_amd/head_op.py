@@ -236,9 +236,12 @@ def head_step_grpo(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labe
     tail = _lib.GrpoTail(_p(prox_), _p(old_), _p(adv_), _p(mask_), adv_.numel(), eps_lo, eps_hi, reject_upper,
                          _p(g), _p(loss))
     w_code = _dtype_code(weight2)
-    ws_flags = _lib.WS_STEP | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, idx)
+    if need_rows or need_weight:
+        ws_flags = _lib.WS_STEP | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, idx)
+    else:  # no gradient: the library runs the forward with its GRPO tail, in the forward's workspace
+        ws_flags = _gather_flag(rows2, idx)
     nbytes = _lib.workspace_bytes(n_max, d, V, w_code, ws_flags)
-    if STEP_WORKSPACE_BYTES is not None:
+    if STEP_WORKSPACE_BYTES is not None and (need_rows or need_weight):
         nbytes = int(STEP_WORKSPACE_BYTES)
     ws = _workspace(nbytes, rows2)
     gh = None
@@ -266,6 +269,25 @@ def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, lab
             rows.new_empty((), dtype=torch.float32),
             torch.empty_like(rows) if need_rows else rows.new_empty(0),
             torch.empty_like(weight) if need_weight else weight.new_empty(0))
+
+
+def _step_setup(ctx, inputs, output):
+    _out, _lse, _g, _loss, grad_rows, grad_w = output
+    ctx.save_for_backward(grad_rows, grad_w)
+    ctx.need = (inputs[19], inputs[20])
+
+
+def _step_backward(ctx, _gout, _glse, _gg, gloss, _ggr, _ggw):
+    """The loss is the only differentiable output: its gradients were computed by the forward call, scaled here by
+    the incoming gradient of the loss (1 for loss.backward())."""
+    grad_rows, grad_w = ctx.saved_tensors
+    need_rows, need_weight = ctx.need
+    gr = grad_rows * gloss.to(grad_rows.dtype) if need_rows and ctx.needs_input_grad[0] else None
+    gw = grad_w * gloss.to(grad_w.dtype) if need_weight and ctx.needs_input_grad[1] else None
+    return (gr, gw) + (None,) * 19
+
+
+torch.library.register_autograd("octohead::head_step_grpo", _step_backward, setup_context=_step_setup)
 
 
 def _head_setup(ctx, inputs, output):
@@ -312,6 +334,28 @@ def fused_head(rows: Tensor, weight: Tensor, labels: Tensor, temperature: float,
     out, _ = head_fwd(rows, weight, w_scale, labels, idx, count, 1.0 / float(temperature), float(post.pre),
                       float(post.post), bool(post.tanh), labels_via_idx, scatter)
     return out
+
+
+def fused_grpo_head(rows: Tensor, weight: Tensor, labels: Tensor, temperature: float, adv: Tensor, mask: Tensor, *,
+                    prox: Optional[Tensor] = None, old: Optional[Tensor] = None, post: Post = Post(),
+                    idx: Optional[Tensor] = None, count: Optional[Tensor] = None, labels_via_idx: bool = False,
+                    scatter: bool = False, w_scale: Optional[Tensor] = None, eps_lo: float = 0.2,
+                    eps_hi: float = 0.28, reject_upper: float = 5.0) -> tuple[Tensor, Tensor]:
+    """(loss, out): the GRPO objective (grpo_loss's, on the head's logprobs) and fused_head's [n, 2] (logprob,
+    entropy) columns, from one octo_head_step_grpo call that also computes the loss's gradients with respect to rows
+    and weight (each when it requires grad and grad mode is on); loss.backward() then only scales them. The columns
+    carry no gradient: for losses other than this objective, use fused_head. prox, old, adv, mask are per flat
+    token (row of `rows`), as grpo_loss takes them. The gradients are held from this call to the backward."""
+    if temperature <= 0:
+        raise ValueError("temperature must be positive")
+    grad_on = torch.is_grad_enabled()
+    need_rows = grad_on and rows.requires_grad
+    need_weight = grad_on and weight.requires_grad
+    out, _lse, _g, loss, _gr, _gw = head_step_grpo(
+        rows, weight, w_scale, labels, idx, count, 1.0 / float(temperature), float(post.pre), float(post.post),
+        bool(post.tanh), labels_via_idx, scatter, prox, old, adv, mask, float(eps_lo), float(eps_hi),
+        float(reject_upper), need_rows, need_weight)
+    return loss, out.detach()
 
 
 # ---- _head_columns over materialised logits ------------------------------------------------------

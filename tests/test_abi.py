@@ -242,6 +242,28 @@ def test_small_entry_point_checks():
         _lib.call("octo_head_fwd_grpo", *fwd, ctypes.byref(tail), P, 1 << 30, None)
 
 
+def test_step_dispatch_checks_before_queueing():
+    """octo_head_step_grpo on the host: without a gradient it is the forward (whose workspace check answers), with
+    one it needs the step's plan; a missing GRPO tail or lse is refused; nothing is queued in any of these."""
+    tail = _lib.GrpoTail(P, None, P, P, 10, 0.2, 0.28, 5.0, P, None)
+
+    def step(gh, gw, ws_bytes=0, tail_=tail, lse=P):
+        _lib.call("octo_head_step_grpo", P, 10, 64, _lib.BF16, P, 64, _lib.BF16, None, P, None, None, 10, 64, 100,
+                  _lib.LSE_PAIR, 1.0, 1.0, 1.0, 0, None, None, lse, None, 2,
+                  ctypes.byref(tail_) if tail_ is not None else None, gh, 64, _lib.BF16, gw, _lib.BF16, None,
+                  ws_bytes, None)
+
+    with pytest.raises(ValueError, match="head_fwd: workspace"):
+        step(None, None)
+    for gh, gw in ((P, None), (None, P), (P, P)):
+        with pytest.raises(ValueError, match="head_step_grpo: workspace"):
+            step(gh, gw)
+    with pytest.raises(ValueError, match="null grpo"):
+        step(P, P, tail_=None)
+    with pytest.raises(ValueError, match="null lse"):
+        step(P, P, lse=None)
+
+
 def test_timing_hook_without_launches():
     """The timing hook records nothing until a GEMM is launched, and reading an unknown name is not an error."""
     _lib.call("octo_timing_enable", 1)

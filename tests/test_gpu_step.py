@@ -213,6 +213,31 @@ def test_step_extreme_logits():
         assert _rel(gh_s.cpu(), gh_ref) <= 1e-2 + 1.5 * e_two, (T, e_two)
 
 
+def test_step_grad_w_only():
+    """grad_W without grad_h (the rows frozen): over two passes, against the two-call backward and the oracle."""
+    N, d, V = 3000, 256, 5120
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, torch.bfloat16, seed=90)
+    ws, plan = _step_ws(N, d, V, _lib.BF16, 0, lambda p: p[1] == 2)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    idx, count = head_op.compact_rows(scored.to(DEV))
+    old = head_op.head_fwd(hd, Wd, None, yd, None, None, 1.0, 1.0, 1.0, False, False, False)[0][:, 0] + \
+        noise.to(DEV)
+    args = (hd, Wd, None, yd, idx, count, 1.0, 1.0, 1.0, False, True, True, old, None, adv.to(DEV), mask.to(DEV),
+            *EPS)
+    head_op.STEP_WORKSPACE_BYTES = ws
+    try:
+        out, lse, g, loss, gr, gw = head_op.head_step_grpo(*args, False, True)
+    finally:
+        head_op.STEP_WORKSPACE_BYTES = None
+    assert gr.numel() == 0
+    _, _, g2, _ = head_op.head_fwd_grpo(*args)
+    _, gw2 = head_op.head_bwd(hd, Wd, None, yd, idx, count, lse, g2, 1.0, 1.0, 1.0, False, True, False, True)
+    sel = scored.nonzero()[:, 0]
+    _, gw_ref = ohead.head_backward(h[sel], W.float(), y[sel], 1.0, g[:sel.numel()].cpu())
+    assert torch.equal(g, g2)
+    assert _rel(gw.cpu(), gw_ref) <= 1e-2 and _rel(gw, gw2) <= 4e-3, plan
+
+
 def test_step_with_no_scored_rows():
     N, d, V = 512, 64, 1024
     h, W, y, _, _, adv, noise = _batch(N, d, V, torch.bfloat16, seed=96)
@@ -257,3 +282,35 @@ def test_step_grad_w_accumulate_through_the_c_abi():
         _lib.call("octo_head_step_grpo", P(hd), n, hd.stride(0), _lib.BF16, P(Wd), Wd.stride(0), _lib.BF16, None,
                   P(yd), None, None, n, d, V, _lib.LSE_PAIR, 1.0 / T, 1.0, 1.0, 0, None, None, P(lse), P(out), 2,
                   ctypes.byref(tail), P(gh), d, _lib.F32, P(gw), _lib.F32, P(ws), 1 << 20, st)
+
+
+def test_fused_grpo_head_autograd_matches_the_two_call_route():
+    """fused_grpo_head under autograd: loss.backward() (here of 2 x loss) gives the gradients the step computed,
+    scaled, and they match the autograd route of fused_head then grpo_loss (the trainer's two-call composition) to
+    the 16-bit rounding of dz; the columns and the loss match that route's; under no_grad nothing is kept."""
+    from octopus_amd.head_op import fused_grpo_head, fused_head
+    N, d, V, T = 1800, 256, 4096, 0.9
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, torch.bfloat16, seed=99)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    idx, count = head_op.compact_rows(scored.to(DEV))
+    kw = dict(idx=idx, count=count, labels_via_idx=True, scatter=True)
+    old = (fused_head(hd, Wd, yd, T, **kw)[:, 0] + noise.to(DEV)).detach()
+    advd, maskd = adv.to(DEV), mask.to(DEV)
+
+    h1, W1 = hd.clone().requires_grad_(True), Wd.clone().requires_grad_(True)
+    loss1, out1 = fused_grpo_head(h1, W1, yd, T, advd, maskd, prox=old, **kw)
+    assert not out1.requires_grad and loss1.requires_grad
+    (2.0 * loss1).backward()
+
+    h2, W2 = hd.clone().requires_grad_(True), Wd.clone().requires_grad_(True)
+    out2 = fused_head(h2, W2, yd, T, **kw)
+    loss2, _ = head_op.grpo_loss(out2[:, 0], old, None, advd, maskd, *EPS)
+    (2.0 * loss2).backward()
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2.detach())
+    assert abs(loss1.item() - loss2.item()) <= 1e-5 * max(1.0, abs(loss2.item()))
+    assert (h1.grad[~scored.to(DEV)] == 0).all()
+    assert _rel(h1.grad, h2.grad) <= 4e-3 and _rel(W1.grad, W2.grad) <= 4e-3
+    with torch.no_grad():
+        loss3, out3 = fused_grpo_head(h1, W1, yd, T, advd, maskd, prox=old, **kw)
+    assert torch.equal(out3, out1) and not loss3.requires_grad
