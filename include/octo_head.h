@@ -252,13 +252,14 @@ int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
  * form under OCTO_LSE_PAIR, as for the backward). The gradients are those of grpo->loss; a caller whose loss is
  * c L scales them by c.
  * The rows run in passes of at most 32,768 (as many as the staging budget holds, balanced). The forward GEMM of a
- * pass stores each element's exponential relative to its 256-column tile's maximum, exp2(s log2 e - m_tile) x
- * post'(z) (x the fp8 row scale), as [rows, V rounded up to 256] in the MFMA type; once the merge has the rows'
- * (m2, l2S) and g, each tile is scaled by -g exp2(m_tile - m2 - l2S) / T into dz (the label entry written from the
- * fp32 target logit), and grad_h = dz . W, grad_W = dz^T . h run as in octo_head_bwd: the logits are computed
- * once instead of twice. dz differs from octo_head_bwd's by one more rounding to the MFMA type (the exponential's).
+ * pass stores each element's exponential relative to the maximum of its 128-column half tile, exp2(s log2 e - m_h)
+ * x post'(z) (the exp2 its softmax sums use), as f16 [rows, V rounded up to 256]; once the merge has the rows'
+ * (m2, l2S) and g, each half tile is scaled by -g exp2(m_h - m2 - l2S) / T (x the fp8 row scales) into dz in the
+ * MFMA type, the label entry written from the fp32 target logit; grad_h = dz . W and grad_W = dz^T . h then run as
+ * in octo_head_bwd (both in one launch per pass). The logits are computed once instead of twice; dz differs from
+ * octo_head_bwd's by one more rounding (the f16 exponential's, 2^-11 relative).
  * Workspace: octo_head_workspace_bytes with OCTO_WS_STEP [| OCTO_WS_NO_GRADW | OCTO_WS_GATHER], the plan at a
- * 2 GiB staging budget ([rows, V] of one pass); outside the staging are the pass's (m, S, U) per vocabulary tile,
+ * 2 GiB staging budget ([rows, V] of one pass); outside the staging are the pass's statistics per vocabulary tile,
  * h^T of a pass, fp32 grad_w partials [V, d] over several passes, and once per call W widened to bf16 (fp8 weights)
  * or W^T (16-bit weights with V % 64 or d % 256 not 0). A smaller workspace is accepted down to the plan at a
  * 1 MiB budget; octo_head_bwd_plan with OCTO_WS_STEP gives {rows per pass, passes, V rounded up to 256, 1}.

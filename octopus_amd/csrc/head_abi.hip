@@ -267,7 +267,7 @@ bool bwd_plan_for(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool n
 
 // ---- the fused GRPO step's plan (octo_head_step_grpo) ----------------------------------------------------
 // The step runs the rows in passes of P; per pass its forward GEMM stores, besides the statistics, every element's
-// tile-relative exponential (StatsArgs::ex) into a [P, V_pad] staging area in the MFMA type, which launch_dz_scale
+// exponential relative to its half tile's maximum (StatsArgs::ex) into a [P, V_pad] staging area, which launch_dz_scale
 // turns into dz once the merge has the rows' (m2, l2S) and g; the gradient GEMMs read it as the backward's read
 // their dz. Rows per pass: the most that fit the staging budget (at most kPassRowsMax), balanced over the passes.
 // The staging is the only part that grows with the budget; outside it sit the pass's statistics [P, V / 256], h^T
@@ -651,7 +651,8 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
 
 // ---- the fused GRPO step (octo_head_step_grpo) ---------------------------------------------------------
 // Forward, GRPO weight and backward of the compact rows in one call, pass by pass (StepLayout). The logits are
-// computed once per pass: the forward GEMM leaves each element's tile-relative exponential in the staging area, the
+// computed once per pass: the forward GEMM leaves each element's exponential (relative to its half tile's maximum, the
+// same exp2 its statistics sum) in the staging area, the
 // merge gives the rows' outputs, row state, g and label entry, launch_dz_scale scales the exponentials into dz, and
 // grad_h = dz . W, grad_W = dz^T . h follow as in the backward. fp32 operands run head_fwd, then octo_head_bwd.
 int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
@@ -735,7 +736,7 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     const int64_t rows = (n_max - r0) < L.P ? (n_max - r0) : L.P;
     const Operand Bh = hidden_operand(h, ldh, idx, count, r0, rows, cm, gathered, d);
 
-    // logits once: statistics per (row, vocabulary tile) and the tile-relative exponentials
+    // logits once: statistics per (row, vocabulary tile) and each element's exponential
     StatsArgs e;
     e.part = part;
     e.mtiles = L.mtiles;

@@ -109,7 +109,7 @@ __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
     const f32x4 *pr = a.part + rl * a.mtiles;
     for (int64_t mt = lane; mt < a.mtiles; mt += 64) {
       const f32x4 p = pr[mt];
-      st = stat_merge(st, Stat3{p[0], p[1], p[2]});
+      st = stat_merge(st, Stat3{fmaxf(p[0], p[3]), p[1], p[2]});
     }
     st = wave_stat_merge(st);
 
@@ -259,7 +259,8 @@ __global__ __launch_bounds__(256) void dz_scale_kernel(DzScaleArgs a) {
   for (int k = 0; k < kScaleChunks; ++k) {
     const int64_t c0 = (chunk0 + 256 * k) * 8;
     if (c0 >= a.V_pad) continue;
-    const float s = ngs * fexp2(pr[c0 >> 8][0] - m2 - l2s);
+    const f32x4 q = pr[c0 >> 8];  // the maximum the exponentials of this half of the tile are relative to
+    const float s = ngs * fexp2(((c0 & 128) ? q[3] : q[0]) - m2 - l2s);
     float x[8];
     unpack8(v[k], true, x);
 #pragma unroll

@@ -21,6 +21,35 @@
 
 namespace octo {
 
+// ---- 16-bit staging tiles ------------------------------------------------------------------------
+
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, bf16x2 *) {
+  bf16x2 p;
+  p[0] = (__bf16)lo;
+  p[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, p);
+}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi, f16x2_t *) {
+  f16x2_t p;
+  p[0] = (_Float16)lo;
+  p[1] = (_Float16)hi;
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// A 16-bit tile staged in LDS for a token-major store (dz, or the fused step's exponentials) (the ring, free after
+// the mainloop): T[t] holds token t (tile column) over the tile's 256 vocabulary rows, as 64 slots of 8 bytes (4
+// consecutive rows); logical slot s of token t sits at physical slot s ^ swz(t), the swizzle chosen for the
+// accumulator layout so that both accesses are free of bank conflicts:
+//   - the accumulator writes (Acc16N: a half-wave = 16 consecutive tokens x 2 adjacent slots, for 4 and 8 waves);
+//   - the token-major read-back (16 lanes: one token, 16 consecutive 16-byte pairs).
+template <class L> struct DzSwz;
+template <int NJ> struct DzSwz<Acc16N<NJ>> {
+  static __device__ __forceinline__ int at(int t) { return (((t & 15) << 1) | ((t >> 4) & 1)) ^ (((t >> 5) & 1) << 3); }
+};
+
 // ---- epilogue: online softmax statistics ----------------------------------------------------
 
 // acc *= per-vocab-row scale (fp8 weights), then the softcap tanh if any; then stats per token.
@@ -61,9 +90,15 @@ __device__ __forceinline__ void pre_transform(typename L::V (&acc)[L::NI][L::NJ]
 
 typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 
-template <class L, bool MASK>
-__device__ __forceinline__ void stats_cols(typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int wn, int lane,
-                                           int64_t V, float c, lds_f32x4 *red) {
+// The per-token softmax statistics of this wave's rows of the tile: red[wm * 256 + column] = (m2, S, U), m2 the
+// base-2 maximum, S and U the sums of e = exp2(t - m2) and e t (0 past V). EXT (16-bit, the fused step): each e,
+// times the softcap's derivative 1 - x^2 when TANH (acc holds x = tanh(pre z) then), is also written into the LDS
+// staging tile as f16, laid out as dz_stage lays out dz (zero past V and for tokens at or past nvalid): the stored
+// exponentials are relative to the wave's own maximum, which the tile's part keeps.
+template <class L, bool MASK, bool EXT = false, bool TANH = false>
+__device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int wn,
+                                           int lane, int64_t V, float c, lds_f32x4 *red, lds_char *tile = nullptr,
+                                           int64_t nvalid = 0) {
 #pragma unroll
   for (int j = 0; j < L::NJ; ++j) {
     float mx = -INFINITY;
@@ -76,26 +111,43 @@ __device__ __forceinline__ void stats_cols(typename L::V (&acc)[L::NI][L::NJ], i
       }
     mx = L::col_max(mx);
     const float m2 = mx * c;
+    const int tt = L::col(wn, j, lane);
     float S = 0.f, U = 0.f;
 #pragma unroll
     for (int i = 0; i < L::NI; ++i)
 #pragma unroll
-      for (int v = 0; v < L::NV; ++v) {
-        const float t = __builtin_fmaf(acc[i][j][v], c, -m2);
-        float e = fexp2(t);
-        if (MASK) {
-          const bool ok = m0 + L::row(wm, i, v, lane) < V;
-          e = ok ? e : 0.f;
+      for (int g4 = 0; g4 < L::NV / 4; ++g4) {
+        float x4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int v = 4 * g4 + u;
+          const float t = __builtin_fmaf(acc[i][j][v], c, -m2);
+          float e = fexp2(t);
+          if (MASK) {
+            const bool ok = m0 + L::row(wm, i, v, lane) < V;
+            e = ok ? e : 0.f;
+          }
+          S += e;
+          U = __builtin_fmaf(e, t, U);
+          if constexpr (EXT) {
+            const float x = acc[i][j][v];
+            x4[u] = tt < nvalid ? (TANH ? e * (1.f - x * x) : e) : 0.f;
+          }
         }
-        S += e;
-        U = __builtin_fmaf(e, t, U);
+        if constexpr (EXT) {
+          const int rl = L::row(wm, i, 4 * g4, lane);  // first of this lane's 4 vocab rows in the tile
+          i32x2 pk;
+          pk[0] = (int)pack2(x4[0], x4[1], (f16x2_t *)nullptr);
+          pk[1] = (int)pack2(x4[2], x4[3], (f16x2_t *)nullptr);
+          *(lds_i32x2 *)(tile + tt * 512 + (((rl >> 2) ^ DzSwz<L>::at(tt)) << 3)) = pk;
+        }
       }
     S = L::col_sum(S);
     U = L::col_sum(U);
     if (L::col_lane(lane)) {
       f32x4 o;
       o[0] = m2; o[1] = S; o[2] = U; o[3] = 0.f;
-      red[wm * 256 + L::col(wn, j, lane)] = o;
+      red[wm * 256 + tt] = o;
     }
   }
 }
@@ -127,7 +179,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
     Stat3 sa{a[0], a[1], a[2]}, sb{b[0], b[1], b[2]};
     Stat3 r = stat_merge(sa, sb);
     f32x4 o;
-    o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
+    o[0] = a[0]; o[1] = r.S; o[2] = r.U; o[3] = b[0];
     e.part[(n0 + t) * e.mtiles + e.v0 / TM + mt] = o;
   }
 }
@@ -138,22 +190,6 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 // only (dzA [token][vocab]: grad_h reads it K-contiguous, grad_W K-major), through one LDS staging tile as whole
 // 512-byte rows (dz_stage / dz_write below). fp32 is computed in place in the accumulators and stored directly in
 // both layouts (dzB [vocab][token] for grad_W's K-contiguous fp32 loop).
-
-typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pack2(float lo, float hi, bf16x2 *) {
-  bf16x2 p;
-  p[0] = (__bf16)lo;
-  p[1] = (__bf16)hi;
-  return __builtin_bit_cast(uint32_t, p);
-}
-__device__ __forceinline__ uint32_t pack2(float lo, float hi, f16x2_t *) {
-  f16x2_t p;
-  p[0] = (_Float16)lo;
-  p[1] = (_Float16)hi;
-  return __builtin_bit_cast(uint32_t, p);
-}
 
 // Stream a 256 x 512-byte LDS tile (rows stored with slot swizzle `s(row)` on 8-byte slots) to global
 // rows dst + row * ld_bytes, 16 bytes per thread per row-eighth. Non-temporal stores: dz is read back only by the
@@ -264,18 +300,8 @@ __device__ __forceinline__ void dz_store_direct(const f32x16 (&acc)[4][4], const
   }
 }
 
-// 16-bit dz through one LDS staging tile T (the ring, free after the mainloop): T[t] holds dz of token t (tile
-// column) over the tile's 256 vocabulary rows, as 64 slots of 8 bytes (4 consecutive rows); logical slot s of token t
-// sits at physical slot s ^ swz(t), the swizzle chosen for the accumulator layout so that both accesses are free
-// of bank conflicts:
-//   - the accumulator writes (Acc16N: a half-wave = 16 consecutive tokens x 2 adjacent slots, for 4 and 8 waves);
-//   - the token-major read-back (16 lanes: one token, 16 consecutive 16-byte pairs).
-// The dense pass writes -g p / T x post' (x fp8 row scale) everywhere; after a barrier one thread per token writes the
-// label entry (launch_hit's value) over it, so no element is compared against the label.
-template <class L> struct DzSwz;
-template <int NJ> struct DzSwz<Acc16N<NJ>> {
-  static __device__ __forceinline__ int at(int t) { return (((t & 15) << 1) | ((t >> 4) & 1)) ^ (((t >> 5) & 1) << 3); }
-};
+// (dz_stage below: the dense pass writes -g p / T x post' (x fp8 row scale) everywhere; after a barrier one thread per
+// token writes the label entry (launch_hit's value) over it, so no element is compared against the label.)
 
 typedef __attribute__((address_space(3))) short lds_short;
 
@@ -374,48 +400,6 @@ __device__ __forceinline__ void dz_stage(const typename L::V (&acc)[L::NI][L::NJ
         *(lds_i32x2 *)(tile + tt * 512 + (((rl >> 2) ^ sw) << 3)) = pk;
       }
   }
-}
-
-// The stats epilogue's tile-relative exponentials (StatsArgs::ex) into the LDS staging tile, laid out as dz_stage
-// lays out dz: ex = exp2(c t - m_tile) x post'(z), zero past V and past the tile's valid tokens. acc holds t's
-// argument after pre_transform (z, or tanh(pre z) under the softcap, whose derivative is 1 - t^2); m_tile of each token
-// column is the larger of its two waves' maxima in red, as stat_merge keeps it in part. (fp8 row scales are applied
-// by launch_dz_scale: in f16 here they would push the values into its subnormal range.)
-template <class L, typename P2, bool TANH, bool EDGE>
-__device__ __forceinline__ void ex_stage(const typename L::V (&acc)[L::NI][L::NJ], const StatsArgs &e, int64_t ma,
-                                         int64_t nvalid, int wm, int wn, int lane, const lds_f32x4 *red,
-                                         lds_char *tile) {
-  float mt[L::NJ];
-  int tt[L::NJ], sw[L::NJ];
-#pragma unroll
-  for (int j = 0; j < L::NJ; ++j) {
-    tt[j] = L::col(wn, j, lane);
-    const f32x4 a = red[tt[j]], b = red[256 + tt[j]];
-    mt[j] = fmaxf(a[0], b[0]);
-    sw[j] = DzSwz<L>::at(tt[j]);
-  }
-#pragma unroll
-  for (int i = 0; i < L::NI; ++i)
-#pragma unroll
-    for (int g4 = 0; g4 < L::NV / 4; ++g4) {
-      const int rl = L::row(wm, i, 4 * g4, lane);  // first of this lane's 4 vocab rows in the tile
-#pragma unroll
-      for (int j = 0; j < L::NJ; ++j) {
-        float x4[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float x = acc[i][j][4 * g4 + u];
-          float ev = fexp2(__builtin_fmaf(x, e.c, -mt[j]));
-          if constexpr (TANH) ev *= 1.f - x * x;
-          if constexpr (EDGE) ev = (ma + rl + u < e.V) ? ev : 0.f;
-          x4[u] = tt[j] < nvalid ? ev : 0.f;
-        }
-        i32x2 pk;
-        pk[0] = (int)pack2(x4[0], x4[1], (P2 *)nullptr);
-        pk[1] = (int)pack2(x4[2], x4[3], (P2 *)nullptr);
-        *(lds_i32x2 *)(tile + tt[j] * 512 + (((rl >> 2) ^ sw[j]) << 3)) = pk;
-      }
-    }
 }
 
 // ma: the tile's first vocabulary row; m0: its first dz column (ma - v0)
@@ -629,8 +613,8 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
 // the split stage barrier. Same box, 24,576 rows, d 2560, V 151,936 (against the 4-wave loop): gemm_stats 14.3
 // against 15.1 ms, gemm_dz 15.3 against 16.5 ms; without the split barrier gemm_dz was 0.4 ms slower than the 4-wave
 // loop.
-// EX: also store the tile-relative exponentials (StatsArgs::ex) through the LDS staging tile, as gemm_dz8 stores dz;
-// the per-wave statistics then sit past that tile.
+// EX: also store the exponentials (StatsArgs::ex) through the LDS staging tile, as gemm_dz8 stores dz; the per-wave
+// statistics then sit past that tile.
 template <int DT, bool A_FP8, bool TANH, bool EX>
 __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_stats8_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
   static_assert(ring5_ok(DT), "16-bit operands");
@@ -649,27 +633,21 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, s.K, smem, acc);
   const int64_t ma = e.v0 + m0;  // first vocabulary row of the tile
   pre_transform<L, A_FP8, TANH>(acc, ma, wm, lane, e.wscale, e.V, e.pre);
-  if (ma + TM > e.V) stats_cols<L, true>(acc, ma, wm, wn, lane, e.V, e.c, red);
-  else stats_cols<L, false>(acc, ma, wm, wn, lane, e.V, e.c, red);
-  __syncthreads();
-  if constexpr (EX) {  // f16 whatever the MFMA type: the values lie in [0, 1]
-    if (ma + TM > e.V) ex_stage<L, f16x2_t, TANH, true>(acc, e, ma, nvalid, wm, wn, lane, red, smem);
-    else ex_stage<L, f16x2_t, TANH, false>(acc, e, ma, nvalid, wm, wn, lane, red, smem);
-  }
+  if (ma + TM > e.V) stats_cols<L, true, EX, TANH>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid);
+  else stats_cols<L, false, EX, TANH>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid);
+  __syncthreads();  // per-wave statistics (and the staging tile) written
   const int t = threadIdx.x;
-  if (t < nvalid) {
+  if (t < nvalid) {  // (m_a, S, U, m_b): S and U relative to max(m_a, m_b), the halves' maxima kept
     const f32x4 a = red[t], b = red[256 + t];
     Stat3 sa{a[0], a[1], a[2]}, sb{b[0], b[1], b[2]};
     Stat3 r = stat_merge(sa, sb);
     f32x4 o;
-    o[0] = r.m; o[1] = r.S; o[2] = r.U; o[3] = 0.f;
+    o[0] = a[0]; o[1] = r.S; o[2] = r.U; o[3] = b[0];
     e.part[(n0 + t) * e.mtiles + e.v0 / TM + mt] = o;
   }
-  if constexpr (EX) {
-    __syncthreads();  // staging tile written
+  if constexpr (EX)
     lds_tile_to_global<2 * NTHREADS>(smem, (char *)e.ex + (n0 * e.ldx + ma) * 2, e.ldx * 2,
                                      [](int row) { return DzSwz<L>::at(row); });
-  }
 }
 
 template <int DT, bool A_FP8, bool TANH>

@@ -8,17 +8,19 @@ namespace octo {
 struct Operand;
 struct GemmShape;
 
-// gemm_stats epilogue arguments: part[row * mtiles + mt] = (m, S, U) of row over vocab tile mt. The GEMM's first
-// operand holds the vocabulary rows v0 .. (a chunk of W starting at row v0, a multiple of 256): its tile mt is vocab
-// tile v0 / 256 + mt.
+// gemm_stats epilogue arguments: part[row * mtiles + mt] = (m_a, S, U, m_b) of row over vocab tile mt: m_a and m_b
+// the base-2 maxima of the tile's first and last 128 vocabulary rows (m_b = -inf when none of those is below V), S and
+// U the online-softmax sums relative to max(m_a, m_b). The GEMM's first operand holds the vocabulary rows v0 .. (a
+// chunk of W starting at row v0, a multiple of 256): its tile mt is vocab tile v0 / 256 + mt.
 //
-// With ex != NULL (16-bit operands) the epilogue also stores, per element, the tile-relative exponential
-//   ex[token][v] = exp2(c t - m_tile) x post'(z)
+// With ex != NULL (16-bit operands) the epilogue also stores, per element, its exponential relative to its half
+// tile's maximum (m_h = m_a or m_b),
+//   ex[token][v] = exp2(c t - m_h) x post'(z)
 // token-major in f16 (columns v of the vocabulary, rows = the GEMM's tokens, ldx elements apart; zero past V and past
-// the tile's valid tokens), where m_tile is the tile's base-2 maximum as part stores it. Once the row's (m2, l2S) and
-// g are known, dz = -g gmul exp2(m_tile - m2 - l2S) ex x (fp8 row scale) (the fused step, launch_dz_scale). f16 for
-// any MFMA type: the values lie in [0, 1], where f16 keeps 11 bits to bf16's 8; what it rounds in its subnormal range,
-// below 2^-14 of the tile's largest probability, errs by at most 2^-25 of it per element.
+// the tile's valid tokens), the same exp2 the sums use. Once the row's (m2, l2S) and g are known, dz = -g gmul
+// exp2(m_h - m2 - l2S) ex x (fp8 row scale) (the fused step, launch_dz_scale). f16 for any MFMA type: the values lie
+// in [0, 1], where f16 keeps 11 bits to bf16's 8; what it rounds in its subnormal range, below 2^-14 of the half
+// tile's largest probability, errs by at most 2^-25 of it per element.
 struct StatsArgs {
   f32x4 *part;
   int64_t mtiles;
@@ -161,10 +163,10 @@ struct MergeArgs {
 };
 int launch_merge(const MergeArgs &a, hipStream_t st);
 
-// dz of compact rows r0 .. r0 + rows (local row i = r - r0) from the tile-relative exponentials a stats GEMM stored
-// (StatsArgs::ex, f16), in place: dz[i][v] = -g[r] gmul exp2(part[i][v / 256].m - m2 - l2S) ex[i][v] (x wscale[v]
-// for fp8 weights, 0 past V) for v < V_pad, then dz[i][y] = hit[i], in the MFMA type. Rows at or past the count are
-// left as they are (the GEMMs that read dz stop at the count).
+// dz of compact rows r0 .. r0 + rows (local row i = r - r0) from the exponentials a stats GEMM stored (StatsArgs::ex,
+// f16), in place: dz[i][v] = -g[r] gmul exp2(m_h - m2 - l2S) ex[i][v] (x wscale[v] for fp8 weights, 0 past V) for
+// v < V_pad, m_h the maximum of v's half tile in part[i][v / 256], then dz[i][y] = hit[i], in the MFMA type. Rows at
+// or past the count are left as they are (the GEMMs that read dz stop at the count).
 struct DzScaleArgs {
   void *dz;  // [rows, ld] 16-bit: f16 exponentials in, dz in dtype (bf16 / f16) out
   int64_t ld, V_pad;
