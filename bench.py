@@ -76,10 +76,10 @@ PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 def recorded_traffic(kernel: str, workload: str, fused: bool = False):
     """HBM bytes per launch of `kernel` at `workload` as recorded from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-    in profiles/gemm_kernels_<workload>_counters.md (line `traffic <kernel>: <bytes>`, or `traffic step <kernel>:`
-    for the fused step's launches), or None."""
-    path = os.path.join(PROFILES, f"gemm_kernels_{workload}_counters.md")
-    key = f"traffic step {kernel}:" if fused else f"traffic {kernel}:"
+    (line `traffic <kernel>: <bytes>`) in profiles/step_kernels_<workload>.md for the fused step's launches, in
+    profiles/gemm_kernels_<workload>_counters.md for the two-call route's; None when not recorded."""
+    path = os.path.join(PROFILES, f"step_kernels_{workload}.md" if fused else f"gemm_kernels_{workload}_counters.md")
+    key = f"traffic {kernel}:"
     try:
         for line in open(path):
             if line.startswith(key):
