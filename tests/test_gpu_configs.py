@@ -77,3 +77,35 @@ def test_configuration(name):
         assert _rel(h.grad[ref_idx].float(), gr_r) <= 1e-2
     if need_w:
         assert _rel(W.grad.float(), gw_r) <= 1e-2
+
+
+@pytest.mark.parametrize("name", ["cfg3", "cfg4", "cfg5"])
+def test_configuration_fused_step(name):
+    """The fused GRPO step (`fused_grpo_head`, what bench.py times) at full size: its columns bitwise the two-call
+    forward's, its GRPO weight against the oracle on those logprobs, and its gradients (loss.backward()) against the
+    chunked fp32 reference for that weight over every scored row, plus the size-independent properties."""
+    from octopus_amd.head_op import fused_grpo_head
+    cfg = CONFIGS[name]
+    b = make_batch(cfg, DEV)
+    idx, count = head_op.compact_rows(b.scored)
+    ref_idx = torch.nonzero(b.scored)[:, 0]
+    kw = dict(idx=idx, count=count, labels_via_idx=True, scatter=True, w_scale=b.w_scale)
+    out0 = fused_head(b.hidden, b.weight, b.labels, cfg.temperature, **kw)
+    old = (out0[:, 0] + b.old_noise).detach()
+    need_w = cfg.backward == "full"
+    h = b.hidden.detach().requires_grad_(True)
+    W = b.weight.detach().requires_grad_(need_w)
+    loss, out = fused_grpo_head(h, W, b.labels, cfg.temperature, b.adv, b.scored.float(), prox=old, **kw)
+    loss.backward()
+    torch.cuda.synchronize()
+    assert torch.equal(out, out0.detach())
+    lo, g_ref = ogrpo.grpo(out[:, 0].double().cpu().numpy(), b.adv.double().cpu().numpy(), b.scored.cpu().numpy(),
+                           prox=old.double().cpu().numpy())
+    assert abs(loss.item() - lo) <= 1e-5 * max(1.0, abs(lo))
+    g = torch.from_numpy(g_ref).float().to(DEV)[ref_idx]
+    _, _, gr_r, gw_r = head_fp32(b.hidden[ref_idx], dequantised(b), b.labels[ref_idx], cfg.temperature, g=g,
+                                 want_w=need_w)
+    assert (h.grad[~b.scored] == 0).all()
+    assert _rel(h.grad[ref_idx].float(), gr_r) <= 1e-2
+    if need_w:
+        assert _rel(W.grad.float(), gw_r) <= 1e-2
