@@ -36,7 +36,8 @@
  *   octopus/rl/actor.py:343-347 (AReaL's grpo_loss_fn reads the head's columns, then loss.backward()
  *     runs lm_head.py:115-121's checkpoint recompute) -> octo_head_step_grpo (forward, GRPO loss and
  *                                                     backward in one call, the logits computed once per
- *                                                     row pass)
+ *                                                     row pass); over a tree's pair rows (tree_head_output,
+ *                                                     prefix_tree.py:416-421): octo_head_step_grpo_pairs
  */
 #ifndef OCTO_HEAD_H
 #define OCTO_HEAD_H
@@ -274,6 +275,26 @@ int octo_head_step_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
                         const octo_grpo_tail *grpo,
                         void *grad_h, int64_t ld_gh, int gh_dtype, void *grad_w, int gw_dtype,
                         void *ws, size_t ws_bytes, void *stream);
+
+/* octo_head_step_grpo over a prefix tree's deduplicated (position, label) pair rows (prefix_tree.py:156-166,
+ * 416-421: the rows tree_head_output runs the head on): compact row r is hidden row pair_pos[r] with label
+ * pair_label[r], r < *pair_count (or n_pairs); flat token t takes pair row flat_pair[t] (none when negative or at or
+ * past the row count). The GRPO tail's arrays (prox, old, adv, mask; n_tokens of them) are per flat token, so a pair
+ * row's g is the sum of its flat tokens' dL/dlogprob and the loss sums over the flat tokens. out_flat [n_flat,
+ * ld_out] receives each flat token's (logprob, entropy), 0 for a token with no pair (a masked one adds its loss term
+ * at logprob 0, as the objective over the expanded columns does); lse and grpo->g are per pair row
+ * (grpo->g complete, also past the count: 0); grad_h [n_pairs, ld_gh] per pair row (rows of one tree position are
+ * summed by the caller's scatter). g and the loss are sums of float atomics: their last bits may vary run to run.
+ * flags: OCTO_LSE_PAIR only (labels are per pair row). 16-bit operands; workspace as octo_head_step_grpo. */
+int octo_head_step_grpo_pairs(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
+                              const void *w, int64_t ldw, int w_dtype, const float *w_scale,
+                              const int64_t *pair_label, const int64_t *pair_pos, const int32_t *pair_count,
+                              int64_t n_pairs, int d, int V, int flags,
+                              float inv_T, float pre, float post, int use_tanh, float *lse,
+                              const int64_t *flat_pair, int64_t n_flat, float *out_flat, int64_t ld_out,
+                              const octo_grpo_tail *grpo,
+                              void *grad_h, int64_t ld_gh, int gh_dtype, void *grad_w, int gw_dtype,
+                              void *ws, size_t ws_bytes, void *stream);
 
 /* GRPO/PPO policy-gradient weight per token (AReaL grpo_loss_fn semantics):
  *   ratio r = exp(logp - prox)          (prox == NULL: prox = logp, i.e. reuse_train_logp)

@@ -56,6 +56,9 @@ SIGNATURES = {
     "octo_head_step_grpo": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
                             _f32, _f32, _f32, _i32, _p, _p, _p, _p, _i64, ctypes.POINTER(GrpoTail),
                             _p, _i64, _i32, _p, _i32, _p, _sz, _p],
+    "octo_head_step_grpo_pairs": [_p, _i64, _i64, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i64, _i32, _i32, _i32,
+                                  _f32, _f32, _f32, _i32, _p, _p, _i64, _p, _i64, ctypes.POINTER(GrpoTail),
+                                  _p, _i64, _i32, _p, _i32, _p, _sz, _p],
     "octo_columns_fwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p],
     "octo_columns_bwd": [_p, _i64, _i32, _p, _i64, _i32, _f32, _p, _p, _p, _i64, _p],
     "octo_pairs_expand": [_p, _i64, _i32, _p, _i64, _p, _p],

@@ -277,7 +277,7 @@ struct StepLayout {
   int64_t P, passes, mtiles, V_pad;
   int esz;
   bool gacc_on, wide_on, wt_on;
-  size_t part, z, hit, ht, dz, wide, wt, gacc, rows, total;
+  size_t part, z, hit, rowout, ht, dz, wide, wt, gacc, rows, total;
 };
 
 // Rows per pass for a step without grad_W: each pass's grad_h launch is one tile per CU per round of long tiles (K =
@@ -325,8 +325,10 @@ bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need
   off += align_up((size_t)L.P * L.mtiles * sizeof(f32x4));
   L.z = off;  // the GRPO tail's token count
   off += kAlign;
-  L.hit = off;  // dz at each row's label [P] fp32
+  L.hit = off;  // dz at each row's label per unit of g gmul [P] fp32
   off += align_up((size_t)L.P * sizeof(float));
+  L.rowout = off;  // (logprob, entropy) per compact row [n_max, 2] fp32, for the pair-row GRPO tail
+  off += align_up((size_t)n_max * 2 * sizeof(float));
   L.ht = off;  // h^T [d, P] of the pass's rows (grad_W)
   if (need_gw) off += align_up((size_t)d * L.P * L.esz);
   L.dz = off;  // the exponentials, then dz [P, V_pad], token-major
@@ -655,11 +657,21 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
 // same exp2 its statistics sum) in the staging area, the
 // merge gives the rows' outputs, row state, g and label entry, launch_dz_scale scales the exponentials into dz, and
 // grad_h = dz . W, grad_W = dz^T . h follow as in the backward. fp32 operands run head_fwd, then octo_head_bwd.
+// Prefix-tree pair rows (octo_head_step_grpo_pairs): the compact rows are the tree's (position, label) pairs, the
+// GRPO tail's arrays are per flat token, and flat token t reads pair row flat_pair[t]; its columns go to out_flat.
+struct StepPairs {
+  const int64_t *flat_pair;
+  int64_t n_flat;
+  float *out_flat;
+  int64_t ld_out;
+};
+
 int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,
               const float *w_scale, const int64_t *labels, const int64_t *idx, const int32_t *count, int64_t n_max,
               int d, int V, int flags, float inv_T, float pre, float post, int use_tanh, float *logp, float *ent,
               float *lse, float *out2, int64_t ld_out2, const octo_grpo_tail *gt, void *grad_h, int64_t ld_gh,
-              int gh_dtype, void *grad_w, int gw_dtype, void *ws, size_t ws_bytes, void *stream) {
+              int gh_dtype, void *grad_w, int gw_dtype, void *ws, size_t ws_bytes, void *stream,
+              const StepPairs *pm = nullptr) {
   Common cm;
   int rc = check_common(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, n_max, d, V, flags, inv_T,
                         pre, post, use_tanh, cm);
@@ -678,8 +690,14 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     OCTO_CHECK_ARG(gw_dtype == OCTO_BF16 || gw_dtype == OCTO_F16 || gw_dtype == OCTO_F32, "head_step_grpo: grad_w dtype");
   }
   const bool need_gh = grad_h != nullptr, need_gw = grad_w != nullptr;
-  if (n_max == 0) return OCTO_OK;
-  if (!need_gh && !need_gw)  // no gradient asked for: the forward with its GRPO tail (its own workspace size)
+  if (pm) {
+    OCTO_CHECK_ARG(!(flags & (OCTO_ROWS_VIA_IDX | OCTO_OUT_SCATTER)), "head_step_grpo_pairs: labels are per pair row");
+    OCTO_CHECK_ARG(pm->n_flat >= 0 && (pm->n_flat == 0 || (pm->flat_pair && pm->out_flat)) && pm->ld_out >= 2,
+                   "head_step_grpo_pairs: flat_pair, out_flat or ld_out");
+    if (cm.dt == OCTO_F32) return octo_fail(OCTO_EUNSUPPORTED, "head_step_grpo_pairs: fp32 operands");
+  }
+  if (n_max == 0 && !pm) return OCTO_OK;
+  if (!need_gh && !need_gw && !pm)  // no gradient asked for: the forward with its GRPO tail (its own workspace size)
     return head_fwd(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
                     pre, post, use_tanh, logp, ent, lse, out2, ld_out2, gt, ws, ws_bytes, stream);
   if (cm.dt == OCTO_F32) {  // fp32: the forward, then the backward
@@ -712,6 +730,26 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
 
   rc = launch_grpo_count(gt->mask, gt->n_tokens, z, gt->loss, st);  // Z, and the loss zeroed
   if (rc) return rc;
+  const bool grads = need_gh || need_gw;
+  float *rowout = (float *)(wsb + L.rowout);
+  if (pm && L.passes == 0) {  // no pair row: every flat token's columns are 0
+    PairsGrpoArgs pa{};
+    pa.flat_pair = pm->flat_pair;
+    pa.n_flat = pm->n_flat;
+    pa.count = count;
+    pa.rowout = rowout;
+    pa.prox = gt->prox;
+    pa.old = gt->old;
+    pa.adv = gt->adv;
+    pa.mask = gt->mask;
+    pa.n_tokens = gt->n_tokens;
+    pa.z = z;
+    pa.g = gt->g;
+    pa.out2 = pm->out_flat;
+    pa.ld_out2 = pm->ld_out;
+    pa.first_pass = 1;
+    return launch_pairs_grpo(pa, st);
+  }
   void *gathered = cm.gather ? wsb + L.rows : nullptr;
   if (gathered) {
     rc = launch_rows_gather(h, ldh * cm.hesz, idx, count, n_max, (int64_t)d * cm.hesz, gathered, st);
@@ -745,7 +783,7 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     e.wscale = w_scale;
     e.c = cm.c;
     e.pre = cm.pre;
-    e.ex = dz;
+    e.ex = grads ? dz : nullptr;
     e.ldx = L.V_pad;
     {
       TimedLaunch t("gemm_stats", st);
@@ -753,16 +791,50 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     }
     if (rc) return rc;
 
-    // the pass's outputs, row state, GRPO weight g (the loss summed) and dz at each label
-    MergeArgs m = merge_args(part, L.mtiles, h, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max,
-                             d, V, flags, inv_T, pre, post, use_tanh, logp, ent, lse, out2, ld_out2, gt, z);
+    // the pass's outputs, row state, GRPO weight g (the loss summed) and dz at each label per unit of g; pair rows:
+    // the rows' columns to rowout, then each flat token's columns and GRPO weight, summed into its pair's g
+    MergeArgs m = pm ? merge_args(part, L.mtiles, h, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count,
+                                  n_max, d, V, flags, inv_T, pre, post, use_tanh, logp, ent, lse, rowout, 2, nullptr,
+                                  z)
+                     : merge_args(part, L.mtiles, h, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count,
+                                  n_max, d, V, flags, inv_T, pre, post, use_tanh, logp, ent, lse, out2, ld_out2, gt, z);
     m.row_off = r0;
     m.rows = rows;
     m.c = cm.c;
-    m.gmul = cm.gmul;
     m.hit = hit;
+    if (pm) {
+      m.zero_g = 1;
+      m.g_zero = gt->g;
+    }
     rc = launch_merge(m, st);
     if (rc) return rc;
+    if (pm) {
+      PairsGrpoArgs pa{};
+      pa.flat_pair = pm->flat_pair;
+      pa.n_flat = pm->n_flat;
+      pa.r0 = r0;
+      pa.rows = rows;
+      pa.n_max = n_max;
+      pa.count = count;
+      pa.rowout = rowout;
+      pa.prox = gt->prox;
+      pa.old = gt->old;
+      pa.adv = gt->adv;
+      pa.mask = gt->mask;
+      pa.n_tokens = gt->n_tokens;
+      pa.eps_lo = gt->eps_lo;
+      pa.eps_hi = gt->eps_hi;
+      pa.reject_upper = gt->reject_upper;
+      pa.z = z;
+      pa.g = gt->g;
+      pa.loss = gt->loss;
+      pa.out2 = pm->out_flat;
+      pa.ld_out2 = pm->ld_out;
+      pa.first_pass = p == 0;
+      rc = launch_pairs_grpo(pa, st);
+      if (rc) return rc;
+    }
+    if (!grads) continue;
 
     DzScaleArgs sa;
     sa.dz = dz;
@@ -997,6 +1069,20 @@ int octo_head_step_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
   return head_step(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, labels, idx, count, n_max, d, V, flags, inv_T,
                    pre, post, use_tanh, logp, ent, lse, out2, ld_out2, grpo, grad_h, ld_gh, gh_dtype, grad_w,
                    gw_dtype, ws, ws_bytes, stream);
+}
+
+int octo_head_step_grpo_pairs(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw,
+                              int w_dtype, const float *w_scale, const int64_t *pair_label, const int64_t *pair_pos,
+                              const int32_t *pair_count, int64_t n_pairs, int d, int V, int flags, float inv_T,
+                              float pre, float post, int use_tanh, float *lse, const int64_t *flat_pair,
+                              int64_t n_flat, float *out_flat, int64_t ld_out, const octo_grpo_tail *grpo,
+                              void *grad_h, int64_t ld_gh, int gh_dtype, void *grad_w, int gw_dtype, void *ws,
+                              size_t ws_bytes, void *stream) {
+  OCTO_CHECK_ARG(pair_pos != nullptr, "head_step_grpo_pairs: null pair_pos");
+  const StepPairs pm{flat_pair, n_flat, out_flat, ld_out};
+  return head_step(h, h_rows, ldh, h_dtype, w, ldw, w_dtype, w_scale, pair_label, pair_pos, pair_count, n_pairs, d,
+                   V, flags, inv_T, pre, post, use_tanh, nullptr, nullptr, lse, nullptr, 2, grpo, grad_h, ld_gh,
+                   gh_dtype, grad_w, gw_dtype, ws, ws_bytes, stream, &pm);
 }
 
 int octo_head_bwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void *w, int64_t ldw, int w_dtype,

@@ -147,26 +147,27 @@ __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
           grpo_token(lp, a.gprox ? a.gprox + hrow : nullptr, a.gold ? a.gold + hrow : nullptr, a.gadv[hrow],
                      a.eps_lo, a.eps_hi, a.reject_upper, 1.f / a.z[0], gt, lt);
         a.g[r] = gt;
-        if (a.hit) {  // launch_hit's formula, from the same target logit and row state
-          float v = 0.f;
-          if (y_ok) {
-            const bool f8 = a.w_dtype == OCTO_FP8E4M3;
-            const float x = f8 ? raw * a.wscale[y] : raw;
-            const float gs = gt * a.gmul;
-            if (a.use_tanh) {
-              const float th = ftanh(a.pre * x);
-              v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(th, a.c, -st.m) - l2S), gs) * (1.f - th * th);
-            } else {
-              v = __builtin_fmaf(-gs, fexp2(__builtin_fmaf(x, a.c, -st.m) - l2S), gs);
-            }
-            if (f8) v *= a.wscale[y];
-          }
-          a.hit[rl] = v;
-        }
       }
+      if (a.hit) {  // the label entry per unit of g gmul: launch_hit's formula from the same target logit and state
+        float v = 0.f;
+        if (y_ok) {
+          const bool f8 = a.w_dtype == OCTO_FP8E4M3;
+          const float x = f8 ? raw * a.wscale[y] : raw;
+          if (a.use_tanh) {
+            const float th = ftanh(a.pre * x);
+            v = (1.f - fexp2(__builtin_fmaf(th, a.c, -st.m) - l2S)) * (1.f - th * th);
+          } else {
+            v = 1.f - fexp2(__builtin_fmaf(x, a.c, -st.m) - l2S);
+          }
+          if (f8) v *= a.wscale[y];
+        }
+        a.hit[rl] = v;
+      }
+      if (a.zero_g) a.g_zero[r] = 0.f;
     }
-  } else if (a.hit && lane == 0 && rl < rows) {
-    a.hit[rl] = 0.f;
+  } else if (lane == 0 && rl < rows) {
+    if (a.hit) a.hit[rl] = 0.f;
+    if (a.zero_g && a.row_off + rl < a.n_max) a.g_zero[a.row_off + rl] = 0.f;
   }
   if (!a.loss) return;  // uniform across the workgroup: no barrier below is skipped by part of it
   if (lane == 0) loss_part[wave] = lt;
@@ -278,7 +279,7 @@ __global__ __launch_bounds__(256) void dz_scale_kernel(DzScaleArgs a) {
         for (int e = 0; e < 8; ++e) x[e] *= (c0 + e < a.V) ? a.wscale[c0 + e] : 0.f;
       }
     }
-    if (y >= c0 && y < c0 + 8 && y < a.V) x[y - c0] = a.hit[i];
+    if (y >= c0 && y < c0 + 8 && y < a.V) x[y - c0] = -ngs * a.hit[i];  // g gmul (1 - p_y) post'(z_y) (x scale)
     __builtin_nontemporal_store(pack8(x, f16), (i32x4 *)(row + c0 * 2));
   }
 }
@@ -292,6 +293,53 @@ int launch_dz_scale(const DzScaleArgs &a, hipStream_t st) {
   const unsigned bx = (unsigned)cdiv(a.V_pad / 8, 256 * kScaleChunks);
   hipLaunchKernelGGL(dz_scale_kernel, dim3(bx, (unsigned)a.rows), dim3(256), 0, st, a);
   OCTO_CHECK_LAUNCH("dz_scale");
+  return OCTO_OK;
+}
+
+// ---- the fused step's GRPO tail over prefix-tree pair rows ----------------------------------------------
+// One thread per flat token; the workgroup's loss terms are summed in LDS and added with one atomic (as the merge).
+__global__ __launch_bounds__(256) void pairs_grpo_kernel(PairsGrpoArgs a) {
+  __shared__ float part[256];
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
+  float lt = 0.f;
+  if (t < a.n_flat) {
+    const int64_t p = a.flat_pair[t];
+    const bool paired = p >= 0 && p < cnt;
+    if (paired && p >= a.r0 && p < a.r0 + a.rows) {
+      const float lp = a.rowout[2 * p], ent = a.rowout[2 * p + 1];
+      a.out2[t * a.ld_out2] = lp;
+      a.out2[t * a.ld_out2 + 1] = ent;
+      if (t < a.n_tokens && a.mask[t] != 0.f) {
+        float gt = 0.f;
+        grpo_token(lp, a.prox ? a.prox + t : nullptr, a.old ? a.old + t : nullptr, a.adv[t], a.eps_lo, a.eps_hi,
+                   a.reject_upper, 1.f / a.z[0], gt, lt);
+        if (gt != 0.f) atomicAdd(a.g + p, gt);
+      }
+    } else if (!paired && a.first_pass) {  // columns 0; a masked token adds its loss term at logprob 0 (no row)
+      a.out2[t * a.ld_out2] = 0.f;
+      a.out2[t * a.ld_out2 + 1] = 0.f;
+      if (t < a.n_tokens && a.mask[t] != 0.f) {
+        float gt = 0.f;
+        grpo_token(0.f, a.prox ? a.prox + t : nullptr, a.old ? a.old + t : nullptr, a.adv[t], a.eps_lo, a.eps_hi,
+                   a.reject_upper, 1.f / a.z[0], gt, lt);
+      }
+    }
+  }
+  if (!a.loss) return;  // uniform across the workgroup
+  part[threadIdx.x] = lt;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) part[threadIdx.x] += part[threadIdx.x + s];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0 && part[0] != 0.f) atomicAdd(a.loss, part[0]);
+}
+
+int launch_pairs_grpo(const PairsGrpoArgs &a, hipStream_t st) {
+  if (a.n_flat == 0) return OCTO_OK;
+  hipLaunchKernelGGL(pairs_grpo_kernel, dim3((unsigned)cdiv(a.n_flat, 256)), dim3(256), 0, st, a);
+  OCTO_CHECK_LAUNCH("pairs_grpo");
   return OCTO_OK;
 }
 

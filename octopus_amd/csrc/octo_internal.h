@@ -155,18 +155,22 @@ struct MergeArgs {
   const float *z;  // max(1, masked-token count), from launch_grpo_count
   float *g, *loss;
   // Rows row_off .. row_off + rows of the compact order (rows < 0: all n_max), part indexed from row_off. With hit
-  // != NULL (and g), hit[r - row_off] = the row's dz at its label, g gmul (1 - p_y) post'(z_y) x (fp8 row scale), as
-  // launch_hit computes it; 0 past the count or for a label outside [0, V).
+  // != NULL, hit[r - row_off] = the row's dz at its label per unit of g gmul, (1 - p_y) post'(z_y) x (fp8 row scale)
+  // (launch_hit's formula without g gmul); 0 past the count or for a label outside [0, V). zero_g: g_zero[r] = 0 for
+  // the launch's rows (rows whose g a later kernel accumulates).
   int64_t row_off = 0, rows = -1;
-  float c = 0.f, gmul = 0.f;
+  float c = 0.f;
   float *hit = nullptr;
+  int zero_g = 0;
+  float *g_zero = nullptr;
 };
 int launch_merge(const MergeArgs &a, hipStream_t st);
 
 // dz of compact rows r0 .. r0 + rows (local row i = r - r0) from the exponentials a stats GEMM stored (StatsArgs::ex,
 // f16), in place: dz[i][v] = -g[r] gmul exp2(m_h - m2 - l2S) ex[i][v] (x wscale[v] for fp8 weights, 0 past V) for
-// v < V_pad, m_h the maximum of v's half tile in part[i][v / 256], then dz[i][y] = hit[i], in the MFMA type. Rows at
-// or past the count are left as they are (the GEMMs that read dz stop at the count).
+// v < V_pad, m_h the maximum of v's half tile in part[i][v / 256], then dz[i][y] = g[r] gmul hit[i] (the merge's
+// label entry per unit of g gmul), in the MFMA type. Rows at or past the count are left as they are (the GEMMs that
+// read dz stop at the count).
 struct DzScaleArgs {
   void *dz;  // [rows, ld] 16-bit: f16 exponentials in, dz in dtype (bf16 / f16) out
   int64_t ld, V_pad;
@@ -186,6 +190,27 @@ struct DzScaleArgs {
   int64_t V;
 };
 int launch_dz_scale(const DzScaleArgs &a, hipStream_t st);
+
+// The GRPO tail of the fused step over prefix-tree pair rows: flat token t reads its pair row p = flat_pair[t]; for
+// the pass's rows (r0 <= p < r0 + rows, below the row count) it takes the row's (logprob, entropy) from rowout (2
+// floats per compact row) into out2[t] and, when mask[t] != 0, adds its GRPO weight to g[p] and its loss term to the
+// loss (atomics: the last bits of both sums may vary). Tokens with no pair (p < 0 or past the count) get out2 = 0
+// in the first pass and, when masked, their loss term at logprob 0 (as the objective over the expanded columns).
+struct PairsGrpoArgs {
+  const int64_t *flat_pair;
+  int64_t n_flat;
+  int64_t r0, rows, n_max;
+  const int32_t *count;
+  const float *rowout;
+  const float *prox, *old, *adv, *mask;
+  int64_t n_tokens;
+  float eps_lo, eps_hi, reject_upper;
+  const float *z;
+  float *g, *loss, *out2;
+  int64_t ld_out2;
+  int first_pass;
+};
+int launch_pairs_grpo(const PairsGrpoArgs &a, hipStream_t st);
 // dst row r (row_bytes, contiguous) = src row idx[r] (ld_src_bytes apart) for r < *count; 16-byte aligned rows
 int launch_rows_gather(const void *src, int64_t ld_src_bytes, const int64_t *idx, const int32_t *count,
                        int64_t n_max, int64_t row_bytes, void *dst, hipStream_t st);

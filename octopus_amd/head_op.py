@@ -271,10 +271,68 @@ def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, lab
             torch.empty_like(weight) if need_weight else weight.new_empty(0))
 
 
+@torch.library.custom_op("octohead::head_step_grpo_pairs", mutates_args=(), device_types="cuda")
+def head_step_grpo_pairs(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], pair_label: Tensor,
+                         pair_pos: Tensor, pair_count: Optional[Tensor], flat_pair: Tensor, inv_T: float, pre: float,
+                         post: float, use_tanh: bool, prox: Optional[Tensor], old: Optional[Tensor], adv: Tensor,
+                         mask: Tensor, eps_lo: float, eps_hi: float, reject_upper: float, need_rows: bool,
+                         need_weight: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """head_step_grpo over a prefix tree's pair rows (octo_head_step_grpo_pairs): row r is rows[pair_pos[r]] with
+    label pair_label[r]; flat token t reads pair row flat_pair[t] (none when negative or at or past the row count);
+    prox, old, adv, mask are per flat token. Returns (out [T_flat, 2] per flat token, lse [P, 2], g [P] per pair row,
+    loss, grad_rows [rows, d] (pair rows summed into their tree positions), grad_weight)."""
+    rows2, weight2 = _rows2d(rows), _rows2d(weight)
+    pair_label, pair_pos, flat_pair = _index(pair_label), _index(pair_pos), _index(flat_pair)
+    n_pairs = pair_pos.numel()
+    n_flat = flat_pair.numel()
+    V, d = weight2.shape
+    dev = rows2.device
+    out = torch.zeros(n_flat, 2, dtype=torch.float32, device=dev)
+    lse = torch.zeros(n_pairs, 2, dtype=torch.float32, device=dev)
+    g = torch.zeros(n_pairs, dtype=torch.float32, device=dev)
+    loss = torch.zeros((), dtype=torch.float32, device=dev)
+    grad_rows = torch.zeros_like(rows) if need_rows else rows.new_empty(0)
+    grad_w = (torch.zeros_like(weight) if n_pairs == 0 else torch.empty_like(weight)) if need_weight \
+        else weight.new_empty(0)
+    f = lambda t: None if t is None else t.float().contiguous().reshape(-1)  # noqa: E731
+    prox_, old_, adv_, mask_ = f(prox), f(old), f(adv), f(mask)
+    tail = _lib.GrpoTail(_p(prox_), _p(old_), _p(adv_), _p(mask_), adv_.numel(), eps_lo, eps_hi, reject_upper,
+                         _p(g), _p(loss))
+    w_code = _dtype_code(weight2)
+    ws_flags = _lib.WS_STEP | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, pair_pos)
+    nbytes = _lib.workspace_bytes(n_pairs, d, V, w_code, ws_flags)
+    if STEP_WORKSPACE_BYTES is not None:
+        nbytes = int(STEP_WORKSPACE_BYTES)
+    ws = _workspace(nbytes, rows2)
+    gh = torch.empty(n_pairs, d, dtype=rows2.dtype, device=dev) if need_rows and n_pairs else None
+    _lib.call("octo_head_step_grpo_pairs", _p(rows2), rows2.shape[0], rows2.stride(0), _dtype_code(rows2),
+              _p(weight2), weight2.stride(0), w_code, _p(w_scale), _p(pair_label), _p(pair_pos), _p(pair_count),
+              n_pairs, d, V, _lib.LSE_PAIR, inv_T, pre, post, int(use_tanh), _p(lse), _p(flat_pair), n_flat,
+              _p(out), 2, ctypes.byref(tail), _p(gh), d, _dtype_code(rows2) if need_rows else _lib.F32,
+              _p(grad_w if need_weight else None), _dtype_code(grad_w) if need_weight else _lib.F32,
+              _p(ws), ws.numel(), _stream(rows2))
+    if gh is not None:  # pair rows of one tree position (pair_pos ascending) summed into that position
+        _lib.call("octo_rows_scatter", _p(gh), d, _dtype_code(gh), _p(pair_pos), _p(pair_count), n_pairs, d,
+                  _p(grad_rows), grad_rows.stride(0), _dtype_code(grad_rows), 0, _stream(rows2))
+    return out, lse, g, loss, grad_rows, grad_w
+
+
+@head_step_grpo_pairs.register_fake
+def _(rows, weight, w_scale, pair_label, pair_pos, pair_count, flat_pair, inv_T, pre, post, use_tanh, prox, old, adv,
+      mask, eps_lo, eps_hi, reject_upper, need_rows, need_weight):
+    n_pairs = pair_pos.shape[0]
+    return (rows.new_empty(flat_pair.shape[0], 2, dtype=torch.float32),
+            rows.new_empty(n_pairs, 2, dtype=torch.float32), rows.new_empty(n_pairs, dtype=torch.float32),
+            rows.new_empty((), dtype=torch.float32),
+            torch.empty_like(rows) if need_rows else rows.new_empty(0),
+            torch.empty_like(weight) if need_weight else weight.new_empty(0))
+
+
 def _step_setup(ctx, inputs, output):
     _out, _lse, _g, _loss, grad_rows, grad_w = output
     ctx.save_for_backward(grad_rows, grad_w)
-    ctx.need = (inputs[19], inputs[20])
+    ctx.need = (inputs[-2], inputs[-1])  # need_rows, need_weight: the ops' last two arguments
+    ctx.n_inputs = len(inputs)
 
 
 def _step_backward(ctx, _gout, _glse, _gg, gloss, _ggr, _ggw):
@@ -284,10 +342,11 @@ def _step_backward(ctx, _gout, _glse, _gg, gloss, _ggr, _ggw):
     need_rows, need_weight = ctx.need
     gr = grad_rows * gloss.to(grad_rows.dtype) if need_rows and ctx.needs_input_grad[0] else None
     gw = grad_w * gloss.to(grad_w.dtype) if need_weight and ctx.needs_input_grad[1] else None
-    return (gr, gw) + (None,) * 19
+    return (gr, gw) + (None,) * (ctx.n_inputs - 2)
 
 
 torch.library.register_autograd("octohead::head_step_grpo", _step_backward, setup_context=_step_setup)
+torch.library.register_autograd("octohead::head_step_grpo_pairs", _step_backward, setup_context=_step_setup)
 
 
 def _head_setup(ctx, inputs, output):
@@ -356,6 +415,28 @@ def fused_grpo_head(rows: Tensor, weight: Tensor, labels: Tensor, temperature: f
         bool(post.tanh), labels_via_idx, scatter, prox, old, adv, mask, float(eps_lo), float(eps_hi),
         float(reject_upper), need_rows, need_weight)
     return loss, out.detach()
+
+
+def fused_grpo_tree_head(hidden: Tensor, weight: Tensor, meta, temperature: float, adv: Tensor, mask: Tensor, *,
+                         prox: Optional[Tensor] = None, old: Optional[Tensor] = None, post: Post = Post(),
+                         w_scale: Optional[Tensor] = None, eps_lo: float = 0.2, eps_hi: float = 0.28,
+                         reject_upper: float = 5.0) -> tuple[Tensor, Tensor]:
+    """fused_grpo_head over a prefix tree (the tree_head_output form, prefix_tree.py:416-421): hidden [1, T_tree, H]
+    or [T_tree, H], the head run on the tree's deduplicated (position, label) pair rows of `meta` (a TreeMeta, pairs
+    built on the host or on the device), the GRPO objective over the flat tokens (prox, old, adv, mask per flat
+    token). Returns (loss, out [1, T_flat, 2]): each flat token's (logprob, entropy), 0 where it has no pair,
+    detached; loss.backward() gives hidden and weight their gradients (a pair row's summed over its flat tokens)."""
+    if temperature <= 0:
+        raise ValueError("temperature must be positive")
+    rows = hidden[0] if hidden.dim() == 3 else hidden
+    grad_on = torch.is_grad_enabled()
+    need_rows = grad_on and hidden.requires_grad
+    need_weight = grad_on and weight.requires_grad
+    out, _lse, _g, loss, _gr, _gw = head_step_grpo_pairs(
+        rows, weight, w_scale, meta.pair_label, meta.pair_pos, meta.pair_count, meta.flat_pair,
+        1.0 / float(temperature), float(post.pre), float(post.post), bool(post.tanh), prox, old, adv, mask,
+        float(eps_lo), float(eps_hi), float(reject_upper), need_rows, need_weight)
+    return loss, out.detach().unsqueeze(0)
 
 
 # ---- _head_columns over materialised logits ------------------------------------------------------

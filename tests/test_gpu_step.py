@@ -314,3 +314,86 @@ def test_fused_grpo_head_autograd_matches_the_two_call_route():
     with torch.no_grad():
         loss3, out3 = fused_grpo_head(h1, W1, yd, T, advd, maskd, prox=old, **kw)
     assert torch.equal(out3, out1) and not loss3.requires_grad
+
+
+def _tree_batch(seed, n_seq=5, prefix=600, V=4096, d=256):
+    """A packed prefix tree (sequences sharing a prefix, random continuations), its per-flat-token GRPO inputs."""
+    from octopus_amd.rl.prefix_tree import build_tree
+    rng = np.random.default_rng(seed)
+    pre = rng.integers(0, V, prefix)
+    seqs = [np.concatenate([pre, rng.integers(0, V, int(k))]) for k in rng.integers(100, 900, n_seq)]
+    cu = np.concatenate([[0], np.cumsum([len(s) for s in seqs])])
+    flat = np.concatenate(seqs)
+    scored = rng.random(len(flat)) < 0.7
+    tree = build_tree(flat, cu, scored=scored)
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(len(tree.tokens), d, generator=g)
+    h = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    W = (torch.randn(V, d, generator=g) * 0.02).to(torch.bfloat16)
+    seq_of = np.repeat(np.arange(n_seq), np.diff(cu))
+    adv = torch.from_numpy(rng.standard_normal(n_seq)[seq_of]).float()
+    mask = torch.from_numpy((scored & (rng.random(len(flat)) < 0.9)).astype(np.float32))
+    return flat, cu, scored, tree, h, W, adv, mask
+
+
+@pytest.mark.parametrize("device_pairs", [False, True], ids=["host_pairs", "device_pairs"])
+@pytest.mark.parametrize("passes", [1, 3])
+def test_tree_step_matches_the_two_call_tree_route_and_oracle(device_pairs, passes):
+    """fused_grpo_tree_head over a prefix tree's pair rows: each flat token's columns bitwise the two-call tree route's
+    (tree_head_output over the bound head), the loss to summation order, the gradients of hidden (pair rows summed
+    into tree positions) and W against that route's autograd (fused_head, pairs_expand, grpo_loss, backward) and
+    against the fp64 oracle with each pair row's g the sum of its flat tokens' GRPO weights (oracle/grpo.py);
+    pairs built on the host (no-pair as the appended row P) and on the device (P on the device, no-pair -1), in one
+    pass and in three."""
+    from octopus_amd.head_op import fused_grpo_tree_head, fused_head
+    from octopus_amd.rl.prefix_tree import TreeMeta, tree_head_output
+    flat, cu, scored, tree, h, W, adv, mask = _tree_batch(101)
+    T = 0.8
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)  # noqa: E731
+    meta = (TreeMeta.on_device(t(flat), t(np.asarray(cu)), t(tree.flat_to_tree), len(tree.tokens), t(scored))
+            if device_pairs else TreeMeta(tree, DEV))
+    P = len(tree.pair_pos)
+    ws = None
+    if passes > 1:
+        n_max = meta.pair_pos.numel()
+        ws, plan = _step_ws(n_max, h.shape[1], W.shape[0], _lib.BF16, 0, lambda p: p[1] == passes)
+    Wd0 = W.to(DEV)
+
+    def route(hd, Wd):
+        def chunk(rows, labels):
+            return fused_head(rows, Wd, labels, T)
+        chunk.octopus_fused_rows = lambda h2, pos, y, count=None: fused_head(h2, Wd, y, T, idx=pos, count=count)
+        return tree_head_output(chunk, hd, meta)
+
+    out0 = route(h.to(DEV)[None], Wd0)
+    prox = (out0[0, :, 0] + 0.05 * torch.randn(len(flat), generator=torch.Generator().manual_seed(3)).to(DEV))
+    prox = prox.detach()
+    advd, maskd = adv.to(DEV), mask.to(DEV)
+
+    h1, W1 = h.to(DEV)[None].requires_grad_(True), Wd0.clone().requires_grad_(True)
+    head_op.STEP_WORKSPACE_BYTES = ws
+    try:
+        loss1, out1 = fused_grpo_tree_head(h1, W1, meta, T, advd, maskd, prox=prox)
+    finally:
+        head_op.STEP_WORKSPACE_BYTES = None
+    loss1.backward()
+    h2, W2 = h.to(DEV)[None].requires_grad_(True), Wd0.clone().requires_grad_(True)
+    out2 = route(h2, W2)
+    loss2, _ = head_op.grpo_loss(out2[0, :, 0], prox, None, advd, maskd, *EPS)
+    loss2.backward()
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2.detach())
+    assert abs(loss1.item() - loss2.item()) <= 1e-5 * max(1.0, abs(loss2.item()))
+    assert _rel(h1.grad, h2.grad) <= 4e-3 and _rel(W1.grad, W2.grad) <= 4e-3
+    # the oracle: g per pair row = the sum of its flat tokens' weights, the gradients of the pair rows scattered
+    lp_flat = out1[0, :, 0].cpu().double().numpy()
+    _, g_flat = ogrpo.grpo(lp_flat, adv.numpy(), mask.numpy(), prox=prox.double().cpu().numpy())
+    fp = tree.flat_pair
+    g_pair = np.zeros(P)
+    np.add.at(g_pair, fp[fp >= 0], g_flat[fp >= 0])
+    rows = h[torch.from_numpy(tree.pair_pos)]
+    gh_pairs, gw_ref = ohead.head_backward(rows, W.float(), torch.from_numpy(tree.pair_label), T,
+                                           torch.from_numpy(g_pair))
+    gh_ref = torch.zeros(len(tree.tokens), h.shape[1], dtype=torch.float64)
+    gh_ref.index_add_(0, torch.from_numpy(tree.pair_pos), gh_pairs)
+    assert _rel(h1.grad[0].cpu(), gh_ref) <= 1e-2 and _rel(W1.grad.cpu(), gw_ref) <= 1e-2
