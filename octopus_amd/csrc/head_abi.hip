@@ -280,15 +280,17 @@ struct StepLayout {
   size_t part, z, hit, rowout, ht, dz, wide, wt, gacc, rows, total;
 };
 
-// Rows per pass for a step without grad_W: each pass's grad_h launch is one tile per CU per round of long tiles (K =
-// V), so a pass whose tiles overrun a multiple of the 256 CUs pays a whole extra round for the overrun. Of the pass
-// sizes up to pmax (multiples of 256), the one whose passes take the fewest grad_h rounds in total, the largest on a
-// tie: at d 2560 and 131,072 rows, 25 x 256 rows (250 tiles, 21 passes, 21 rounds) against 27 x 256 (270 tiles,
-// 19 passes, 38 rounds). With grad_W the two gradients share one launch, whose short grad_W tiles fill those rounds.
+// Rows per pass when grad_h is asked for: each pass's grad_h is one tile per CU per round of long tiles (K = V), so
+// a pass whose tiles overrun a multiple of the 256 CUs pays a whole extra round for the overrun, with or without
+// grad_W's short tiles beside them in the same launch (those fill the CUs the long tiles leave, but cannot start the
+// overrun early). Of the pass sizes up to pmax (multiples of 256), the one whose passes take the fewest grad_h rounds
+// in total, the largest (up to the rows there are) on a tie: at d 2560 and 131,072 rows, 25 x 256 rows (250 tiles, 21 passes, 21 rounds)
+// against 27 x 256 (270 tiles, 19 passes, 38 rounds); at 32,768 rows, 25 x 256 (6 passes, 6 rounds) against
+// 26 x 256 (260 tiles: 5 passes, 9 rounds).
 int64_t gradh_pass_rows(int64_t n_max, int d, int64_t pmax) {
   const int64_t nt = cdiv(n_max, TN), nd = cdiv(d, TN), cus = 256;
   int64_t best_p = 0, best_r = 0;
-  for (int64_t p = pmax / TN; p >= 1; --p) {
+  for (int64_t p = (pmax / TN < nt ? pmax / TN : nt); p >= 1; --p) {
     const int64_t passes = cdiv(nt, p), last = nt - (passes - 1) * p;
     const int64_t r = (passes - 1) * cdiv(p * nd, cus) + cdiv(last * nd, cus);
     if (!best_p || r < best_r) {
@@ -315,7 +317,7 @@ bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need
   }
   L.passes = n_max > 0 ? cdiv(n_max, pmax) : 0;
   L.P = n_max > 0 ? round_up(cdiv(n_max, L.passes), TN) : 0;
-  if (n_max > 0 && need_gh && !need_gw) L.P = gradh_pass_rows(n_max, d, pmax);
+  if (n_max > 0 && need_gh) L.P = gradh_pass_rows(n_max, d, pmax);
   L.passes = n_max > 0 ? cdiv(n_max, L.P) : 0;
   L.gacc_on = need_gw && L.passes > 1;
   L.wide_on = w_dtype == OCTO_FP8E4M3;

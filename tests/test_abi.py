@@ -143,26 +143,26 @@ def _gradh_rounds(n, d, p_tiles):
 def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     """The fused step's workspace at the default plan: one pass's [rows, V_pad] exponentials (then dz) within the
     2 GiB staging budget, plus that pass's statistics, h^T and label entries, each row's columns (for pair rows),
-    fp32 grad_W partials over several passes, and once per call the widened fp8 weights or W^T. Rows per pass: the most the budget holds, balanced;
-    without grad_W, the size whose passes take the fewest grad_h rounds."""
+    fp32 grad_W partials over several passes, and once per call the widened fp8 weights or W^T. Rows per pass: the
+    size up to what the budget holds whose passes take the fewest grad_h rounds."""
     ws = _lib.workspace_bytes(n, d, V, w, _lib.WS_STEP | flags)
     P, passes, Vp, one = _lib.bwd_plan(n, d, V, w, _lib.WS_STEP | flags, ws)
     assert Vp == (V + 255) // 256 * 256 and one == 1
     assert P % 256 == 0 and P * Vp * 2 <= BUDGET and passes == -(-n // P)
     need_gw = not flags & _lib.WS_NO_GRADW
     pmax = min(32768, BUDGET // (Vp * 2) // 256 * 256)
-    if need_gw:
-        assert P == -(-(-(-n // -(-n // pmax))) // 256) * 256
-    else:
-        best = min(_gradh_rounds(n, d, p) for p in range(1, pmax // 256 + 1))
-        assert _gradh_rounds(n, d, P // 256) == best
-        assert all(_gradh_rounds(n, d, p) > best for p in range(P // 256 + 1, pmax // 256 + 1))
+    top = min(pmax // 256, -(-n // 256))
+    best = min(_gradh_rounds(n, d, p) for p in range(1, top + 1))
+    assert _gradh_rounds(n, d, P // 256) == best
+    assert all(_gradh_rounds(n, d, p) > best for p in range(P // 256 + 1, top + 1))
     extra = (P * ((V + 255) // 256) * 16 + P * 4 + n * 8 + (d * P * 2 if need_gw else 0) +
              (V * d * 4 if need_gw and passes > 1 else 0) + (V * d * 2 if w == _lib.FP8E4M3 else 0) +
              (d * Vp * 2 if V % 64 or d % 256 else 0))
     assert P * Vp * 2 <= ws <= P * Vp * 2 + extra + (1 << 20), (ws, extra)
     if n == 131072:
         assert (P, passes) == (6400, 21)  # 21 grad_h rounds, against 38 for 27 x 256 rows
+    if (n, d) == (32768, 2560):
+        assert (P, passes) == (6400, 6)  # 250 grad_h tiles a pass: one round each
 
 
 def test_step_plan_follows_the_workspace_and_fp32_falls_back():
