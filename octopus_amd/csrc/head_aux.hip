@@ -231,11 +231,19 @@ int launch_hit(const HitArgs &a, hipStream_t st) {
 }
 
 // ---- dz from the stored exponentials (the fused step) ---------------------------------------------------
-// One workgroup per (row, 8,192 columns): 4 x 16 bytes per thread, loaded together, scaled by the row's factor for
-// their vocabulary tile (8 columns never straddle a 256-column tile), the label entry replaced, stored back. The
+// One workgroup per (row, 4,096 columns): 2 x 16 bytes per thread, loaded together, scaled by the row's factor for
+// their half tile (8 columns never straddle a 128-column half tile), the label entry replaced, stored back. The
 // row's state is uniform over the workgroup (scalar loads). Non-temporal: the rows are read back only by the
-// gradient GEMMs, after the rest of the pass's [rows, V] has streamed through.
-constexpr int kScaleChunks = 4;  // 16-byte chunks per thread
+// gradient GEMMs, after the rest of the pass's [rows, V] has streamed through. Same box, 24,576 rows at V 151,936 and
+// 114,688 at fp8: 2 chunks per thread 2.50 and 12.2 ms per step, against 2.73 and 15.0 for 4, 2.60 and 13.5 for 1,
+// 31.7 ms at fp8 for 8; temporal loads 2.52 and 13.0.
+#ifndef OCTO_SCALE_CHUNKS
+#define OCTO_SCALE_CHUNKS 2
+#endif
+#ifndef OCTO_SCALE_NT_LOAD
+#define OCTO_SCALE_NT_LOAD 1
+#endif
+constexpr int kScaleChunks = OCTO_SCALE_CHUNKS;  // 16-byte chunks per thread
 
 __global__ __launch_bounds__(256) void dz_scale_kernel(DzScaleArgs a) {
   const int64_t i = blockIdx.y;  // row of the pass
@@ -254,7 +262,8 @@ __global__ __launch_bounds__(256) void dz_scale_kernel(DzScaleArgs a) {
 #pragma unroll
   for (int k = 0; k < kScaleChunks; ++k) {
     const int64_t c0 = (chunk0 + 256 * k) * 8;
-    if (c0 < a.V_pad) v[k] = __builtin_nontemporal_load((const i32x4 *)(row + c0 * 2));
+    if (c0 < a.V_pad)
+      v[k] = OCTO_SCALE_NT_LOAD ? __builtin_nontemporal_load((const i32x4 *)(row + c0 * 2)) : *(const i32x4 *)(row + c0 * 2);
   }
 #pragma unroll
   for (int k = 0; k < kScaleChunks; ++k) {
