@@ -264,6 +264,30 @@ def test_step_dispatch_checks_before_queueing():
         step(P, P, lse=None)
 
 
+def test_step_pairs_checks_before_queueing():
+    """octo_head_step_grpo_pairs on the host: labels are per pair row (no idx-based flags), 16-bit operands only, the
+    flat-token arrays must be there, and the workspace is the step's; nothing is queued in any of these."""
+    tail = _lib.GrpoTail(P, None, P, P, 10, 0.2, 0.28, 5.0, P, None)
+
+    def step(flags=_lib.LSE_PAIR, dtype=_lib.BF16, flat=P, out=P, ld_out=2, pos=P):
+        _lib.call("octo_head_step_grpo_pairs", P, 10, 64, dtype, P, 64, dtype, None, P, pos, None, 10, 64, 100, flags,
+                  1.0, 1.0, 1.0, 0, P, flat, 10, out, ld_out, ctypes.byref(tail), P, 64, dtype, P, dtype, None, 0,
+                  None)
+
+    with pytest.raises(ValueError, match="per pair row"):
+        step(flags=_lib.LSE_PAIR | _lib.ROWS_VIA_IDX)
+    with pytest.raises(ValueError, match="flat_pair, out_flat or ld_out"):
+        step(flat=None)
+    with pytest.raises(ValueError, match="flat_pair, out_flat or ld_out"):
+        step(ld_out=1)
+    with pytest.raises(ValueError, match="null pair_pos"):
+        step(pos=None)
+    with pytest.raises(NotImplementedError):
+        step(dtype=_lib.F32)
+    with pytest.raises(ValueError, match="head_step_grpo: workspace"):
+        step()
+
+
 def test_timing_hook_without_launches():
     """The timing hook records nothing until a GEMM is launched, and reading an unknown name is not an error."""
     _lib.call("octo_timing_enable", 1)
