@@ -396,3 +396,36 @@ def test_tree_step_matches_the_two_call_tree_route_and_oracle(device_pairs, pass
     gh_ref = torch.zeros(len(tree.tokens), h.shape[1], dtype=torch.float64)
     gh_ref.index_add_(0, torch.from_numpy(tree.pair_pos), gh_pairs)
     assert _rel(h1.grad[0].cpu(), gh_ref) <= 1e-2 and _rel(W1.grad.cpu(), gw_ref) <= 1e-2
+
+
+def test_step_hidden_of_more_than_2_gib_through_idx():
+    """The fused step over a 2.2 GB bf16 hidden matrix read through the compaction (its compact rows gathered into the
+    workspace first, OCTO_WS_GATHER): 70,000 scored rows of 270,000 in passes of the step's plan, against the chunked
+    fp32 reference with the step's own GRPO weight."""
+    from octopus_amd.head_op import fused_grpo_head
+    from tests.gpu_reference import head_fp32
+    rows_total, d, V = 270_000, 4096, 1000
+    gen = torch.Generator(device=DEV).manual_seed(52)
+    h = torch.randn(rows_total, d, device=DEV, generator=gen)
+    h = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    W = (torch.randn(V, d, device=DEV, generator=gen) * 0.02).to(torch.bfloat16)
+    y = torch.randint(0, V, (rows_total,), device=DEV, generator=gen)
+    scored = torch.zeros(rows_total, dtype=torch.bool, device=DEV)
+    scored[torch.randperm(rows_total, device=DEV, generator=gen)[:70_000]] = True
+    adv = torch.randn(rows_total, device=DEV, generator=gen)
+    prox = -7.0 + 0.1 * torch.randn(rows_total, device=DEV, generator=gen)
+    idx, count = head_op.compact_rows(scored)
+    assert h.numel() * 2 >= 1 << 31 and head_op._gather_flag(h, idx) == _lib.WS_GATHER
+    a, b = h.requires_grad_(True), W.clone().requires_grad_(True)
+    loss, out = fused_grpo_head(a, b, y, 1.0, adv, scored.float(), prox=prox, idx=idx, count=count,
+                                labels_via_idx=True, scatter=True)
+    loss.backward()
+    n = int(count.item())
+    sel = idx[:n]
+    _, g_flat = ogrpo.grpo(out[:, 0].double().cpu().numpy(), adv.double().cpu().numpy(), scored.cpu().numpy(),
+                           prox=prox.double().cpu().numpy())
+    g = torch.from_numpy(g_flat).float().to(DEV)[sel]
+    lp, ent, gr, gw = head_fp32(h.detach()[sel], W.float(), y[sel], 1.0, g=g)
+    assert (out[sel, 0] - lp).abs().max().item() <= 2e-3 and (out[sel, 1] - ent).abs().max().item() <= 2e-3
+    assert _rel(a.grad[sel], gr) <= 1e-2 and _rel(b.grad, gw) <= 1e-2
+    assert (a.grad[~scored] == 0).all()
