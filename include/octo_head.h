@@ -94,13 +94,15 @@ int octo_timing_read(const char *kernel, int *launches, double *total_ms);
  * 2 GiB or more (h_rows * ldh * element bytes >= 2^31) is first gathered into the workspace (the GEMMs address
  * mapped rows with 32-bit offsets): add OCTO_WS_GATHER for those calls.
  * Backward: the size of its plan at a 2 GiB staging budget (see octo_head_bwd); a smaller workspace is accepted
- * down to the plan at a 1 MiB budget, a larger one may run fewer chunks. */
+ * down to the plan at a 1 MiB budget, a larger one may run fewer chunks. OCTO_WS_STEP [| OCTO_WS_NO_GRADW]: the
+ * same for octo_head_step_grpo and octo_head_step_grpo_pairs (n_max = the pair rows), whose plan has row passes
+ * only; for fp32 operands the larger of the forward's and the backward's. */
 int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes);
 
 /* The chunking octo_head_bwd runs in ws_bytes of workspace (a planning aid; no counterpart in the reference):
  * plan[0] rows per pass, plan[1] passes, plan[2] vocabulary columns per chunk, plan[3] chunks. flags as for
- * octo_head_workspace_bytes (OCTO_WS_NO_GRADW, OCTO_WS_GATHER); grad_h is assumed asked for.
- * OCTO_EWORKSPACE when no plan fits. */
+ * octo_head_workspace_bytes (OCTO_WS_NO_GRADW, OCTO_WS_GATHER); grad_h is assumed asked for. With OCTO_WS_STEP, the
+ * fused step's plan: {rows per pass, passes, V rounded up to 256, 1}. OCTO_EWORKSPACE when no plan fits. */
 int octo_head_bwd_plan(int64_t n_max, int d, int V, int w_dtype, int flags, size_t ws_bytes, int64_t plan[4]);
 
 /* Masked-row compaction (lm_head.py:128 `scored.nonzero()[:, 0]`): idx[0..count) = the positions
