@@ -330,7 +330,9 @@ def _(rows, weight, w_scale, pair_label, pair_pos, pair_count, flat_pair, inv_T,
 
 def _step_setup(ctx, inputs, output):
     _out, _lse, _g, _loss, grad_rows, grad_w = output
-    ctx.save_for_backward(grad_rows, grad_w)
+    # Held on ctx as detached aliases, not saved: an activation-offload pack hook (saved_tensors_hooks) would otherwise
+    # copy the [V, d] weight gradient to the host and back, and the aliases carry no grad_fn back to this node.
+    ctx.grads = (grad_rows.detach(), grad_w.detach())
     ctx.need = (inputs[-2], inputs[-1])  # need_rows, need_weight: the ops' last two arguments
     ctx.n_inputs = len(inputs)
 
@@ -338,7 +340,7 @@ def _step_setup(ctx, inputs, output):
 def _step_backward(ctx, _gout, _glse, _gg, gloss, _ggr, _ggw):
     """The loss is the only differentiable output: its gradients were computed by the forward call, scaled here by
     the incoming gradient of the loss (1 for loss.backward())."""
-    grad_rows, grad_w = ctx.saved_tensors
+    grad_rows, grad_w = ctx.grads
     need_rows, need_weight = ctx.need
     gr = grad_rows * gloss.to(grad_rows.dtype) if need_rows and ctx.needs_input_grad[0] else None
     gw = grad_w * gloss.to(grad_w.dtype) if need_weight and ctx.needs_input_grad[1] else None

@@ -315,3 +315,28 @@ def test_gather_flag_asks_for_the_row_copy_only_past_2_gib_through_idx():
     assert _gather_flag(big, idx) == _lib.WS_GATHER
     assert _gather_flag(wide, idx) == _lib.WS_GATHER
     assert _gather_flag(big, None) == 0  # without idx each tile's rows are addressed from their own base
+
+
+def test_the_fused_step_saves_no_weight_gradient_for_backward():
+    """The fused GRPO step computes both gradients in its forward call and holds them for the backward on the autograd
+    context, out of a pack hook's reach: saved_tensors_hooks sees no [V, d] tensor (meta tensors through the op's fake
+    kernels; no GPU), and loss.backward() still gives rows and weight their gradients."""
+    from octopus_amd import head_op
+    V, d, n = 1000, 64, 32
+    rows = torch.empty(n, d, device="meta", dtype=torch.bfloat16, requires_grad=True)
+    W = torch.empty(V, d, device="meta", dtype=torch.bfloat16, requires_grad=True)
+    labels = torch.empty(n, device="meta", dtype=torch.int64)
+    adv = torch.empty(n, device="meta", dtype=torch.float32)
+    mask = torch.empty(n, device="meta", dtype=torch.bool)
+    packed = []
+
+    def pack(t):
+        packed.append(tuple(t.shape))
+        return t
+
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+        loss, out = head_op.fused_grpo_head(rows, W, labels, 0.9, adv, mask)
+    assert (V, d) not in packed and (n, d) not in packed, packed
+    assert out.shape == (n, 2) and not out.requires_grad
+    loss.backward()
+    assert W.grad.shape == (V, d) and rows.grad.shape == (n, d)
