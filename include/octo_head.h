@@ -13,7 +13,10 @@
  *   - returns an int status (OCTO_OK or a negative OCTO_E* code) and never throws;
  *     octo_last_error() gives a message for the last failing call on the calling thread;
  *   - takes plain device pointers, element strides and sizes, and an explicit hipStream_t
- *     (passed as void* so that the header needs no HIP include); all work is queued on that stream;
+ *     (passed as void* so that the header needs no HIP include); all work is queued on that stream.
+ *     Outputs and the workspace are ordinary device memory (hipMalloc, coarse-grained): sums into
+ *     fp32 outputs (the loss, grad_W accumulated across row passes or into the caller's fp32 gradient)
+ *     use the GPU's hardware float atomics, which fine-grained (host-coherent) memory does not take;
  *   - allocates no device memory: scratch memory comes from a caller-provided workspace whose size the
  *     matching *_workspace_bytes query returns (the one exception is the timing hook below, which
  *     creates HIP events while it is enabled);
