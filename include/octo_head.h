@@ -267,8 +267,10 @@ int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
  * Workspace: octo_head_workspace_bytes with OCTO_WS_STEP [| OCTO_WS_NO_GRADW | OCTO_WS_GATHER], the plan at a
  * 2 GiB staging budget ([rows, V] of one pass); outside the staging are the pass's statistics per vocabulary tile,
  * h^T of a pass, fp32 grad_w partials [V, d] over several passes, and once per call W widened to bf16 (fp8 weights)
- * or W^T (16-bit weights with V % 64 or d % 256 not 0). A smaller workspace is accepted down to the plan at a
- * 1 MiB budget; octo_head_bwd_plan with OCTO_WS_STEP gives {rows per pass, passes, V rounded up to 256, 1}.
+ * and W^T (16-bit weights with V % 64 or d % 256 not 0; and, for speed, when grad_h is the only gradient and
+ * n_max >= 16,384). A smaller workspace is accepted down to the plan at a 1 MiB budget (without the optional W^T
+ * first, before smaller passes); octo_head_bwd_plan with OCTO_WS_STEP gives {rows per pass, passes, V rounded up
+ * to 256, 1}.
  * fp32 operands run octo_head_fwd_grpo, then octo_head_bwd, in the same workspace. With grad_h and grad_w both
  * NULL the call is octo_head_fwd_grpo (whose workspace size then suffices). */
 int octo_head_step_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,

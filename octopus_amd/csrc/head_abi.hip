@@ -301,10 +301,18 @@ int64_t gradh_pass_rows(int64_t n_max, int d, int64_t pmax) {
   return best_p * TN;
 }
 
+// grad_h reads W^T K-contiguous faster than W K-major (its B fragments one ds_read_b128 each rather than two
+// transposing reads): 57.3 against 60.3 ms per step at 114,688 rows, d 2560, V 151,936 (grad_h alone, fp8 weights
+// widened), for a transpose of the weight once per call (about 0.3 ms at 0.78 GB). Beside grad_W in the same launch
+// the gain is smaller (24,576 rows: the launches 0.4 ms faster, the step equal), so W^T is staged by choice only when
+// grad_h is the only gradient and the rows reach kWtRows.
+constexpr int64_t kWtRows = 16384;
+
 // False when the budget holds fewer than 256 rows, or for fp32 operands (the step then runs the forward and the
-// backward: step_fallback).
+// backward: step_fallback). opt_wt: stage W^T where it pays (kWtRows); it is staged regardless where grad_h cannot
+// read W as stored.
 bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw, bool gather, size_t budget,
-               StepLayout &L) {
+               StepLayout &L, bool opt_wt = true) {
   L.esz = elem_bytes(staged_dtype(w_dtype));
   if (L.esz != 2) return false;
   L.mtiles = cdiv(V, TM);
@@ -321,7 +329,7 @@ bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need
   L.passes = n_max > 0 ? cdiv(n_max, L.P) : 0;
   L.gacc_on = need_gw && L.passes > 1;
   L.wide_on = w_dtype == OCTO_FP8E4M3;
-  L.wt_on = need_gh && !gh_reads_w(d, V, w_dtype);
+  L.wt_on = need_gh && (!gh_reads_w(d, V, w_dtype) || (opt_wt && !need_gw && n_max >= kWtRows));
   size_t off = 0;
   L.part = off;  // (m, S, U) per (row of the pass, vocabulary tile)
   off += align_up((size_t)L.P * L.mtiles * sizeof(f32x4));
@@ -337,7 +345,7 @@ bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need
   off += align_up((size_t)L.P * L.V_pad * L.esz);
   L.wide = off;  // fp8 weights widened to bf16 [V, d]
   if (L.wide_on) off += align_up((size_t)V * d * 2);
-  L.wt = off;  // W^T [d, V_pad] (grad_h, when it cannot read W K-major)
+  L.wt = off;  // W^T [d, V_pad] (grad_h: when it cannot read W K-major, or by choice)
   if (L.wt_on) off += align_up((size_t)d * L.V_pad * L.esz);
   L.gacc = off;  // fp32 grad_W partial sums across passes
   if (L.gacc_on) off += align_up((size_t)V * d * sizeof(float));
@@ -347,13 +355,16 @@ bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need
   return true;
 }
 
-// The plan the step runs in ws_bytes: unbounded if it fits, else the largest candidate staging budget that fits.
+// The plan the step runs in ws_bytes: unbounded if it fits, else the largest candidate staging budget that fits; at
+// each budget the optional W^T first, then without it (a workspace short of the W^T keeps the larger passes).
 bool step_plan_for(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need_gw, bool gather,
                    size_t ws_bytes, StepLayout &L) {
-  if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, 0, L) && L.total <= ws_bytes) return true;
-  for (int q = kBudgetQMax; q >= kBudgetQMin; --q)
-    if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, staging_candidate(q), L) && L.total <= ws_bytes)
-      return true;
+  for (int q = kBudgetQMax + 1; q >= kBudgetQMin; --q) {
+    const size_t budget = q > kBudgetQMax ? 0 : staging_candidate(q);
+    for (int opt = 1; opt >= 0; --opt)
+      if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, budget, L, opt != 0) && L.total <= ws_bytes)
+        return true;
+  }
   return false;
 }
 
@@ -718,7 +729,8 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     StepLayout Lmin;
     size_t least = 0;
     for (int q = kBudgetQMin; q <= kBudgetQMax && !least; ++q)
-      if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, cm.gather, staging_candidate(q), Lmin)) least = Lmin.total;
+      if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, cm.gather, staging_candidate(q), Lmin, false))
+        least = Lmin.total;
     return octo_fail(OCTO_EWORKSPACE, "head_step_grpo: workspace %zu bytes, below the smallest plan's %zu%s",
                      ws ? ws_bytes : (size_t)0, least,
                      cm.gather ? " (hidden of 2 GiB or more through idx: query with OCTO_WS_GATHER)" : "");

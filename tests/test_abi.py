@@ -143,8 +143,9 @@ def _gradh_rounds(n, d, p_tiles):
 def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     """The fused step's workspace at the default plan: one pass's [rows, V_pad] exponentials (then dz) within the
     2 GiB staging budget, plus that pass's statistics, h^T and label entries, each row's columns (for pair rows),
-    fp32 grad_W partials over several passes, and once per call the widened fp8 weights or W^T. Rows per pass: the
-    size up to what the budget holds whose passes take the fewest grad_h rounds."""
+    fp32 grad_W partials over several passes, and once per call the widened fp8 weights and W^T (where grad_h cannot
+    read W as stored, or grad_h alone over 16,384 rows or more). Rows per pass: the size up to what the budget holds
+    whose passes take the fewest grad_h rounds."""
     ws = _lib.workspace_bytes(n, d, V, w, _lib.WS_STEP | flags)
     P, passes, Vp, one = _lib.bwd_plan(n, d, V, w, _lib.WS_STEP | flags, ws)
     assert Vp == (V + 255) // 256 * 256 and one == 1
@@ -157,7 +158,7 @@ def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     assert all(_gradh_rounds(n, d, p) > best for p in range(P // 256 + 1, top + 1))
     extra = (P * ((V + 255) // 256) * 16 + P * 4 + n * 8 + (d * P * 2 if need_gw else 0) +
              (V * d * 4 if need_gw and passes > 1 else 0) + (V * d * 2 if w == _lib.FP8E4M3 else 0) +
-             (d * Vp * 2 if V % 64 or d % 256 else 0))
+             (d * Vp * 2 if V % 64 or d % 256 or (not need_gw and n >= 16384) else 0))
     assert P * Vp * 2 <= ws <= P * Vp * 2 + extra + (1 << 20), (ws, extra)
     if n == 131072:
         assert (P, passes) == (6400, 21)  # 21 grad_h rounds, against 38 for 27 x 256 rows
@@ -296,3 +297,15 @@ def test_timing_hook_without_launches():
     _lib.call("octo_timing_enable", 0)
     with pytest.raises(ValueError):
         _lib.call("octo_timing_read", None, None, None)
+
+
+def test_step_plan_keeps_its_passes_when_the_workspace_lacks_the_optional_w_transpose():
+    """grad_h alone over 16,384 rows or more stages W^T by choice; a workspace short of exactly that W^T gets the same
+    rows per pass without it, not smaller passes."""
+    n, d, V, w, fl = 131072, 2560, 151936, _lib.FP8E4M3, _lib.WS_STEP | _lib.WS_NO_GRADW
+    ws = _lib.workspace_bytes(n, d, V, w, fl)
+    Vp = (V + 255) // 256 * 256
+    full = _lib.bwd_plan(n, d, V, w, fl, ws)
+    assert _lib.bwd_plan(n, d, V, w, fl, ws - d * Vp * 2) == full
+    small = _lib.workspace_bytes(8192, d, V, w, fl)  # below 16,384 rows: no W^T
+    assert _lib.workspace_bytes(16384, d, V, w, fl) - small >= d * Vp * 2

@@ -175,6 +175,22 @@ def test_step_fp8_weights_to_hidden():
     _check(h, W32, y, scored, mask, adv, old, 1.0, (1.0, 1.0, False), step, two, False, 1e-2, 4e-3)
 
 
+@pytest.mark.parametrize("passes", [1, 3])
+def test_step_grad_h_alone_reads_a_staged_w_transpose(passes):
+    """grad_h as the only gradient over 16,384 rows or more: the step stages W^T once per call and grad_h reads it
+    K-contiguous (16-bit weights it could read as stored); in one pass and in three, against the two-call path and
+    the oracle."""
+    N, d, V = 20000, 256, 4096
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, torch.bfloat16, seed=97)
+    ws = None
+    if passes > 1:
+        ws, _ = _step_ws(N, d, V, _lib.BF16, _lib.WS_NO_GRADW, lambda p: p[1] == passes)
+    lp0 = head_op.head_fwd(h.to(DEV), W.to(DEV), None, y.to(DEV), None, None, 1.0, 1.0, 1.0, False, False, False)[0]
+    old = lp0[:, 0].cpu() + noise
+    idx, count, step, two = _run(h, W, y, scored, mask, adv, old, 1.0, need_w=False, ws=ws)
+    _check(h, W.float(), y, scored, mask, adv, old, 1.0, (1.0, 1.0, False), step, two, False, 1e-2, 4e-3)
+
+
 def test_step_extreme_logits():
     """Every row's hidden vector is e_0, so logit j is W[j, 0]: a 600-nat peak in the last vocabulary tile against
     logits in [-50, 50] (the other tiles' exponentials scale to exact zeros), and logits near -1,000 at T 0.7 (each
