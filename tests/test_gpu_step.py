@@ -299,6 +299,49 @@ def test_step_grad_w_accumulate_through_the_c_abi():
                   ctypes.byref(tail), P(gh), d, _lib.F32, P(gw), _lib.F32, P(ws), 1 << 20, st)
 
 
+def test_step_strided_rows_weight_and_grad_h_through_the_c_abi():
+    """Hidden rows, weight and grad_h as strided views (row strides past d, bases offset into wider buffers) through
+    the C ABI, over two passes: every output bitwise the contiguous call's (the same kernels and tile order, only the
+    addressing differs), the loss to summation order."""
+    n, d, V, T = 3000, 256, 4096, 0.8
+    h, W, y, _, _, adv, noise = _batch(n, d, V, torch.bfloat16, seed=96)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    hw = torch.zeros(n, d + 64, dtype=torch.bfloat16, device=DEV)
+    hw[:, 16:16 + d] = hd
+    Ww = torch.zeros(V, d + 128, dtype=torch.bfloat16, device=DEV)
+    Ww[:, 64:64 + d] = Wd
+    hs, Ws = hw[:, 16:16 + d], Ww[:, 64:64 + d]
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    old = (head_op.head_fwd(hd, Wd, None, yd, None, None, 1.0 / T, 1.0, 1.0, False, False, False)[0][:, 0].cpu()
+           + noise).to(DEV)
+    advd, maskd = adv.to(DEV), torch.ones(n, device=DEV)
+    wsb, plan = _step_ws(n, d, V, _lib.BF16, 0, lambda p: p[1] == 2)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+
+    def call(hx, Wx, gh, ld_gh):
+        out, lse, g = torch.zeros(n, 2, device=DEV), torch.zeros(n, 2, device=DEV), torch.zeros(n, device=DEV)
+        loss = torch.zeros((), device=DEV)
+        gw = torch.zeros(V, d, dtype=torch.bfloat16, device=DEV)
+        tail = _lib.GrpoTail(P(old), None, P(advd), P(maskd), n, *EPS, P(g), P(loss))
+        _lib.call("octo_head_step_grpo", P(hx), n, hx.stride(0), _lib.BF16, P(Wx), Wx.stride(0), _lib.BF16, None,
+                  P(yd), None, None, n, d, V, _lib.LSE_PAIR, 1.0 / T, 1.0, 1.0, 0, None, None, P(lse), P(out), 2,
+                  ctypes.byref(tail), P(gh), ld_gh, _lib.BF16, P(gw), _lib.BF16, P(ws), ws.numel(), st)
+        torch.cuda.synchronize()
+        return out, lse, g, loss, gw
+
+    gh0 = torch.zeros(n, d, dtype=torch.bfloat16, device=DEV)
+    r0 = call(hd, Wd, gh0, d)
+    ghw = torch.zeros(n, d + 32, dtype=torch.bfloat16, device=DEV)
+    r1 = call(hs, Ws, ghw, d + 32)
+    for a, b in zip(r0[:3] + r0[4:], r1[:3] + r1[4:]):
+        assert torch.equal(a, b), plan
+    assert abs(r0[3].item() - r1[3].item()) <= 1e-6 * max(1.0, abs(r0[3].item()))
+    assert torch.equal(ghw[:, :d], gh0) and (ghw[:, d:] == 0).all()
+    gh_ref, _ = ohead.head_backward(h, W, y, T, r0[2].cpu(), want_w=False)
+    assert _rel(gh0.float().cpu(), gh_ref) <= 1e-2
+
+
 def test_fused_grpo_head_autograd_matches_the_two_call_route():
     """fused_grpo_head under autograd: loss.backward() (here of 2 x loss) gives the gradients the step computed,
     scaled, and they match the autograd route of fused_head then grpo_loss (the trainer's two-call composition) to
