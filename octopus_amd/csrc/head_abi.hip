@@ -347,8 +347,8 @@ bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need
   if (L.wide_on) off += align_up((size_t)V * d * 2);
   L.wt = off;  // W^T [d, V_pad] (grad_h: when it cannot read W K-major, or by choice)
   if (L.wt_on) off += align_up((size_t)d * L.V_pad * L.esz);
-  L.gacc = off;  // fp32 grad_W partial sums across passes
-  if (L.gacc_on) off += align_up((size_t)V * d * sizeof(float));
+  L.gacc = off;  // fp32 grad_W partial sums across passes (tile-blocked over V_pad rows when d % 256 == 0)
+  if (L.gacc_on) off += align_up((size_t)(d % TN == 0 ? L.V_pad : V) * d * sizeof(float));
   L.rows = off;  // the gathered hidden rows (OCTO_WS_GATHER), last
   if (gather) off += gather_bytes(n_max, d, w_dtype == OCTO_FP8E4M3 ? OCTO_BF16 : w_dtype);
   L.total = off;
@@ -518,7 +518,7 @@ GemmShape shape(int64_t M, int64_t N, int64_t K, int group_m, int count_on, cons
 // else as fp32 partials (gacc_on) or added to the output. With a device row count the count decides which pass is
 // the last (passes at or past it store nothing). gacc and gw point at row v0.
 StoreArgs grad_w_store(int d, int64_t r0, int64_t rows, int64_t p, int64_t passes, bool gacc_on, float *gacc, void *gw,
-                       int gw_dtype, int flags, const int32_t *count) {
+                       int gw_dtype, int flags, const int32_t *count, bool blocked = false) {
   const bool last_pass = p + 1 == passes;
   StoreArgs o;
   const bool acc_out = flags & OCTO_GRADW_ACCUMULATE;
@@ -547,14 +547,16 @@ StoreArgs grad_w_store(int d, int64_t r0, int64_t rows, int64_t p, int64_t passe
     o.part = gacc;
     o.part_accumulate = p > 0 ? 1 : 0;
   }
+  // with a device count every pass reaches the partials through part / addend, so their layout may be blocked
+  o.part_blocked = (blocked && count && gacc_on && d % TN == 0) ? 1 : 0;
   o.ldc = d;
   o.ld_add = d;
   return o;
 }
 int grad_w_pass(int dt, const Operand &A3, int kmajor, const Operand &B3, int64_t vc, int d, int64_t r0, int64_t rows,
                 int64_t p, int64_t passes, bool gacc_on, float *gacc, void *gw, int gw_dtype, int flags,
-                const int32_t *count, hipStream_t st) {
-  const StoreArgs o = grad_w_store(d, r0, rows, p, passes, gacc_on, gacc, gw, gw_dtype, flags, count);
+                const int32_t *count, hipStream_t st, bool blocked = false) {
+  const StoreArgs o = grad_w_store(d, r0, rows, p, passes, gacc_on, gacc, gw, gw_dtype, flags, count, blocked);
   TimedLaunch t("gemm_store_grad_w", st);
   return launch_gemm_store(dt, A3, B3, shape(vc, d, rows, kGroupM, 3, count, r0), o, st, kmajor);
 }
@@ -894,7 +896,8 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
       if (rc) return rc;
     }
     if (need_gh && need_gw) {  // both in one launch
-      const StoreArgs o3 = grad_w_store(d, r0, rows, p, L.passes, L.gacc_on, gacc, grad_w, gw_dtype, flags, count);
+      const StoreArgs o3 = grad_w_store(d, r0, rows, p, L.passes, L.gacc_on, gacc, grad_w, gw_dtype, flags, count,
+                                        true);
       TimedLaunch t("gemm_grads", st);
       rc = launch_gemm_grads(cm.dt, A2, B2, s2, o2, !L.wt_on, A3, B3, shape(V, d, rows, kGroupM, 3, count, r0), o3,
                              st);
@@ -903,7 +906,7 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
       rc = launch_gemm_store(cm.dt, A2, B2, s2, o2, st, L.wt_on ? KM_NONE : KM_B);
     } else if (need_gw) {
       rc = grad_w_pass(cm.dt, A3, KM_A, B3, V, d, r0, rows, p, L.passes, L.gacc_on, gacc, grad_w, gw_dtype, flags,
-                       count, st);
+                       count, st, true);
     }
     if (rc) return rc;
   }

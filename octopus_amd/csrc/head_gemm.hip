@@ -517,11 +517,50 @@ __device__ __forceinline__ int pass_store(const StoreArgs &e) {
   return (e.part && c > e.pass_end) ? 2 : 1;
 }
 
+// The tile's fp32 partials in the blocked layout (StoreArgs::part_blocked): this wave's 8192 values, element v of
+// block (i, j) of lane l at ((i NJ + j) NV + v) 64 + l, stored or added (no-return atomics).
+template <class L>
+__device__ __forceinline__ float *blocked_part(float *base, int64_t ldc, int64_t m0, int64_t n0) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  return base + ((m0 / TM) * (ldc / TN) + n0 / TN) * (int64_t)(TM * TN) + w * (L::NI * L::NJ * L::NV * 64) + lane;
+}
+
+template <class L>
+__device__ __forceinline__ void store_blocked(const typename L::V (&acc)[L::NI][L::NJ], const StoreArgs &e,
+                                              int64_t m0, int64_t n0) {
+  float *b = blocked_part<L>(e.part, e.ldc, m0, n0);
+#pragma unroll
+  for (int i = 0; i < L::NI; ++i)
+#pragma unroll
+    for (int j = 0; j < L::NJ; ++j)
+#pragma unroll
+      for (int v = 0; v < L::NV; ++v) {
+        float *q = b + ((i * L::NJ + j) * L::NV + v) * 64;
+        if (e.part_accumulate) __hip_atomic_fetch_add(q, acc[i][j][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else *q = acc[i][j][v];
+      }
+}
+
+// acc += the blocked partials of the earlier passes (the pass that stores C).
+template <class L>
+__device__ __forceinline__ void add_blocked(typename L::V (&acc)[L::NI][L::NJ], const float *addend, int64_t ldc,
+                                            int64_t m0, int64_t n0) {
+  const float *b = blocked_part<L>((float *)addend, ldc, m0, n0);
+#pragma unroll
+  for (int i = 0; i < L::NI; ++i)
+#pragma unroll
+    for (int j = 0; j < L::NJ; ++j)
+#pragma unroll
+      for (int v = 0; v < L::NV; ++v) acc[i][j][v] += b[((i * L::NJ + j) * L::NV + v) * 64];
+}
+
 template <class L, typename OT>
 __device__ __forceinline__ void store_pass(const typename L::V (&acc)[L::NI][L::NJ], const StoreArgs &e, int which,
                                            int64_t m0, int64_t n0, int64_t mvalid, int64_t nvalid) {
   if (which == 1) {
     store_any<L, OT>(acc, e, m0, n0, mvalid, nvalid);
+  } else if (e.part_blocked) {
+    store_blocked<L>(acc, e, m0, n0);
   } else {
     StoreArgs p = e;
     p.C = e.part;
@@ -570,13 +609,18 @@ __device__ __forceinline__ void store8_tile(const Operand &A, const Operand &B, 
   if constexpr (KM == KM_A) mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
   else if constexpr (KM == KM_B) mainloop_ring5<DT, OpRowsN<8, 128>, OpColsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
   else mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
+  StoreArgs eb = e;
+  if (e.part_blocked && which == 1 && e.addend) {  // the blocked partials added here, C stored as usual
+    add_blocked<Acc16N<4>>(acc, e.addend, e.ldc, m0, n0);
+    eb.addend = nullptr;
+  }
   if constexpr (OT >= 0) {
-    store_pass<Acc16N<4>, typename Elem<OT>::T>(acc, e, which, m0, n0, mvalid, nvalid);
+    store_pass<Acc16N<4>, typename Elem<OT>::T>(acc, eb, which, m0, n0, mvalid, nvalid);
   } else {
-    switch (e.dtype) {
-      case OCTO_BF16: store_pass<Acc16N<4>, __bf16>(acc, e, which, m0, n0, mvalid, nvalid); break;
-      case OCTO_F16: store_pass<Acc16N<4>, _Float16>(acc, e, which, m0, n0, mvalid, nvalid); break;
-      default: store_pass<Acc16N<4>, float>(acc, e, which, m0, n0, mvalid, nvalid); break;
+    switch (eb.dtype) {
+      case OCTO_BF16: store_pass<Acc16N<4>, __bf16>(acc, eb, which, m0, n0, mvalid, nvalid); break;
+      case OCTO_F16: store_pass<Acc16N<4>, _Float16>(acc, eb, which, m0, n0, mvalid, nvalid); break;
+      default: store_pass<Acc16N<4>, float>(acc, eb, which, m0, n0, mvalid, nvalid); break;
     }
   }
 }

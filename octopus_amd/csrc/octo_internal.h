@@ -109,6 +109,10 @@ struct StoreArgs {
   int64_t pass_r0 = 0, pass_end = 0;
   float *part = nullptr;
   int part_accumulate = 0;
+  // part_blocked: the fp32 partials (part, and the addend of the pass that stores C) laid out tile by tile in the
+  // 8-wave accumulator order, [tile mt * (ldc / 256) + nt][wave][i][j][v][lane], so that each 4-byte store or atomic
+  // of a wave covers 256 contiguous bytes; needs ldc a multiple of 256 and M rounded up to 256 rows of room.
+  int part_blocked = 0;
 };
 
 int launch_gemm_stats(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
