@@ -86,7 +86,7 @@ const char *octo_last_error(void);
 /* Kernel timing hook (no counterpart in the reference: a measurement aid for benchmarks). While enabled,
  * every GEMM launch of octo_head_fwd / octo_head_bwd / octo_head_step_grpo is bracketed by HIP events on its
  * stream, under the names "gemm_stats", "gemm_dz", "gemm_store_grad_h" and "gemm_store_grad_w" (and the step's
- * "dz_scale"). octo_timing_read waits for
+ * "gemm_grads", "ex_fix" and, for f16 operands, "dz_scale"). octo_timing_read waits for
  * the recorded launches of one name and returns their count and summed duration. octo_timing_enable
  * (either value) discards what was recorded. Off by default; enabling it creates events (allocates). */
 int octo_timing_enable(int on);
@@ -258,12 +258,16 @@ int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
  * form under OCTO_LSE_PAIR, as for the backward). The gradients are those of grpo->loss; a caller whose loss is
  * c L scales them by c.
  * The rows run in passes of at most 32,768 (as many as the staging budget holds, balanced). The forward GEMM of a
- * pass stores each element's exponential relative to the maximum of its 128-column half tile, exp2(s log2 e - m_h)
- * x post'(z) (the exp2 its softmax sums use), as f16 [rows, V rounded up to 256]; once the merge has the rows'
- * (m2, l2S) and g, each half tile is scaled by -g exp2(m_h - m2 - l2S) / T (x the fp8 row scales) into dz in the
- * MFMA type, the label entry written from the fp32 target logit; grad_h = dz . W and grad_W = dz^T . h then run as
- * in octo_head_bwd (both in one launch per pass). The logits are computed once instead of twice; dz differs from
- * octo_head_bwd's by one more rounding (the f16 exponential's, 2^-11 relative).
+ * pass stores each element's exponential [rows, V rounded up to 256] in the MFMA type. bf16 (and fp8 weights): as
+ * exp2(s log2 e - o_r) x post'(z) (x the fp8 row scale) relative to a per-row offset o_r set before the pass, the
+ * row's fp32 label logit (base 2) + 48, so that dz = -g exp2(o_r - m2 - l2S) / T x the stored value is one scale per
+ * row: grad_h = dz . W takes it in its store and grad_W = dz^T . h through h^T scaled by it (rounded once to bf16);
+ * the merge writes the label entry from the fp32 target logit, and a row whose maximum lies more than 112 (base 2)
+ * above its label logit is rescaled to o_r = m2 after the merge. f16: relative to the maximum of each 128-column half
+ * tile, then scaled into dz by -g exp2(m_h - m2 - l2S) / T once the merge has the rows' (m2, l2S) and g. grad_h and
+ * grad_W run as in octo_head_bwd (both in one launch per pass). The logits are computed once instead of twice; dz
+ * differs from octo_head_bwd's by the rounding of the stored value (bf16: 2^-9 relative, in place of the backward's
+ * rounding of dz; f16: 2^-11 relative, besides it), and bf16 grad_W by the rounding of the scaled h^T as well.
  * Workspace: octo_head_workspace_bytes with OCTO_WS_STEP [| OCTO_WS_NO_GRADW | OCTO_WS_GATHER], the plan at a
  * 2 GiB staging budget ([rows, V] of one pass); outside the staging are the pass's statistics per vocabulary tile,
  * h^T of a pass, fp32 grad_w partials [V, d] over several passes, and once per call W widened to bf16 (fp8 weights)

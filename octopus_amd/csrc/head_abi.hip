@@ -267,9 +267,11 @@ bool bwd_plan_for(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool n
 
 // ---- the fused GRPO step's plan (octo_head_step_grpo) ----------------------------------------------------
 // The step runs the rows in passes of P; per pass its forward GEMM stores, besides the statistics, every element's
-// exponential relative to its half tile's maximum (StatsArgs::ex) into a [P, V_pad] staging area, which launch_dz_scale
-// turns into dz once the merge has the rows' (m2, l2S) and g; the gradient GEMMs read it as the backward's read
-// their dz. Rows per pass: the most that fit the staging budget (at most kPassRowsMax), balanced over the passes.
+// exponential (StatsArgs::ex) into a [P, V_pad] staging area: bf16, relative to the row's offset (StatsArgs::xoff),
+// so that dz is one scale per row times it (launch_ex_fix sets the scales); f16, relative to its half tile's maximum,
+// turned into dz by launch_dz_scale once the merge has the rows' (m2, l2S) and g. The gradient GEMMs read it as the
+// backward's read their dz. Rows per pass: the most that fit the staging budget (at most kPassRowsMax), balanced over
+// the passes.
 // The staging is the only part that grows with the budget; outside it sit the pass's statistics [P, V / 256], h^T
 // [d, P], the label entries [P], fp32 grad_W partials [V, d] over several passes, and, once per call, W widened to
 // bf16 (fp8 weights) or staged as W^T (16-bit weights that grad_h cannot read K-major as stored).
@@ -277,7 +279,7 @@ struct StepLayout {
   int64_t P, passes, mtiles, V_pad;
   int esz;
   bool gacc_on, wide_on, wt_on;
-  size_t part, z, hit, rowout, ht, dz, wide, wt, gacc, rows, total;
+  size_t part, z, hit, rowout, xoff, tdot, xuse, scale, flags, ht, dz, wide, wt, gacc, rows, total;
 };
 
 // Rows per pass when grad_h is asked for: each pass's grad_h is one tile per CU per round of long tiles (K = V), so
@@ -339,6 +341,18 @@ bool step_plan(int64_t n_max, int d, int V, int w_dtype, bool need_gh, bool need
   off += align_up((size_t)L.P * sizeof(float));
   L.rowout = off;  // (logprob, entropy) per compact row [n_max, 2] fp32, for the pair-row GRPO tail
   off += align_up((size_t)n_max * 2 * sizeof(float));
+  // bf16 operands, the row-offset exponentials: each compact row's offset and target dot [n_max] fp32; per pass row
+  // the offset in use and the dz scale [P] fp32, the flagged rows [P] int32; a flag count per pass
+  L.xoff = off;
+  off += align_up((size_t)n_max * sizeof(float));
+  L.tdot = off;
+  off += align_up((size_t)n_max * sizeof(float));
+  L.xuse = off;
+  off += align_up((size_t)L.P * sizeof(float));
+  L.scale = off;
+  off += align_up((size_t)L.P * sizeof(float));
+  L.flags = off;  // flag counts [passes], then the flagged rows [P]
+  off += align_up((size_t)(L.passes + L.P) * sizeof(int32_t));
   L.ht = off;  // h^T [d, P] of the pass's rows (grad_W)
   if (need_gw) off += align_up((size_t)d * L.P * L.esz);
   L.dz = off;  // the exponentials, then dz [P, V_pad], token-major
@@ -668,10 +682,11 @@ int head_fwd(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const void
 
 // ---- the fused GRPO step (octo_head_step_grpo) ---------------------------------------------------------
 // Forward, GRPO weight and backward of the compact rows in one call, pass by pass (StepLayout). The logits are
-// computed once per pass: the forward GEMM leaves each element's exponential (relative to its half tile's maximum, the
-// same exp2 its statistics sum) in the staging area, the
-// merge gives the rows' outputs, row state, g and label entry, launch_dz_scale scales the exponentials into dz, and
-// grad_h = dz . W, grad_W = dz^T . h follow as in the backward. fp32 operands run head_fwd, then octo_head_bwd.
+// computed once per pass: the forward GEMM leaves each element's exponential (from the same exp2 its statistics sum)
+// in the staging area; the merge gives the rows' outputs, row state, g and label entry; bf16: launch_ex_fix sets each
+// row's dz scale (and rescales the rows flagged by the merge), which grad_h's store and the scaled h^T of grad_W
+// apply; f16: launch_dz_scale scales the exponentials into dz. grad_h = dz . W, grad_W = dz^T . h follow as in the
+// backward. fp32 operands run head_fwd, then octo_head_bwd.
 // Prefix-tree pair rows (octo_head_step_grpo_pairs): the compact rows are the tree's (position, label) pairs, the
 // GRPO tail's arrays are per flat token, and flat token t reads pair row flat_pair[t]; its columns go to out_flat.
 struct StepPairs {
@@ -784,6 +799,39 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
                           cm.dt, st);
     if (rc) return rc;
   }
+  // bf16 operands: the exponentials are stored relative to per-row offsets (StatsArgs::xoff), so dz is one scale per
+  // row times the stored value: grad_h takes the scale in its store, grad_W through the scaled h^T, and no pass of its
+  // own turns the exponentials into dz. f16 (5 exponent bits) keeps the half-tile form and launch_dz_scale.
+  const bool rowoff = grads && cm.dt == OCTO_BF16 && cm.c > 0.f;
+  float *xoff = (float *)(wsb + L.xoff), *tdot = (float *)(wsb + L.tdot);
+  float *xuse = (float *)(wsb + L.xuse), *rscale = (float *)(wsb + L.scale);
+  int32_t *flag_cnt = (int32_t *)(wsb + L.flags), *flag_rows = flag_cnt + L.passes;
+  if (rowoff) {
+    RowOffArgs ro{};
+    ro.h = h;
+    ro.ldh = ldh;
+    ro.h_dtype = h_dtype;
+    ro.idx = idx;
+    ro.w = w;
+    ro.ldw = ldw;
+    ro.w_dtype = w_dtype;
+    ro.wscale = w_scale;
+    ro.labels = labels;
+    ro.label_via_idx = (flags & OCTO_ROWS_VIA_IDX) != 0;
+    ro.count = count;
+    ro.n_max = n_max;
+    ro.d = d;
+    ro.V = V;
+    ro.c = cm.c;
+    ro.pre = cm.pre;
+    ro.use_tanh = use_tanh;
+    ro.tdot = tdot;
+    ro.xoff = xoff;
+    ro.flag_cnt = flag_cnt;
+    ro.nflag = (int)L.passes;
+    rc = launch_row_offsets(ro, st);
+    if (rc) return rc;
+  }
 
   for (int64_t p = 0; p < L.passes; ++p) {
     const int64_t r0 = p * L.P;
@@ -801,6 +849,7 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     e.pre = cm.pre;
     e.ex = grads ? dz : nullptr;
     e.ldx = L.V_pad;
+    e.xoff = rowoff ? xoff + r0 : nullptr;
     {
       TimedLaunch t("gemm_stats", st);
       rc = launch_gemm_stats(cm.dt, cm.fp8, use_tanh != 0, Aw, Bh, shape(V, rows, d, kGroupM, 2, count, r0), e, st);
@@ -818,6 +867,15 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     m.rows = rows;
     m.c = cm.c;
     m.hit = hit;
+    if (rowoff) {
+      m.tdot = tdot;
+      m.exs = dz;
+      m.ldx = L.V_pad;
+      m.xoff = xoff;
+      m.xuse = xuse;
+      m.flag_cnt = flag_cnt + p;
+      m.flag_rows = flag_rows;
+    }
     if (pm) {
       m.zero_g = 1;
       m.g_zero = gt->g;
@@ -852,31 +910,62 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     }
     if (!grads) continue;
 
-    DzScaleArgs sa;
-    sa.dz = dz;
-    sa.ld = L.V_pad;
-    sa.V_pad = L.V_pad;
-    sa.dtype = cm.dt;
-    sa.part = part;
-    sa.mtiles = L.mtiles;
-    sa.lse = lse;
-    sa.lse_pair = (flags & OCTO_LSE_PAIR) != 0;
-    sa.g = gt->g;
-    sa.gmul = cm.gmul;
-    sa.wscale = cm.fp8 ? w_scale : nullptr;
-    sa.labels = labels;
-    sa.label_idx = (flags & OCTO_ROWS_VIA_IDX) ? idx : nullptr;
-    sa.hit = hit;
-    sa.count = count;
-    sa.r0 = r0;
-    sa.rows = rows;
-    sa.n_max = n_max;
-    sa.V = V;
-    {
-      TimedLaunch t("dz_scale", st);
-      rc = launch_dz_scale(sa, st);
+    if (rowoff) {  // the rows' dz scales, and any flagged row's exponentials rescaled
+      ExFixArgs fx{};
+      fx.ex = dz;
+      fx.ldx = L.V_pad;
+      fx.V_pad = L.V_pad;
+      fx.part = part;
+      fx.mtiles = L.mtiles;
+      fx.xoff = xoff;
+      fx.xuse = xuse;
+      fx.lse = lse;
+      fx.lse_pair = (flags & OCTO_LSE_PAIR) != 0;
+      fx.g = gt->g;
+      fx.gmul = cm.gmul;
+      fx.hit = hit;
+      fx.labels = labels;
+      fx.label_idx = (flags & OCTO_ROWS_VIA_IDX) ? idx : nullptr;
+      fx.count = count;
+      fx.flag_cnt = flag_cnt + p;
+      fx.flag_rows = flag_rows;
+      fx.r0 = r0;
+      fx.rows = rows;
+      fx.n_max = n_max;
+      fx.V = V;
+      fx.scale = rscale;
+      {
+        TimedLaunch t("ex_fix", st);
+        rc = launch_ex_fix(fx, st);
+      }
+      if (rc) return rc;
+    } else {
+      DzScaleArgs sa;
+      sa.dz = dz;
+      sa.ld = L.V_pad;
+      sa.V_pad = L.V_pad;
+      sa.dtype = cm.dt;
+      sa.part = part;
+      sa.mtiles = L.mtiles;
+      sa.lse = lse;
+      sa.lse_pair = (flags & OCTO_LSE_PAIR) != 0;
+      sa.g = gt->g;
+      sa.gmul = cm.gmul;
+      sa.wscale = cm.fp8 ? w_scale : nullptr;
+      sa.labels = labels;
+      sa.label_idx = (flags & OCTO_ROWS_VIA_IDX) ? idx : nullptr;
+      sa.hit = hit;
+      sa.count = count;
+      sa.r0 = r0;
+      sa.rows = rows;
+      sa.n_max = n_max;
+      sa.V = V;
+      {
+        TimedLaunch t("dz_scale", st);
+        rc = launch_dz_scale(sa, st);
+      }
+      if (rc) return rc;
     }
-    if (rc) return rc;
 
     // grad_h[rows] = dz . W   (K = V, or V_pad through the staged W^T)
     const Operand A2 = plain_operand(dz, L.V_pad * esz, rows, count, r0);
@@ -886,12 +975,13 @@ int head_step(const void *h, int64_t h_rows, int64_t ldh, int h_dtype, const voi
     o2.C = (char *)grad_h + r0 * ld_gh * elem_bytes(gh_dtype);
     o2.ldc = ld_gh;
     o2.dtype = gh_dtype;
+    o2.row_scale = rowoff ? rscale : nullptr;
     // grad_W (+)= dz^T . h   (K = this pass's rows)
     const Operand A3 = plain_operand(dz, L.V_pad * esz, L.P, nullptr, 0);
     const Operand B3 = plain_operand(ht, L.P * esz, d, nullptr, 0);
     if (need_gw) {  // h^T [d, P] of the pass's rows, zero past the count
       const int64_t rows_pad = round_up(rows, TN);
-      rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, nullptr,
+      rc = launch_transpose(idx ? h : (const char *)h + r0 * ldh * cm.hesz, ldh, h_dtype, rowoff ? rscale : nullptr,
                             idx ? idx + r0 : nullptr, count, r0, rows, rows_pad, d, ht, L.P, cm.dt, st);
       if (rc) return rc;
     }

@@ -115,8 +115,12 @@ __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
 
     float dot = 0.f;
     const bool y_ok = y >= 0 && y < a.V;
-    if (y_ok) dot = row_dot(a.h, a.h_dtype, hrow * a.ldh, a.w, a.w_dtype, y * a.ldw, a.d, lane);
-    dot = wave_sum(dot);
+    if (a.tdot) {
+      dot = a.tdot[r];
+    } else {
+      if (y_ok) dot = row_dot(a.h, a.h_dtype, hrow * a.ldh, a.w, a.w_dtype, y * a.ldw, a.d, lane);
+      dot = wave_sum(dot);
+    }
     if (lane == 0) {
       const float raw = dot;  // h . W_y as stored (fp8: before the row scale)
       if (a.w_dtype == OCTO_FP8E4M3 && y_ok) dot *= a.wscale[y];
@@ -162,6 +166,16 @@ __global__ __launch_bounds__(64 * kMergeRows) void merge_kernel(MergeArgs a) {
           if (f8) v *= a.wscale[y];
         }
         a.hit[rl] = v;
+        if (a.exs) {  // row-offset exponentials: the label entry, or the row flagged for launch_ex_fix
+          const float xo = a.xoff[r];
+          if (st.m - xo <= kExClamp) {  // false for xo = -inf (a label outside [0, V)) and NaN
+            a.xuse[rl] = xo;
+            if (y_ok) ((__bf16 *)a.exs)[rl * a.ldx + y] = (__bf16)(-v * fexp2(st.m - xo + l2S));
+          } else {
+            a.xuse[rl] = st.m;
+            a.flag_rows[atomicAdd(a.flag_cnt, 1)] = (int32_t)rl;
+          }
+        }
       }
       if (a.zero_g) a.g_zero[r] = 0.f;
     }
@@ -305,6 +319,91 @@ int launch_dz_scale(const DzScaleArgs &a, hipStream_t st) {
   return OCTO_OK;
 }
 
+// ---- the row-offset exponentials of the fused step (StatsArgs::xoff) ------------------------------------------
+// Before the passes, one wave per compact row (4 per workgroup): the target dot product exactly as the merge forms it
+// (row_dot, wave_sum), kept for the merge, and the row's offset: the label's base-2 logit + kExAbove. The label's
+// logit lies at or below the row's maximum m2, so every element within 2^-40 of the row's largest is stored at
+// 2^-88 or more (a bf16 normal), and a row's exponentials need no rescaling unless m2 lies more than kExAbove +
+// kExClamp = 112 (base 2; 77.6 nats) above its label's logit.
+__global__ __launch_bounds__(256) void row_offsets_kernel(RowOffArgs a) {
+  if (blockIdx.x == 0)
+    for (int k = threadIdx.x; k < a.nflag; k += 256) a.flag_cnt[k] = 0;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
+  if (r >= cnt) return;
+  const int64_t hrow = a.idx ? a.idx[r] : r;
+  const int64_t y = a.labels[a.label_via_idx ? hrow : r];
+  const bool y_ok = y >= 0 && y < a.V;
+  float dot = 0.f;
+  if (y_ok) dot = row_dot(a.h, a.h_dtype, hrow * a.ldh, a.w, a.w_dtype, y * a.ldw, a.d, lane);
+  dot = wave_sum(dot);
+  if (lane == 0) {
+    a.tdot[r] = dot;
+    float x = (a.w_dtype == OCTO_FP8E4M3 && y_ok) ? dot * a.wscale[y] : dot;
+    if (a.use_tanh) x = ftanh(a.pre * x);
+    a.xoff[r] = y_ok ? __builtin_fmaf(x, a.c, kExAbove) : -INFINITY;
+  }
+}
+
+int launch_row_offsets(const RowOffArgs &a, hipStream_t st) {
+  const int64_t blocks = cdiv(a.n_max, 4) > 0 ? cdiv(a.n_max, 4) : 1;
+  OCTO_CHECK_ARG(blocks <= 0x7fffffff, "row_offsets: %lld rows", (long long)a.n_max);
+  hipLaunchKernelGGL(row_offsets_kernel, dim3((unsigned)blocks), dim3(256), 0, st, a);
+  OCTO_CHECK_LAUNCH("row_offsets");
+  return OCTO_OK;
+}
+
+// After a pass's merge: every workgroup sets the dz scales of a strided slice of the pass's rows, then takes the
+// flagged rows in turn (none in the usual case, so each workgroup then reads the count and ends). A flagged row is
+// rescaled in place to its new offset (the merge set xuse = m2), 16 bytes per thread and step, by its half tiles'
+// factors (8 columns never straddle a 128-column half tile): the stored value of half tile h is e exp2(min(m_h - xoff,
+// kExClamp)) with e = exp2(c t - m_h), and exp2(c t - m2) = that x exp2(m_h - m2 - min(m_h - xoff, kExClamp)).
+constexpr int kExFixBlocks = 64;
+__global__ __launch_bounds__(256) void ex_fix_kernel(ExFixArgs a) {
+  const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.rows; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = a.r0 + i;
+    float s = 0.f;
+    if (r < cnt) {
+      float m2, l2s;
+      row_state(a.lse, a.lse_pair, r, m2, l2s);
+      s = -(a.g[r] * a.gmul) * fexp2(a.xuse[i] - m2 - l2s);
+    }
+    a.scale[i] = s;
+  }
+  const int nf = *a.flag_cnt;
+  for (int k = blockIdx.x; k < nf; k += gridDim.x) {
+    const int64_t i = a.flag_rows[k], r = a.r0 + i;
+    const float xo = a.xoff[r], xn = a.xuse[i];
+    float m2, l2s;
+    row_state(a.lse, a.lse_pair, r, m2, l2s);
+    const int64_t y = a.labels[a.label_idx ? a.label_idx[r] : r];
+    const f32x4 *pr = a.part + i * a.mtiles;
+    char *row = (char *)a.ex + i * a.ldx * 2;
+    for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < a.V_pad; c0 += 256 * 8) {
+      const f32x4 q = pr[c0 >> 8];
+      const float mh = (c0 & 128) ? q[3] : q[0];  // -inf: no column of the half lies below V (stored zeros)
+      const float f = mh == -INFINITY ? 0.f : fexp2(mh - xn - fminf(mh - xo, kExClamp));
+      float x[8];
+      unpack8(*(const i32x4 *)(row + c0 * 2), false, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] *= f;
+      if (y >= c0 && y < c0 + 8 && y < a.V) x[y - c0] = -a.hit[i] * fexp2(m2 - xn + l2s);
+      *(i32x4 *)(row + c0 * 2) = pack8(x, false);
+    }
+  }
+}
+
+int launch_ex_fix(const ExFixArgs &a, hipStream_t st) {
+  if (a.rows == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(a.V_pad % 256 == 0 && a.ldx >= a.V_pad && ((uintptr_t)a.ex) % 16 == 0 && a.ldx % 8 == 0,
+                 "ex_fix: rows of whole 256-column tiles");
+  hipLaunchKernelGGL(ex_fix_kernel, dim3(kExFixBlocks), dim3(256), 0, st, a);
+  OCTO_CHECK_LAUNCH("ex_fix");
+  return OCTO_OK;
+}
+
 // ---- the fused step's GRPO tail over prefix-tree pair rows ----------------------------------------------
 // One thread per flat token; the workgroup's loss terms are summed in LDS and added with one atomic (as the merge).
 __global__ __launch_bounds__(256) void pairs_grpo_kernel(PairsGrpoArgs a) {
@@ -386,7 +485,8 @@ typedef __attribute__((address_space(3))) short lds_short16;
 typedef __attribute__((address_space(3))) i32x4 lds_i32x4_t;
 __global__ __launch_bounds__(256) void transpose16_kernel(const char *src, int64_t ld_src, const int64_t *map,
                                                           const int32_t *count, int64_t count_off, int64_t rows,
-                                                          int64_t rows_pad, int64_t cols, char *dst, int64_t ld_dst) {
+                                                          int64_t rows_pad, int64_t cols, char *dst, int64_t ld_dst,
+                                                          const float *rscale, int is_f16) {
   __shared__ __attribute__((aligned(16))) char tile_[64 * 128];
   __attribute__((address_space(3))) char *tile = (__attribute__((address_space(3))) char *)tile_;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
@@ -398,7 +498,17 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const char *src, int64
     const int row = c >> 3, cc = c & 7;
     const int64_t r = r0 + row, col = c0 + 8 * cc;
     i32x4 v = {0, 0, 0, 0};
-    if (r < valid && col < cols) v = *(const i32x4 *)(src + (map ? map[r] : r) * ld_src + col * 2);
+    if (r < valid && col < cols) {
+      v = *(const i32x4 *)(src + (map ? map[r] : r) * ld_src + col * 2);
+      if (rscale) {  // row r times its scale, rounded once
+        float x[8];
+        unpack8(v, is_f16 != 0, x);
+        const float sc = rscale[r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] *= sc;
+        v = pack8(x, is_f16 != 0);
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const short x = (short)((uint32_t)v[e >> 1] >> (16 * (e & 1)));
@@ -418,7 +528,7 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const char *src, int64
   }
 }
 
-int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *,
+int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *row_scale,
                      const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
                      int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st) {
   if (rows_pad == 0 || cols == 0) return OCTO_OK;
@@ -427,10 +537,11 @@ int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float
   if (b16 && cols % 8 == 0 && rows_pad % 64 == 0 && ld_src % 8 == 0 && ld_dst % 8 == 0 &&
       ((uintptr_t)src) % 16 == 0 && ((uintptr_t)dst) % 16 == 0) {
     hipLaunchKernelGGL(transpose16_kernel, grid, dim3(256), 0, st, (const char *)src, ld_src * 2, map, count,
-                       count_off, rows, rows_pad, cols, (char *)dst, ld_dst);
+                       count_off, rows, rows_pad, cols, (char *)dst, ld_dst, row_scale, src_dtype == OCTO_F16 ? 1 : 0);
     OCTO_CHECK_LAUNCH("transpose");
     return OCTO_OK;
   }
+  if (row_scale) return octo_fail(OCTO_EUNSUPPORTED, "transpose: row scales need 16-bit rows of 16-byte chunks");
   hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, st, src, ld_src, src_dtype, map, count, count_off, rows,
                      rows_pad, cols, dst, ld_dst, dst_dtype);
   OCTO_CHECK_LAUNCH("transpose");

@@ -91,14 +91,17 @@ __device__ __forceinline__ void pre_transform(typename L::V (&acc)[L::NI][L::NJ]
 typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 
 // The per-token softmax statistics of this wave's rows of the tile: red[wm * 256 + column] = (m2, S, U), m2 the
-// base-2 maximum, S and U the sums of e = exp2(t - m2) and e t (0 past V). EXT (16-bit, the fused step): each e,
+// base-2 maximum, S and U the sums of e = exp2(t - m2) and e t (0 past V). EXM (16-bit, the fused step): each e,
 // times the softcap's derivative 1 - x^2 when TANH (acc holds x = tanh(pre z) then), is also written into the LDS
-// staging tile as f16, laid out as dz_stage lays out dz (zero past V and for tokens at or past nvalid): the stored
-// exponentials are relative to the wave's own maximum, which the tile's part keeps.
-template <class L, bool MASK, bool EXT = false, bool TANH = false>
+// staging tile, laid out as dz_stage lays out dz (zero past V and for tokens at or past nvalid). EXM 1: as f16,
+// relative to the wave's own maximum, which the tile's part keeps. EXM 2: as bf16, times exp2(min(m2 - xoff[token],
+// kExClamp)) (and the fp8 row scale when A_FP8), i.e. relative to the token's offset (StatsArgs::xoff; xoff here
+// points at the tile's first token).
+template <class L, bool MASK, int EXM = 0, bool TANH = false, bool A_FP8 = false>
 __device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int wn,
                                            int lane, int64_t V, float c, lds_f32x4 *red, lds_char *tile = nullptr,
-                                           int64_t nvalid = 0) {
+                                           int64_t nvalid = 0, const float *xoff = nullptr,
+                                           const float *wscale = nullptr) {
 #pragma unroll
   for (int j = 0; j < L::NJ; ++j) {
     float mx = -INFINITY;
@@ -112,6 +115,10 @@ __device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::
     mx = L::col_max(mx);
     const float m2 = mx * c;
     const int tt = L::col(wn, j, lane);
+    // EXM 2: the half tile's factor to the token's offset (fminf also takes kExClamp for m2 - xoff = NaN, which needs
+    // xoff = -inf and m2 = -inf: no element of the half lies below V, each e is 0)
+    float f = 1.f;
+    if constexpr (EXM == 2) f = tt < nvalid ? fexp2(fminf(m2 - xoff[tt], kExClamp)) : 0.f;
     float S = 0.f, U = 0.f;
 #pragma unroll
     for (int i = 0; i < L::NI; ++i)
@@ -129,16 +136,33 @@ __device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::
           }
           S += e;
           U = __builtin_fmaf(e, t, U);
-          if constexpr (EXT) {
+          if constexpr (EXM != 0) {
             const float x = acc[i][j][v];
-            x4[u] = tt < nvalid ? (TANH ? e * (1.f - x * x) : e) : 0.f;
+            const float ev = TANH ? e * (1.f - x * x) : e;
+            x4[u] = EXM == 2 ? ev * f : (tt < nvalid ? ev : 0.f);
           }
         }
-        if constexpr (EXT) {
+        if constexpr (EXM != 0) {
           const int rl = L::row(wm, i, 4 * g4, lane);  // first of this lane's 4 vocab rows in the tile
+          if constexpr (EXM == 2 && A_FP8) {  // d/d(raw e4m3 product): times the row's scale (0 past V)
+            const int64_t row = m0 + rl;
+            if (row + 3 < V) {
+              const f32x4 q = *(const f32x4 *)(wscale + row);
+#pragma unroll
+              for (int u = 0; u < 4; ++u) x4[u] *= q[u];
+            } else {
+#pragma unroll
+              for (int u = 0; u < 4; ++u) x4[u] *= (row + u < V) ? wscale[row + u] : 0.f;
+            }
+          }
           i32x2 pk;
-          pk[0] = (int)pack2(x4[0], x4[1], (f16x2_t *)nullptr);
-          pk[1] = (int)pack2(x4[2], x4[3], (f16x2_t *)nullptr);
+          if constexpr (EXM == 2) {
+            pk[0] = (int)pack2(x4[0], x4[1], (bf16x2 *)nullptr);
+            pk[1] = (int)pack2(x4[2], x4[3], (bf16x2 *)nullptr);
+          } else {
+            pk[0] = (int)pack2(x4[0], x4[1], (f16x2_t *)nullptr);
+            pk[1] = (int)pack2(x4[2], x4[3], (f16x2_t *)nullptr);
+          }
           *(lds_i32x2 *)(tile + tt * 512 + (((rl >> 2) ^ DzSwz<L>::at(tt)) << 3)) = pk;
         }
       }
@@ -453,7 +477,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 #ifndef OCTO_PART_ATOMIC
 #define OCTO_PART_ATOMIC 1
 #endif
-// C = acc (+ addend, fp32, row stride ld_add) (+ C when ACC), rounded once to OT. An fp32 C += acc is one no-return
+// C = rs[row] x acc (rs NULL: acc) (+ addend, fp32, row stride ld_add) (+ C when ACC), rounded once to OT. An fp32 C += acc is one no-return
 // atomic add per element, performed in the L2, so the tile's epilogue does not wait for C to be read (grad_W's fp32
 // partials of the fused step at 24,576 rows, d 2560, V 151,936: the gradient launches 28.35 against 28.65 ms per
 // step, same box). A launch adds to each element once (one tile), so the sums keep launch order and are
@@ -461,7 +485,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
 template <class L, typename OT, bool ACC, bool ADD, bool EDGE>
 __device__ __forceinline__ void store_tile(const typename L::V (&acc)[L::NI][L::NJ], OT *C, const float *addend,
                                            int64_t ldc, int64_t ld_add, int64_t m0, int64_t n0, int64_t mvalid,
-                                           int64_t nvalid, int wm, int wn, int lane) {
+                                           int64_t nvalid, int wm, int wn, int lane, const float *rs) {
 #pragma unroll
   for (int i = 0; i < L::NI; ++i)
 #pragma unroll
@@ -470,11 +494,12 @@ __device__ __forceinline__ void store_tile(const typename L::V (&acc)[L::NI][L::
       if (EDGE && rr >= mvalid) continue;
       OT *crow = C + (m0 + rr) * ldc + n0;
       const float *arow = ADD ? addend + (m0 + rr) * ld_add + n0 : nullptr;
+      const float sc = rs ? rs[m0 + rr] : 1.f;
 #pragma unroll
       for (int j = 0; j < L::NJ; ++j) {
         const int cc = L::col(wn, j, lane);
         if (EDGE && cc >= nvalid) continue;
-        float x = acc[i][j][v];
+        float x = acc[i][j][v] * sc;
         if (ADD) x += arow[cc];
         if constexpr (OCTO_PART_ATOMIC && ACC && std::is_same<OT, float>::value) {
           __hip_atomic_fetch_add(crow + cc, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -489,10 +514,10 @@ __device__ __forceinline__ void store_tile(const typename L::V (&acc)[L::NI][L::
 template <class L, typename OT, bool ACC, bool ADD>
 __device__ __forceinline__ void store_edge(const typename L::V (&acc)[L::NI][L::NJ], OT *C, const float *addend,
                                            int64_t ldc, int64_t ld_add, int64_t m0, int64_t n0, int64_t mvalid,
-                                           int64_t nvalid, int wm, int wn, int lane) {
+                                           int64_t nvalid, int wm, int wn, int lane, const float *rs) {
   if (mvalid < TM || nvalid < TN)
-    store_tile<L, OT, ACC, ADD, true>(acc, C, addend, ldc, ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
-  else store_tile<L, OT, ACC, ADD, false>(acc, C, addend, ldc, ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
+    store_tile<L, OT, ACC, ADD, true>(acc, C, addend, ldc, ld_add, m0, n0, mvalid, nvalid, wm, wn, lane, rs);
+  else store_tile<L, OT, ACC, ADD, false>(acc, C, addend, ldc, ld_add, m0, n0, mvalid, nvalid, wm, wn, lane, rs);
 }
 
 template <class L, typename OT>
@@ -500,12 +525,13 @@ __device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::N
                                           int64_t n0, int64_t mvalid, int64_t nvalid) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = L::wm(w), wn = L::wn(w);
   OT *c = (OT *)e.C;
+  const float *rs = e.row_scale;
   if (e.accumulate) {
-    if (e.addend) store_edge<L, OT, true, true>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
-    else store_edge<L, OT, true, false>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
+    if (e.addend) store_edge<L, OT, true, true>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane, rs);
+    else store_edge<L, OT, true, false>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane, rs);
   } else {
-    if (e.addend) store_edge<L, OT, false, true>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
-    else store_edge<L, OT, false, false>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane);
+    if (e.addend) store_edge<L, OT, false, true>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane, rs);
+    else store_edge<L, OT, false, false>(acc, c, e.addend, e.ldc, e.ld_add, m0, n0, mvalid, nvalid, wm, wn, lane, rs);
   }
 }
 
@@ -566,6 +592,7 @@ __device__ __forceinline__ void store_pass(const typename L::V (&acc)[L::NI][L::
     p.C = e.part;
     p.addend = nullptr;
     p.accumulate = e.part_accumulate;
+    p.row_scale = nullptr;
     store_any<L, float>(acc, p, m0, n0, mvalid, nvalid);
   }
 }
@@ -669,8 +696,9 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
 // against 15.1 ms, gemm_dz 15.3 against 16.5 ms; without the split barrier gemm_dz was 0.4 ms slower than the 4-wave
 // loop.
 // EX: also store the exponentials (StatsArgs::ex) through the LDS staging tile, as gemm_dz8 stores dz; the per-wave
-// statistics then sit past that tile.
-template <int DT, bool A_FP8, bool TANH, bool EX>
+// statistics then sit past that tile. EX 1: f16 relative to each half tile's maximum; EX 2: bf16 relative to each
+// token's offset (StatsArgs::xoff).
+template <int DT, bool A_FP8, bool TANH, int EX>
 __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_stats8_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
   static_assert(ring5_ok(DT), "16-bit operands");
   static_assert(256 * 512 + 512 * 16 <= SMEM_RING5, "staging tile and statistics fit the ring's LDS");
@@ -688,8 +716,9 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, s.K, smem, acc);
   const int64_t ma = e.v0 + m0;  // first vocabulary row of the tile
   pre_transform<L, A_FP8, TANH>(acc, ma, wm, lane, e.wscale, e.V, e.pre);
-  if (ma + TM > e.V) stats_cols<L, true, EX, TANH>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid);
-  else stats_cols<L, false, EX, TANH>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid);
+  const float *xo = EX == 2 ? e.xoff + n0 : nullptr;
+  if (ma + TM > e.V) stats_cols<L, true, EX, TANH, A_FP8>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid, xo, e.wscale);
+  else stats_cols<L, false, EX, TANH, A_FP8>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid, xo, e.wscale);
   __syncthreads();  // per-wave statistics (and the staging tile) written
   const int t = threadIdx.x;
   if (t < nvalid) {  // (m_a, S, U, m_b): S and U relative to max(m_a, m_b), the halves' maxima kept
@@ -738,10 +767,16 @@ static inline dim3 grid_of(const GemmShape &s) { return dim3((unsigned)tile_grid
 template <int DT, bool F8, bool TH>
 static int go_stats(const Operand &A, const Operand &B, const GemmShape &s, const StatsArgs &e, hipStream_t st) {
   if constexpr (ring5_ok(DT)) {
-    if (e.ex)
-      hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH, true>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
-    else
-      hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH, false>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
+    if (e.ex && e.xoff) {
+      if constexpr (DT == OCTO_BF16)
+        hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH, 2>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
+      else
+        return octo_fail(OCTO_EUNSUPPORTED, "gemm_stats: row-offset exponentials need bf16 operands");
+    } else if (e.ex) {
+      hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH, 1>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
+    } else {
+      hipLaunchKernelGGL((gemm_stats8_kernel<DT, F8, TH, 0>), grid_of(s), dim3(2 * NTHREADS), 0, st, A, B, s, e);
+    }
   } else {
     if (e.ex) return octo_fail(OCTO_EUNSUPPORTED, "gemm_stats: exponentials of fp32 operands");
     hipLaunchKernelGGL((gemm_stats_kernel<DT, F8, TH>), grid_of(s), dim3(NTHREADS), 0, st, A, B, s, e);

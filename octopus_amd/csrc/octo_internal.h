@@ -21,6 +21,15 @@ struct GemmShape;
 // exp2(m_h - m2 - l2S) ex x (fp8 row scale) (the fused step, launch_dz_scale). f16 for any MFMA type: the values lie
 // in [0, 1], where f16 keeps 11 bits to bf16's 8; what it rounds in its subnormal range, below 2^-14 of the half
 // tile's largest probability, errs by at most 2^-25 of it per element.
+//
+// With xoff != NULL as well (bf16 operands, the fused step's row-offset form) the stored value is bf16 and relative to
+// a per-token offset xoff[token] (base-2 units) chosen before the GEMM, instead of the half tile's maximum:
+//   ex[token][v] = exp2(c t - m_h) x exp2(min(m_h - xoff[token], kExClamp)) x post'(z) (x fp8 row scale of v),
+// which is exp2(c t - xoff) x post'(z) (x scale) for every element of a token whose maximum m2 lies at most kExClamp
+// above its offset. dz is then one scale per token times the stored value: dz = s[token] ex, s = -g gmul exp2(xoff
+// - m2 - l2S), except at the label (launch_merge writes that entry); a token whose maximum lies further above its
+// offset is rescaled by launch_ex_fix. bf16 keeps 8 exponent bits: with the offset kExAbove above the label's own
+// logit (<= m2), every element within 2^-40 of the row's largest stays a normal number.
 struct StatsArgs {
   f32x4 *part;
   int64_t mtiles;
@@ -31,7 +40,13 @@ struct StatsArgs {
   float pre;            // tanh argument scale (softcap)
   void *ex = nullptr;
   int64_t ldx = 0;
+  const float *xoff = nullptr;  // per-token base-2 offsets of the stored exponentials (tokens of this GEMM), or NULL
 };
+
+// The row-offset form's constants (base-2 units): the offset sits kExAbove above the label's logit, and a half tile's
+// factor exp2(m_h - offset) is clamped at 2^kExClamp (past it the row is flagged and rescaled).
+constexpr float kExAbove = 48.f;
+constexpr float kExClamp = 64.f;
 
 // The backward's per-row softmax state. Paired (OCTO_LSE_PAIR): lse[2 r] = m2, the row's base-2 maximum exactly as
 // the statistics epilogue subtracts it (t = fma(x, c, -m2)), and lse[2 r + 1] = log2 of the shifted sum, so that
@@ -113,6 +128,8 @@ struct StoreArgs {
   // 8-wave accumulator order, [tile mt * (ldc / 256) + nt][wave][i][j][v][lane], so that each 4-byte store or atomic
   // of a wave covers 256 contiguous bytes; needs ldc a multiple of 256 and M rounded up to 256 rows of room.
   int part_blocked = 0;
+  // row_scale: C's row m takes row_scale[m] x acc (before any addend); the final store only (not the partials)
+  const float *row_scale = nullptr;
 };
 
 int launch_gemm_stats(int dt, bool a_fp8, bool tanh, const Operand &A, const Operand &B, const GemmShape &s,
@@ -167,8 +184,72 @@ struct MergeArgs {
   float *hit = nullptr;
   int zero_g = 0;
   float *g_zero = nullptr;
+  // tdot: the rows' raw target dot products h . W_y from launch_row_offsets (compact rows), used in place of the
+  // merge's own (the same computation). exs (the row-offset exponentials, StatsArgs::xoff; needs hit): a row whose
+  // maximum m2 lies at most kExClamp above its offset xoff[r] gets its label entry written into exs[r - row_off][y],
+  // -hit exp2(m2 + l2S - xoff) (so that the row's dz scale times it is the label's dz), and xuse[r - row_off] =
+  // xoff[r]; any other row (its offset too low, or -inf for a label outside [0, V)) is listed in flag_rows (local
+  // rows, flag_cnt of them) with xuse = m2, for launch_ex_fix.
+  const float *tdot = nullptr;
+  void *exs = nullptr;
+  int64_t ldx = 0;
+  const float *xoff = nullptr;
+  float *xuse = nullptr;
+  int32_t *flag_cnt = nullptr;
+  int32_t *flag_rows = nullptr;
 };
 int launch_merge(const MergeArgs &a, hipStream_t st);
+
+// The fused step's per-row offsets, before its passes: for compact rows r < min(count, n_max), tdot[r] = the raw
+// fp32 dot h_r . W_y (the merge's target-logit product) and xoff[r] = the label's base-2 logit as the statistics
+// epilogue forms it (c x the transformed logit) + kExAbove, -inf for a label outside [0, V); flag_cnt[0 .. nflag) = 0.
+struct RowOffArgs {
+  const void *h;
+  int64_t ldh;  // elements
+  int h_dtype;
+  const int64_t *idx;  // compact row -> hidden row, or NULL
+  const void *w;
+  int64_t ldw;  // elements
+  int w_dtype;
+  const float *wscale;
+  const int64_t *labels;
+  int label_via_idx;  // labels indexed by the hidden row (OCTO_ROWS_VIA_IDX)
+  const int32_t *count;
+  int64_t n_max;
+  int d;
+  int64_t V;
+  float c, pre;
+  int use_tanh;
+  float *tdot, *xoff;
+  int32_t *flag_cnt;
+  int nflag;
+};
+int launch_row_offsets(const RowOffArgs &a, hipStream_t st);
+
+// After a pass's merge (and its pair-row GRPO tail): the rows' dz scales s[i] = -g[r] gmul exp2(xuse[i] - m2 - l2S)
+// for local rows i < rows with r = r0 + i below the count (0 otherwise), and the flagged rows' exponentials rescaled
+// in place to their new offset xuse = m2: per half tile h, by exp2(m_h - m2 - min(m_h - xoff[r], kExClamp)), the
+// label entry written as the merge writes it.
+struct ExFixArgs {
+  void *ex;  // [rows, ldx] bf16
+  int64_t ldx, V_pad;
+  const f32x4 *part;  // [rows, mtiles], local rows
+  int64_t mtiles;
+  const float *xoff;  // compact rows
+  const float *xuse;  // local rows
+  const float *lse;   // compact rows
+  int lse_pair;
+  const float *g;  // compact rows
+  float gmul;
+  const float *hit;  // local rows
+  const int64_t *labels;
+  const int64_t *label_idx;  // labels[label_idx[r]] when set
+  const int32_t *count;
+  const int32_t *flag_cnt, *flag_rows;
+  int64_t r0, rows, n_max, V;
+  float *scale;  // local rows
+};
+int launch_ex_fix(const ExFixArgs &a, hipStream_t st);
 
 // dz of compact rows r0 .. r0 + rows (local row i = r - r0) from the exponentials a stats GEMM stored (StatsArgs::ex,
 // f16), in place: dz[i][v] = -g[r] gmul exp2(m_h - m2 - l2S) ex[i][v] (x wscale[v] for fp8 weights, 0 past V) for
@@ -224,8 +305,9 @@ int launch_grpo_count(const float *mask, int64_t n, float *z, float *loss, hipSt
 // dst[r * d + c] = bf16(e4m3 w[r * ldw + c]) for r < V, c < d (exact).
 int launch_widen_fp8(const void *w, int64_t ldw, int64_t V, int d, void *dst, hipStream_t st);
 // dst[c * ld_dst + r] = src row map[r] (or r), element c, for r < rows_pad, c < cols; rows at or past the valid
-// count (count - count_off, capped at rows) read 0; dst holds the staged MFMA type (bf16/f16/f32).
-int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *src_scale,
+// count (count - count_off, capped at rows) read 0; dst holds the staged MFMA type (bf16/f16/f32). row_scale (16-bit
+// source and destination of one type only): row r is multiplied by row_scale[r] in fp32 and rounded once.
+int launch_transpose(const void *src, int64_t ld_src, int src_dtype, const float *row_scale,
                      const int64_t *map, const int32_t *count, int64_t count_off, int64_t rows,
                      int64_t rows_pad, int64_t cols, void *dst, int64_t ld_dst, int dst_dtype, hipStream_t st);
 

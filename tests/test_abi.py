@@ -142,7 +142,8 @@ def _gradh_rounds(n, d, p_tiles):
 ])
 def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     """The fused step's workspace at the default plan: one pass's [rows, V_pad] exponentials (then dz) within the
-    2 GiB staging budget, plus that pass's statistics, h^T and label entries, each row's columns (for pair rows),
+    2 GiB staging budget, plus that pass's statistics, h^T and label entries, each row's columns (for pair rows), the
+    row offsets of the bf16 exponentials with their target dots, dz scales and flagged rows,
     fp32 grad_W partials over several passes (tile-blocked over V rounded up to 256 rows when d is a multiple of 256),
     and once per call the widened fp8 weights and W^T (where grad_h cannot
     read W as stored, or grad_h alone over 16,384 rows or more). Rows per pass: the size up to what the budget holds
@@ -158,6 +159,7 @@ def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     assert _gradh_rounds(n, d, P // 256) == best
     assert all(_gradh_rounds(n, d, p) > best for p in range(P // 256 + 1, top + 1))
     extra = (P * ((V + 255) // 256) * 16 + P * 4 + n * 8 + (d * P * 2 if need_gw else 0) +
+             n * 8 + P * 12 + passes * 4 +  # bf16 row offsets: offset and target dot per row, per pass row 3 words
              ((Vp if d % 256 == 0 else V) * d * 4 if need_gw and passes > 1 else 0) +
              (V * d * 2 if w == _lib.FP8E4M3 else 0) +
              (d * Vp * 2 if V % 64 or d % 256 or (not need_gw and n >= 16384) else 0))

@@ -3,8 +3,9 @@ computed once per row pass.
 
 The forward half runs the forward's own statistics and merge per row, so its outputs (logprob, entropy, row state,
 g) must equal octo_head_fwd_grpo's bit for bit and its loss up to summation order. The backward half builds dz from
-the stored exponentials instead of a recompute, so its gradients must match octo_head_bwd's for the same g to the
-16-bit rounding of dz, and the fp64 oracle (oracle/head.py, with g from oracle/grpo.py on the same logprobs) within
+the stored exponentials instead of a recompute (bf16: one scale per row times exponentials stored relative to a
+per-row offset; f16: half-tile exponentials scaled into dz), so its gradients must match octo_head_bwd's for the same
+g to the 16-bit roundings involved, and the fp64 oracle (oracle/head.py, with g from oracle/grpo.py on the same logprobs) within
 the relative Frobenius bar 1e-2 (16-bit; 1e-4 for fp32, which runs the forward and the backward). The cases cover
 the plan's branches: one pass and several (fp32 grad_W partials, passes past the device row count), W read K-major
 as stored and W^T staged (V not a multiple of 64), the softcap, fp8 weights (grad_h only), the compacted rows read
@@ -109,7 +110,8 @@ def test_step_matches_forward_backward_and_oracle(dtype, shape):
     N, d, V = shape
     h, W, y, scored, mask, adv, noise = _batch(N, d, V, dtype, seed=91)
     bar = 1e-4 if dtype == torch.float32 else 1e-2
-    # 16-bit: dz differs from the backward's by the rounding of the f16 exponential (at most 2^-11 relative)
+    # 16-bit: dz differs from the backward's by the rounding of the stored exponential (bf16: 2^-9 relative in place
+    # of the backward's rounding of dz, and the scaled h^T's; f16: 2^-11 relative besides it)
     vs_two = 1e-6 if dtype == torch.float32 else 4e-3
     for T, post in ((1.0, (1.0, 1.0, False)), (0.7, (0.5, 2.0, True))):
         lp0 = head_op.head_fwd(h.to(DEV), W.to(DEV), None, y.to(DEV), None, None, 1.0 / T, *post, False, False)[0]
@@ -193,8 +195,9 @@ def test_step_grad_h_alone_reads_a_staged_w_transpose(passes):
 
 def test_step_extreme_logits():
     """Every row's hidden vector is e_0, so logit j is W[j, 0]: a 600-nat peak in the last vocabulary tile against
-    logits in [-50, 50] (the other tiles' exponentials scale to exact zeros), and logits near -1,000 at T 0.7 (each
-    tile's maximum far from zero). The gradients against the two-call backward's, whose own agreement with the
+    logits in [-50, 50] (the other tiles' exponentials scale to exact zeros; the rows not labelled with the peak lie
+    far below their maximum and take the row-offset rescale), and logits near -1,000 at T 0.7 (each tile's maximum
+    far from zero). The gradients against the two-call backward's, whose own agreement with the
     oracle at these logits is bounded in tests/test_gpu_head.py."""
     N, d, V = 300, 64, 1000
     h = torch.zeros(N, d, dtype=torch.bfloat16)
@@ -222,10 +225,36 @@ def test_step_extreme_logits():
         assert _rel(gw_s, gw_t) <= 4e-3, T
         # grad_h at logits near -1,000 is a sum of large cancelling terms (the weights share a -1,000 component): the
         # 16-bit rounding of dz dominates either way (2^-9 relative per element, about 0.7 of the result in the
-        # two-call backward, tests/test_gpu_head.py); the step's extra f16 rounding adds at most a quarter of that
+        # two-call backward, tests/test_gpu_head.py); the step's rounding of its stored exponentials is of the same size
         gh_ref, _ = ohead.head_backward(h, W, y, T, g_s.cpu(), want_w=False)
         e_two = _rel(gh_t.cpu(), gh_ref)
         assert _rel(gh_s.cpu(), gh_ref) <= 1e-2 + 1.5 * e_two, (T, e_two)
+
+
+@pytest.mark.parametrize("weights", ["bf16", "fp8"])
+def test_step_rows_far_below_their_maximum_are_rescaled(weights):
+    """bf16 operands store each row's exponentials relative to an offset 48 (base 2) above the row's label logit, so
+    dz is one scale per row times the stored values; a row whose maximum lies more than 112 (base 2, 77.6 nats) above
+    its label's logit is rescaled after the merge instead. At T 0.01 the logits spread over about +-100 nats: most
+    rows, with random labels, take the rescale, and every third row, labelled with its own argmax, does not. Three
+    passes with the device count inside the second; against the two-call route and the fp64 oracle."""
+    from octopus_amd.workloads import quantise_fp8_rows
+    N, d, V, T = 6000, 256, 5120, 0.01
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, torch.bfloat16, seed=98)
+    sc, W32, code, flags, need_w = None, W.float(), _lib.BF16, 0, True
+    if weights == "fp8":
+        W, sc = quantise_fp8_rows(W)
+        W32, code, flags, need_w = W.float() * sc[:, None], _lib.FP8E4M3, _lib.WS_NO_GRADW, False
+    z = h.float() @ W32.T / T
+    y[::3] = z.argmax(1)[::3]
+    gap = (z.max(1).values - z.gather(1, y[:, None])[:, 0]) * 1.4426950408889634
+    assert int((scored & (gap > 113)).sum()) > 500 and int((scored & (gap < 111)).sum()) > 500
+    ws, plan = _step_ws(N, d, V, code, flags, lambda p: p[1] == 3)
+    lp0 = head_op.head_fwd(h.to(DEV), W.to(DEV), None if sc is None else sc.to(DEV), y.to(DEV), None, None, 1.0 / T,
+                           1.0, 1.0, False, False, False)[0]
+    old = lp0[:, 0].cpu() + noise
+    idx, count, step, two = _run(h, W, y, scored, mask, adv, old, T, w_scale=sc, need_w=need_w, ws=ws)
+    _check(h, W32, y, scored, mask, adv, old, T, (1.0, 1.0, False), step, two, need_w, 1e-2, 4e-3)
 
 
 def test_step_grad_w_only():
