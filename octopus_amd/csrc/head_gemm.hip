@@ -53,9 +53,11 @@ template <int NJ> struct DzSwz<Acc16N<NJ>> {
 // ---- epilogue: online softmax statistics ----------------------------------------------------
 
 // acc *= per-vocab-row scale (fp8 weights), then the softcap tanh if any; then stats per token.
+// wsl (optional): the tile's row scales staged in LDS (0 past V), read instead of wscale.
 template <class L, bool A_FP8, bool TANH>
 __device__ __forceinline__ void pre_transform(typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int lane,
-                                              const float *wscale, int64_t V, float pre) {
+                                              const float *wscale, int64_t V, float pre,
+                                              const __attribute__((address_space(3))) f32x4 *wsl = nullptr) {
   if constexpr (A_FP8) {
 #pragma unroll
     for (int i = 0; i < L::NI; ++i) {
@@ -63,7 +65,11 @@ __device__ __forceinline__ void pre_transform(typename L::V (&acc)[L::NI][L::NJ]
 #pragma unroll
       for (int g4 = 0; g4 < L::NV / 4; ++g4) {
         int64_t row = m0 + L::row(wm, i, 4 * g4, lane);
-        if (row + 3 < V) {
+        if (wsl) {
+          const f32x4 q = wsl[L::row(wm, i, 4 * g4, lane) >> 2];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) sc[4 * g4 + u] = q[u];
+        } else if (row + 3 < V) {
           f32x4 q = *(const f32x4 *)(wscale + row);
 #pragma unroll
           for (int u = 0; u < 4; ++u) sc[4 * g4 + u] = q[u];
@@ -95,13 +101,13 @@ typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 // times the softcap's derivative 1 - x^2 when TANH (acc holds x = tanh(pre z) then), is also written into the LDS
 // staging tile, laid out as dz_stage lays out dz (zero past V and for tokens at or past nvalid). EXM 1: as f16,
 // relative to the wave's own maximum, which the tile's part keeps. EXM 2: as bf16, times exp2(min(m2 - xoff[token],
-// kExClamp)) (and the fp8 row scale when A_FP8), i.e. relative to the token's offset (StatsArgs::xoff; xoff here
-// points at the tile's first token).
+// kExClamp)) (and the fp8 row scale when A_FP8, from the tile's 256 scales staged in LDS at wsl), i.e. relative to
+// the token's offset (StatsArgs::xoff; xoff here points at the tile's first token).
 template <class L, bool MASK, int EXM = 0, bool TANH = false, bool A_FP8 = false>
 __device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int wn,
                                            int lane, int64_t V, float c, lds_f32x4 *red, lds_char *tile = nullptr,
                                            int64_t nvalid = 0, const float *xoff = nullptr,
-                                           const float *wscale = nullptr) {
+                                           const lds_f32x4 *wsl = nullptr) {
 #pragma unroll
   for (int j = 0; j < L::NJ; ++j) {
     float mx = -INFINITY;
@@ -144,16 +150,10 @@ __device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::
         }
         if constexpr (EXM != 0) {
           const int rl = L::row(wm, i, 4 * g4, lane);  // first of this lane's 4 vocab rows in the tile
-          if constexpr (EXM == 2 && A_FP8) {  // d/d(raw e4m3 product): times the row's scale (0 past V)
-            const int64_t row = m0 + rl;
-            if (row + 3 < V) {
-              const f32x4 q = *(const f32x4 *)(wscale + row);
+          if constexpr (EXM == 2 && A_FP8) {  // d/d(raw e4m3 product): times the rows' scales (LDS, 0 past V)
+            const f32x4 q = wsl[rl >> 2];
 #pragma unroll
-              for (int u = 0; u < 4; ++u) x4[u] *= q[u];
-            } else {
-#pragma unroll
-              for (int u = 0; u < 4; ++u) x4[u] *= (row + u < V) ? wscale[row + u] : 0.f;
-            }
+            for (int u = 0; u < 4; ++u) x4[u] *= q[u];
           }
           i32x2 pk;
           if constexpr (EXM == 2) {
@@ -701,7 +701,7 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
 template <int DT, bool A_FP8, bool TANH, int EX>
 __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_stats8_kernel(Operand A, Operand B, GemmShape s, StatsArgs e) {
   static_assert(ring5_ok(DT), "16-bit operands");
-  static_assert(256 * 512 + 512 * 16 <= SMEM_RING5, "staging tile and statistics fit the ring's LDS");
+  static_assert(256 * 512 + 512 * 16 + 256 * 4 <= SMEM_RING5, "staging tile, statistics and scales fit the LDS");
   typedef Acc16N<4> L;
   __shared__ __attribute__((aligned(16))) char smem_[SMEM_RING5];
   lds_char *smem = (lds_char *)smem_;
@@ -715,10 +715,25 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
   f32x4 acc[8][4];
   mainloop_ring5<DT, OpRowsN<8, 128>, OpRowsN<8, 64>, true>(A, B, m0, n0, s.K, smem, acc);
   const int64_t ma = e.v0 + m0;  // first vocabulary row of the tile
-  pre_transform<L, A_FP8, TANH>(acc, ma, wm, lane, e.wscale, e.V, e.pre);
+  lds_f32x4 *wsl = (lds_f32x4 *)(smem + 256 * 512 + 512 * 16);
+  if constexpr (A_FP8) {  // the tile's row scales, read once (the ring is free now)
+    if (threadIdx.x < 64) {
+      const int64_t row = ma + 4 * threadIdx.x;
+      f32x4 q;
+      if (row + 3 < e.V) {
+        q = *(const f32x4 *)(e.wscale + row);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) q[u] = (row + u < e.V) ? e.wscale[row + u] : 0.f;
+      }
+      wsl[threadIdx.x] = q;
+    }
+    __syncthreads();
+  }
+  pre_transform<L, A_FP8, TANH>(acc, ma, wm, lane, e.wscale, e.V, e.pre, A_FP8 ? wsl : nullptr);
   const float *xo = EX == 2 ? e.xoff + n0 : nullptr;
-  if (ma + TM > e.V) stats_cols<L, true, EX, TANH, A_FP8>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid, xo, e.wscale);
-  else stats_cols<L, false, EX, TANH, A_FP8>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid, xo, e.wscale);
+  if (ma + TM > e.V) stats_cols<L, true, EX, TANH, A_FP8>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid, xo, wsl);
+  else stats_cols<L, false, EX, TANH, A_FP8>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid, xo, wsl);
   __syncthreads();  // per-wave statistics (and the staging tile) written
   const int t = threadIdx.x;
   if (t < nvalid) {  // (m_a, S, U, m_b): S and U relative to max(m_a, m_b), the halves' maxima kept
