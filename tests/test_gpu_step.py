@@ -257,6 +257,36 @@ def test_step_rows_far_below_their_maximum_are_rescaled(weights):
     _check(h, W32, y, scored, mask, adv, old, T, (1.0, 1.0, False), step, two, need_w, 1e-2, 4e-3)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_step_labels_outside_the_vocabulary_on_masked_rows(dtype):
+    """A label outside [0, V) (here -1 and V) gives its row a logprob of NaN and no label entry; on a row the GRPO mask
+    leaves out, g is 0. bf16 gives such a row the offset -inf, so it takes the rescale after the merge; either way its
+    gradient rows must be exactly 0 and every other row's as the oracle's and the two-call route's."""
+    N, d, V = 1500, 256, 5120
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, dtype, seed=99)
+    bad = torch.zeros(N, dtype=torch.bool)
+    bad[::7] = True
+    y[bad] = torch.where(torch.arange(N)[bad] % 2 == 0, torch.tensor(-1), torch.tensor(V))
+    mask[bad] = 0.0
+    lp0 = head_op.head_fwd(h.to(DEV), W.to(DEV), None, y.to(DEV), None, None, 1.0, 1.0, 1.0, False, False, False)[0]
+    old = lp0[:, 0].cpu() + noise
+    idx, count, step, two = _run(h, W, y, scored, mask, adv, old, 1.0)
+    out_s, lse_s, g_s, loss_s, gh_s, gw_s = step
+    out_t, lse_t, g_t, loss_t, gh_t, gw_t = two
+    sel = scored.nonzero()[:, 0]
+    n = sel.numel()
+    badc = bad[sel]
+    assert int(badc.sum()) > 50 and torch.equal(g_s, g_t)
+    assert torch.isnan(out_s[:, 0].cpu()[bad & scored]).all() and (g_s[:n].cpu()[badc] == 0).all()
+    gh_s, gw_s = gh_s.cpu(), gw_s.cpu()
+    assert torch.isfinite(gh_s).all() and torch.isfinite(gw_s).all()
+    assert (gh_s[bad] == 0).all()
+    good = sel[~badc]
+    gh_ref, gw_ref = ohead.head_backward(h[good], W.float(), y[good], 1.0, g_s[:n].cpu()[~badc])
+    assert _rel(gh_s[good], gh_ref) <= 1e-2 and _rel(gw_s, gw_ref) <= 1e-2
+    assert _rel(gh_s, gh_t.cpu()) <= 4e-3 and _rel(gw_s, gw_t.cpu()) <= 4e-3
+
+
 def test_step_grad_w_only():
     """grad_W without grad_h (the rows frozen): over two passes, against the two-call backward and the oracle."""
     N, d, V = 3000, 256, 5120
