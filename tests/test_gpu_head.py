@@ -393,26 +393,30 @@ def test_pair_gather_and_expansion_match_the_reference_composition():
 
 
 def test_bound_head_on_a_model_matches_its_own_logits():
-    """Reference tests/test_lm_head.py:11-34 on the GPU, through the fused HIP head (fp32, atol 1e-5)."""
-    from transformers import AutoModelForCausalLM, Gemma2Config, LlamaConfig
+    """The property of reference tests/test_lm_head.py:11-34 on the GPU, through the fused HIP head: once bound, a
+    Llama and a softcapped Gemma2 return each position's next-token log-probability and the entropy of their own fp32
+    logits (torch.distributions.Categorical), at T 1.0 and 0.7, to 1e-5."""
+    from transformers import AutoModelForCausalLM
     from octopus_amd.rl.lm_head import bind_head
-    small = dict(vocab_size=96, hidden_size=32, intermediate_size=64, num_hidden_layers=2, num_attention_heads=2,
-                 num_key_value_heads=1, head_dim=16)
-    for config in (LlamaConfig(**small), Gemma2Config(**small, final_logit_softcapping=2.0)):
-        torch.manual_seed(0)
-        model = AutoModelForCausalLM.from_config(config, attn_implementation="eager").eval().to(DEV)
-        ids = torch.randint(0, 96, (1, 12), device=DEV)
-        labels = torch.roll(ids, -1, -1).reshape(-1)
+    from tests.tiny_models import families
+    for name, config, _ in families():
+        if name not in ("llama", "gemma2"):
+            continue
+        torch.manual_seed(3)
+        model = AutoModelForCausalLM.from_config(config, attn_implementation="eager").to(DEV)
+        model.eval()
+        ids = torch.randint(0, config.vocab_size, (1, 19), generator=torch.Generator().manual_seed(4)).to(DEV)
+        nxt = ids[0].roll(-1)
         with torch.no_grad():
-            own = model(input_ids=ids).logits[0].float()
+            own = model(input_ids=ids).logits[0].double()
         for T in (1.0, 0.7):
             head = bind_head(model, T)
-            head.octopus_labels, head.octopus_tree = labels, None
+            head.octopus_labels, head.octopus_tree = nxt, None
             with torch.no_grad():
-                out = model(input_ids=ids).logits[0]
-            logp = torch.log_softmax(own / T, -1)
-            assert torch.allclose(out[:, 0], logp.gather(-1, labels[:, None])[:, 0], atol=1e-5)
-            assert torch.allclose(out[:, 1], -(logp.exp() * logp).sum(-1), atol=1e-5)
+                cols = model(input_ids=ids).logits[0].double()
+            want = torch.distributions.Categorical(logits=own / T)
+            assert (cols[:, 0] - want.log_prob(nxt)).abs().max().item() <= 1e-5, (name, T)
+            assert (cols[:, 1] - want.entropy()).abs().max().item() <= 1e-5, (name, T)
 
 
 def test_head_columns_hip_matches_eager():

@@ -26,7 +26,8 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "pre
 
 
 def _flat(seqs):
-    return np.concatenate(seqs).astype(np.int64), [0, *np.cumsum([len(s) for s in seqs]).tolist()]
+    from tests.tiny_models import packed
+    return packed(seqs)
 
 
 def _forest(rng, n_seq, vocab=6):
@@ -99,7 +100,7 @@ def test_device_pairs_at_measured_sizes_match_the_host_restatement():
 
 
 def test_tree_positions_out_of_range_are_counted_and_get_no_pair():
-    flat, cu = _flat([np.array([1, 2, 3, 4]), np.array([1, 2, 9])])
+    flat, cu = _flat([[1, 2, 3, 4], [1, 2, 9]])
     f2t = np.array([0, 1, 2, 3, 0, 7, 4], dtype=np.int64)  # position 5 -> tree position 7 of 5
     dpos, dlab, dfp, c = _device(flat, cu, f2t, 5, None)
     assert c == [3, 1]

@@ -11,13 +11,7 @@ from octopus_amd.rl import lm_head, prefix_tree, seq_tiles
 from octopus_amd.rl.lm_head import _fused_post, bind_head
 from octopus_amd.rl.prefix_tree import TreeMeta, build_tree, tree_head_output
 from oracle import pairs as opairs
-
-SMALL = dict(vocab_size=96, hidden_size=32, intermediate_size=64, num_hidden_layers=2, num_attention_heads=2,
-             num_key_value_heads=1, head_dim=16)
-
-
-def _flat(seqs):
-    return np.concatenate(seqs), [0, *np.cumsum([len(s) for s in seqs]).tolist()]
+from tests.tiny_models import TINY, families, packed
 
 
 def _random_forest(rng, n_seq):
@@ -35,7 +29,7 @@ def _random_forest(rng, n_seq):
 def test_build_tree_matches_the_trie_oracle(seed):
     rng = np.random.default_rng(seed)
     seqs = _random_forest(rng, int(rng.integers(1, 9)))
-    flat, cu = _flat(seqs)
+    flat, cu = packed(seqs)
     if len(flat) == 0:
         return
     scored = None if seed % 3 == 0 else rng.random(len(flat)) < 0.5
@@ -46,19 +40,20 @@ def test_build_tree_matches_the_trie_oracle(seed):
     pos, lab, fp = opairs.pairs(flat, cu, scored)
     assert np.array_equal(tree.pair_pos, pos) and np.array_equal(tree.pair_label, lab)
     assert np.array_equal(tree.flat_pair, fp)
-    for node in tree.nodes:  # pre-order ranges tile the tree; a node's path ends with its own tokens
-        assert (node.path[-(node.end - node.start):] == np.arange(node.start, node.end)).all()
+    for node in tree.nodes:  # the last (end - start) entries of a node's path are its own tree range, in order
+        own = np.arange(node.start, node.end)
+        assert np.array_equal(node.path[len(node.path) - own.size:], own)
 
 
 def test_build_tree_reference_cases():
-    flat, cu = _flat([np.array([1, 2, 3, 4]), np.array([1, 2, 9])])
+    flat, cu = packed([[1, 2, 3, 4], [1, 2, 9]])
+    assert build_tree(flat, cu).tokens.tolist() == [1, 2, 3, 4, 9]
+    big = (1 << 21) + 3  # token ids past 2^20
+    flat, cu = packed([[5, big, 7], [5, big, (1 << 20) + 9]])
     tree = build_tree(flat, cu)
-    assert tree.tokens.tolist() == [1, 2, 3, 4, 9]
-    flat, cu = _flat([np.array([5, (1 << 21) + 3, 7]), np.array([5, (1 << 21) + 3, (1 << 20) + 9])])
-    tree = build_tree(flat, cu)
-    for p in (0, 1, 3, 4):
-        row = tree.flat_pair[p]
-        assert tree.tokens[tree.pair_pos[row]] == flat[p] and tree.pair_label[row] == flat[p + 1]
+    for p in (0, 1, 3, 4):  # each position that asks: its pair's hidden row holds its own token, the label the next
+        pos, lab = tree.pair_pos[tree.flat_pair[p]], tree.pair_label[tree.flat_pair[p]]
+        assert (tree.tokens[pos], lab) == (flat[p], flat[p + 1])
     with pytest.raises(NotImplementedError):
         build_tree(flat, cu, mounts={1: [(1, 0, 0, 2)]})
 
@@ -100,21 +95,6 @@ def test_tree_head_output_gives_each_position_its_own_next_token(case):
     assert torch.equal(out.to(torch.float64), want)
 
 
-def _families():
-    from transformers import FalconH1Config, Gemma2Config, GraniteMoeHybridConfig, LlamaConfig
-    return [
-        LlamaConfig(**SMALL),
-        GraniteMoeHybridConfig(**SMALL, logits_scaling=3.0, layer_types=["mamba", "attention"], mamba_n_heads=4,
-                               mamba_d_head=16, mamba_d_state=8, mamba_chunk_size=8),
-        Gemma2Config(**SMALL, final_logit_softcapping=2.0),
-        FalconH1Config(**SMALL, lm_head_multiplier=0.25, mamba_n_heads=4, mamba_d_head=16, mamba_d_ssm=64,
-                       mamba_d_state=8, mamba_chunk_size=8),
-    ]
-
-
-EXPECTED_POST = [dict(pre=1.0, post=1.0, tanh=False), dict(pre=1 / 3.0, post=1.0, tanh=False),
-                 dict(pre=0.5, post=2.0, tanh=True), dict(pre=0.25, post=1.0, tanh=False)]
-
 
 @pytest.mark.parametrize("k", range(4), ids=["llama", "granitemoehybrid", "gemma2", "falcon_h1"])
 def test_bound_head_reproduces_each_familys_softmax(k):
@@ -124,9 +104,10 @@ def test_bound_head_reproduces_each_familys_softmax(k):
     unbound model's logits in fp64, at T 1.0, 0.7 and 1.6. The fused epilogue's reading of each family's recorded
     chain is checked beside it."""
     from transformers import AutoModelForCausalLM
-    config = _families()[k]
+    _, config, (pre, post, tanh) = families()[k]
     torch.manual_seed(40 + k)
-    model = AutoModelForCausalLM.from_config(config, attn_implementation="eager").eval()
+    model = AutoModelForCausalLM.from_config(config, attn_implementation="eager")
+    model.eval()
     ids = torch.randint(0, config.vocab_size, (1, 15), generator=torch.Generator().manual_seed(50 + k))
     nxt = ids[0].roll(-1)
     with torch.no_grad():
@@ -140,8 +121,8 @@ def test_bound_head_reproduces_each_familys_softmax(k):
         assert (cols[:, 0] - want.log_prob(nxt)).abs().max().item() <= 1e-5, temperature
         assert (cols[:, 1] - want.entropy()).abs().max().item() <= 1e-5, temperature
     assert (len(head.octopus_post) > 0) == (config.model_type != "llama")
-    post, exp = _fused_post(head.octopus_post), EXPECTED_POST[k]
-    assert abs(post.pre - exp["pre"]) < 1e-12 and abs(post.post - exp["post"]) < 1e-12 and post.tanh == exp["tanh"]
+    fp = _fused_post(head.octopus_post)
+    assert abs(fp.pre - pre) < 1e-12 and abs(fp.post - post) < 1e-12 and fp.tanh == tanh
 
 
 def _llama_with_tail(after_head):
@@ -153,14 +134,14 @@ def _llama_with_tail(after_head):
     class TailedLlama(LlamaForCausalLM):
         def __init__(self, config):
             super().__init__(config)
-            self.extra = torch.nn.Linear(config.vocab_size, config.vocab_size)
+            self.side = torch.nn.Linear(config.vocab_size, config.vocab_size, bias=False)
 
-        def forward(self, input_ids=None, **kwargs):
-            states = self.model(input_ids=input_ids).last_hidden_state
-            return CausalLMOutput(logits=after_head(self, self.lm_head(states)))
+        def forward(self, input_ids, **_unused):
+            last = self.model(input_ids=input_ids).last_hidden_state
+            return CausalLMOutput(logits=after_head(self, self.lm_head(last)))
 
     torch.manual_seed(7)
-    return TailedLlama(LlamaConfig(**SMALL))
+    return TailedLlama(LlamaConfig(**TINY))
 
 
 def _set_first(x):
@@ -172,7 +153,7 @@ def _set_first(x):
     lambda m, x: x.clamp_(min=-4.0),                 # a write into the head's output
     lambda m, x: _set_first(x),                      # an indexed write
     lambda m, x: torch.maximum(x * 2.0, x),          # the flow forks: the earlier result is read again
-    lambda m, x: m.extra(x),                         # a further submodule
+    lambda m, x: m.side(x),                          # a further submodule
 ], ids=["inplace", "setitem", "fork", "submodule"])
 def test_post_head_flows_one_chain_cannot_replay_are_refused(after_head):
     """The refusals of reference tests/test_lm_head.py:37-55: bind_head raises NotImplementedError for logits that no
@@ -185,7 +166,7 @@ def test_a_replayable_post_head_chain_is_bound_and_fused():
     """A chain of the kinds the fused epilogue takes (a divide, tanh, a multiply) is recorded, read as
     4 tanh(z / 4), and the bound head reproduces the tailed model's own softmax."""
     model = _llama_with_tail(lambda m, x: torch.tanh(x / 4.0) * 4.0).eval()
-    ids = torch.randint(0, SMALL["vocab_size"], (1, 9), generator=torch.Generator().manual_seed(8))
+    ids = torch.randint(0, TINY["vocab_size"], (1, 9), generator=torch.Generator().manual_seed(8))
     with torch.no_grad():
         own = model(input_ids=ids).logits[0].double()
     head = bind_head(model, 0.9)
@@ -204,8 +185,8 @@ def test_scored_positions_alone_give_the_same_values_and_gradients():
     scored positions is exactly the same for every parameter (torch.autograd.grad of both runs)."""
     from transformers import AutoModelForCausalLM, LlamaConfig
     torch.manual_seed(11)
-    model = AutoModelForCausalLM.from_config(LlamaConfig(**SMALL), attn_implementation="eager").double()
-    ids = torch.randint(0, SMALL["vocab_size"], (1, 14), generator=torch.Generator().manual_seed(12))
+    model = AutoModelForCausalLM.from_config(LlamaConfig(**TINY), attn_implementation="eager").to(torch.float64)
+    ids = torch.randint(0, TINY["vocab_size"], (1, 14), generator=torch.Generator().manual_seed(12))
     head = bind_head(model, 0.8)
     head.octopus_labels, head.octopus_tree = ids[0].roll(-1), None
     keep = torch.rand(14, generator=torch.Generator().manual_seed(13)) < 0.5

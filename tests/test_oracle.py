@@ -43,43 +43,30 @@ def test_columns_closed_forms():
     assert abs(lp[1].item() + 200.0) < 1e-9  # a label that is not the peak
 
 
-SMALL = dict(vocab_size=96, hidden_size=32, intermediate_size=64, num_hidden_layers=2, num_attention_heads=2,
-             num_key_value_heads=1, head_dim=16)
-
-
-def _families():
-    from transformers import FalconH1Config, Gemma2Config, GraniteMoeHybridConfig, LlamaConfig
-    return [
-        (LlamaConfig(**SMALL), dict()),
-        (GraniteMoeHybridConfig(**SMALL, logits_scaling=3.0, layer_types=["mamba", "attention"], mamba_n_heads=4,
-                                mamba_d_head=16, mamba_d_state=8, mamba_chunk_size=8), dict(pre=1 / 3.0)),
-        (Gemma2Config(**SMALL, final_logit_softcapping=2.0), dict(pre=0.5, post=2.0, tanh=True)),
-        (FalconH1Config(**SMALL, lm_head_multiplier=0.25, mamba_n_heads=4, mamba_d_head=16, mamba_d_ssm=64,
-                        mamba_d_state=8, mamba_chunk_size=8), dict(pre=0.25)),
-    ]
-
-
 @pytest.mark.parametrize("k", range(4), ids=["llama", "granitemoehybrid", "gemma2", "falcon_h1"])
 def test_head_forward_matches_the_models_own_logits(k):
-    """The oracle on the lm_head input equals log_softmax of the model's own logits (reference
-    tests/test_lm_head.py:11-34, same tiny configs, T in {1.0, 0.7}, atol 1e-5)."""
+    """The oracle on the lm_head input, with the family's post-head transform, gives the log-probability of each
+    position's next token and the entropy of the model's own logits (the property of reference
+    tests/test_lm_head.py:11-34), here against torch.distributions.Categorical in fp64 at T 1.0 and 0.7, to 1e-5."""
     from transformers import AutoModelForCausalLM
-    config, post = _families()[k]
-    torch.manual_seed(0)
-    model = AutoModelForCausalLM.from_config(config, attn_implementation="eager").eval()
-    ids = torch.randint(0, config.vocab_size, (1, 12))
-    labels = torch.roll(ids, -1, -1).reshape(-1)
-    seen = {}
-    hook = model.get_output_embeddings().register_forward_hook(lambda m, a, o: seen.update(h=a[0]))
+    from tests.tiny_models import families
+    _, config, (pre, post, tanh) = families()[k]
+    torch.manual_seed(20 + k)
+    model = AutoModelForCausalLM.from_config(config, attn_implementation="eager")
+    model.eval()
+    ids = torch.randint(0, config.vocab_size, (1, 17), generator=torch.Generator().manual_seed(30 + k))
+    nxt = ids[0].roll(-1)
+    head_in = []
+    handle = model.get_output_embeddings().register_forward_hook(lambda mod, inp, out: head_in.append(inp[0]))
     with torch.no_grad():
-        own = model(input_ids=ids).logits[0].float()
-    hook.remove()
-    h, W = seen["h"][0], model.get_output_embeddings().weight.detach()
+        own = model(input_ids=ids).logits[0].double()
+    handle.remove()
+    W = model.get_output_embeddings().weight.detach()
     for T in (1.0, 0.7):
-        lp, ent, _ = ohead.head_forward(h, W, labels, T, **post)
-        logp = torch.log_softmax(own / T, -1)
-        assert torch.allclose(lp.float(), logp.gather(-1, labels[:, None])[:, 0], atol=1e-5)
-        assert torch.allclose(ent.float(), -(logp.exp() * logp).sum(-1), atol=1e-5)
+        lp, ent, _ = ohead.head_forward(head_in[0][0], W, nxt, T, pre=pre, post=post, tanh=tanh)
+        want = torch.distributions.Categorical(logits=own / T)
+        assert (lp.double() - want.log_prob(nxt)).abs().max().item() <= 1e-5, T
+        assert (ent.double() - want.entropy()).abs().max().item() <= 1e-5, T
 
 
 @pytest.mark.parametrize("post", [dict(), dict(pre=0.5, post=2.0, tanh=True), dict(pre=0.25)])
@@ -140,13 +127,14 @@ def test_compaction_is_nonzero():
 
 
 def _flat(seqs):
-    return np.concatenate(seqs), [0, *np.cumsum([len(s) for s in seqs]).tolist()]
+    from tests.tiny_models import packed
+    return packed(seqs)
 
 
 def test_trie_pairs_expand_to_flat_positions():
     """Reference tests/test_prefix_tree.py:165-176: tree tokens 1 2 3 4 9; flat position 1 ('2') asks for a
     different next token per sequence (3 vs 9); last positions ask for none."""
-    flat, cu = _flat([np.array([1, 2, 3, 4]), np.array([1, 2, 9])])
+    flat, cu = _flat([[1, 2, 3, 4], [1, 2, 9]])
     tokens, f2t, posid = opairs.tree_positions(flat, cu)
     assert tokens.tolist() == [1, 2, 3, 4, 9] and posid.tolist() == [0, 1, 2, 3, 2]
     pos, lab, fp = opairs.pairs(flat, cu)
@@ -182,9 +170,8 @@ def test_tree_output_gives_each_flat_position_its_pairs_row(case):
 
 def test_trie_pairs_of_scored_positions():
     """Reference tests/test_prefix_tree.py:179-188."""
-    flat, cu = _flat([np.array([1, 2, 3, 4]), np.array([1, 2, 3, 5]), np.array([1, 2, 9])])
-    scored = np.zeros(len(flat), dtype=bool)
-    scored[[1, 9]] = True
+    flat, cu = _flat([[1, 2, 3, 4], [1, 2, 3, 5], [1, 2, 9]])
+    scored = np.isin(np.arange(flat.size), [1, 9])
     pos, lab, fp = opairs.pairs(flat, cu, scored)
     fpos, flab, ffp = opairs.pairs(flat, cu)
     assert len(pos) == 2 and (fp[~scored] == -1).all()
@@ -197,7 +184,9 @@ def test_trie_dedups_shared_prefixes_and_keeps_every_sequence_exact():
     """Reference tests/test_prefix_tree.py:28-50."""
     rng = np.random.default_rng(0)
     prefix = rng.integers(0, 1000, 50)
-    seqs = [np.concatenate([prefix, rng.integers(0, 1000, n)]) for n in (7, 3, 12)]
+    seqs = []
+    for tail in (7, 3, 12):  # three continuations of the shared 50-token prefix
+        seqs.append(np.concatenate([prefix, rng.integers(0, 1000, tail)]))
     seqs.append(np.concatenate([prefix[:20], rng.integers(0, 1000, 5)]))
     seqs.append(seqs[1].copy())
     seqs.append(rng.integers(1000, 2000, 9))
@@ -216,11 +205,12 @@ def test_trie_dedups_shared_prefixes_and_keeps_every_sequence_exact():
 
 def test_trie_pairs_with_vocab_above_2_20():
     """Reference tests/test_prefix_tree.py:430-434."""
-    flat, cu = _flat([np.array([5, (1 << 21) + 3, 7]), np.array([5, (1 << 21) + 3, (1 << 20) + 9])])
+    big = (1 << 21) + 3
+    flat, cu = _flat([[5, big, 7], [5, big, (1 << 20) + 9]])
     tokens, _, _ = opairs.tree_positions(flat, cu)
     pos, lab, fp = opairs.pairs(flat, cu)
-    for p in (0, 1, 3, 4):
-        assert tokens[pos[fp[p]]] == flat[p] and lab[fp[p]] == flat[p + 1]
+    got = [(int(tokens[pos[fp[p]]]), int(lab[fp[p]])) for p in (0, 1, 3, 4)]
+    assert got == [(5, big), (big, 7), (5, big), (big, (1 << 20) + 9)]
 
 
 def test_grpo_closed_forms():
