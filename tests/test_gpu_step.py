@@ -358,6 +358,46 @@ def test_step_grad_w_accumulate_through_the_c_abi():
                   ctypes.byref(tail), P(gh), d, _lib.F32, P(gw), _lib.F32, P(ws), 1 << 20, st)
 
 
+def test_step_with_a_plain_lse_through_the_c_abi():
+    """A C-ABI caller without OCTO_LSE_PAIR gets the natural-log lse per row; the row-offset dz scales and the rescale
+    of rows far below their maximum then read the row state from it. At T 0.012 over two passes (about 2,200 of the
+    3,000 rows rescaled),
+    the outputs and g must equal the paired call's bit for bit, and the gradients match it to 1e-3 and the oracle
+    to 1e-2."""
+    n, d, V, T = 3000, 256, 4096, 0.012
+    h, W, y, _, _, adv, noise = _batch(n, d, V, torch.bfloat16, seed=101)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    P = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    old = (head_op.head_fwd(hd, Wd, None, yd, None, None, 1.0 / T, 1.0, 1.0, False, False, False)[0][:, 0].cpu()
+           + noise).to(DEV)
+    advd, maskd = adv.to(DEV), torch.ones(n, device=DEV)
+    wsb, plan = _step_ws(n, d, V, _lib.BF16, 0, lambda p: p[1] == 2)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    runs = []
+    for flags, lse_cols in ((_lib.LSE_PAIR, 2), (0, 1)):
+        out = torch.zeros(n, 2, device=DEV)
+        lse = torch.zeros(n, lse_cols, device=DEV)
+        g = torch.zeros(n, device=DEV)
+        loss = torch.zeros((), device=DEV)
+        tail = _lib.GrpoTail(P(old), None, P(advd), P(maskd), n, *EPS, P(g), P(loss))
+        gh = torch.empty(n, d, dtype=torch.bfloat16, device=DEV)
+        gw = torch.empty(V, d, dtype=torch.bfloat16, device=DEV)
+        _lib.call("octo_head_step_grpo", P(hd), n, hd.stride(0), _lib.BF16, P(Wd), Wd.stride(0), _lib.BF16, None,
+                  P(yd), None, None, n, d, V, flags, 1.0 / T, 1.0, 1.0, 0, None, None, P(lse), P(out), 2,
+                  ctypes.byref(tail), P(gh), d, _lib.BF16, P(gw), _lib.BF16, P(ws), ws.numel(), st)
+        torch.cuda.synchronize()
+        runs.append((out.cpu(), g.cpu(), gh.cpu(), gw.cpu()))
+    (out_p, g_p, gh_p, gw_p), (out_l, g_l, gh_l, gw_l) = runs
+    z = h.float() @ W.float().T / T
+    gap = (z.max(1).values - z.gather(1, y[:, None])[:, 0]) * 1.4426950408889634
+    assert int((gap > 113).sum()) > 1500 and int((gap < 111).sum()) > 500
+    assert torch.equal(out_p, out_l) and torch.equal(g_p, g_l)
+    assert _rel(gh_l, gh_p) <= 1e-3 and _rel(gw_l, gw_p) <= 1e-3
+    gh_ref, gw_ref = ohead.head_backward(h, W.float(), y, T, g_l)
+    assert _rel(gh_l, gh_ref) <= 1e-2 and _rel(gw_l, gw_ref) <= 1e-2, plan
+
+
 def test_step_strided_rows_weight_and_grad_h_through_the_c_abi():
     """Hidden rows, weight and grad_h as strided views (row strides past d, bases offset into wider buffers) through
     the C ABI, over two passes: every output bitwise the contiguous call's (the same kernels and tile order, only the
