@@ -493,19 +493,27 @@ def _tree_batch(seed, n_seq=5, prefix=600, V=4096, d=256):
     return flat, cu, scored, tree, h, W, adv, mask
 
 
-@pytest.mark.parametrize("device_pairs", [False, True], ids=["host_pairs", "device_pairs"])
-@pytest.mark.parametrize("passes", [1, 3])
-def test_tree_step_matches_the_two_call_tree_route_and_oracle(device_pairs, passes):
+@pytest.mark.parametrize("device_pairs,passes,T", [
+    (False, 1, 0.8), (False, 3, 0.8), (True, 1, 0.8), (True, 3, 0.8), (True, 3, 0.012), (False, 1, 0.012),
+], ids=["host_pairs-1", "host_pairs-3", "device_pairs-1", "device_pairs-3", "device_pairs-3-rescaled",
+        "host_pairs-1-rescaled"])
+def test_tree_step_matches_the_two_call_tree_route_and_oracle(device_pairs, passes, T):
     """fused_grpo_tree_head over a prefix tree's pair rows: each flat token's columns bitwise the two-call tree route's
     (tree_head_output over the bound head), the loss to summation order, the gradients of hidden (pair rows summed
     into tree positions) and W against that route's autograd (fused_head, pairs_expand, grpo_loss, backward) and
     against the fp64 oracle with each pair row's g the sum of its flat tokens' GRPO weights (oracle/grpo.py);
     pairs built on the host (no-pair as the appended row P) and on the device (P on the device, no-pair -1), in one
-    pass and in three."""
+    pass and in three. At T 0.012 most pair rows lie far below their maximum and take the row-offset rescale, whose
+    dz scales use the g the flat tokens sum into each pair row after the merge."""
     from octopus_amd.head_op import fused_grpo_tree_head, fused_head
     from octopus_amd.rl.prefix_tree import TreeMeta, tree_head_output
     flat, cu, scored, tree, h, W, adv, mask = _tree_batch(101)
-    T = 0.8
+    if T < 0.1:
+        rows = h[torch.from_numpy(tree.pair_pos)].float()
+        z = rows @ W.float().T / T
+        lab = torch.from_numpy(tree.pair_label)
+        gap = (z.max(1).values - z.gather(1, lab[:, None])[:, 0]) * 1.4426950408889634
+        assert int((gap > 113).sum()) > 100 and int((gap < 111).sum()) > 20
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)  # noqa: E731
     meta = (TreeMeta.on_device(t(flat), t(np.asarray(cu)), t(tree.flat_to_tree), len(tree.tokens), t(scored))
             if device_pairs else TreeMeta(tree, DEV))
