@@ -18,6 +18,7 @@ reference algorithm timed on the host CPU beside it.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import platform
@@ -75,12 +76,13 @@ GEMM_KERNELS = ("gemm_stats", "gemm_dz", "gemm_store_grad_h", "gemm_store_grad_w
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 
-def recorded_traffic(kernel: str, workload: str, fused: bool = False):
+def recorded_traffic(kernel: str, workload: str, fused: bool = False, key: str = "traffic"):
     """HBM bytes per launch of `kernel` at `workload` as recorded from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs
-    (line `traffic <kernel>: <bytes>`) in profiles/step_kernels_<workload>.md for the fused step's launches, in
-    profiles/gemm_kernels_<workload>_counters.md for the two-call route's; None when not recorded."""
+    (line `traffic <kernel>: <bytes>`; with key, `<key> <kernel>: <bytes>`) in profiles/step_kernels_<workload>.md for
+    the fused step's launches, in profiles/gemm_kernels_<workload>_counters.md for the two-call route's; None when not
+    recorded."""
     path = os.path.join(PROFILES, f"step_kernels_{workload}.md" if fused else f"gemm_kernels_{workload}_counters.md")
-    key = f"traffic {kernel}:"
+    key = f"{key} {kernel}:"
     try:
         for line in open(path):
             if line.startswith(key):
@@ -233,6 +235,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="cfg3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--temperature", type=float, default=0.0,
+                    help="run the workload at this temperature instead of its own (low temperatures send most rows "
+                         "through the fused step's row-offset rescale)")
     ap.add_argument("--bwd-workspace-mib", type=int, default=0,
                     help="give the backward this much workspace instead of the queried size (its plan of row passes "
                          "and vocabulary chunks follows the workspace)")
@@ -283,6 +288,8 @@ def main() -> int:
         head_op.STEP_WORKSPACE_BYTES = args.bwd_workspace_mib << 20
 
     cfg = CONFIGS[args.workload]
+    if args.temperature > 0:
+        cfg = dataclasses.replace(cfg, temperature=args.temperature)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _lib.load()
@@ -305,11 +312,12 @@ def main() -> int:
         return idx, count, out, lse
 
     def forward_grpo():
-        # the forward with the GRPO weight dL/dlogprob of each compact row computed in its last kernel (ratio
-        # against the rollout's logprobs, eps 0.2 / 0.28, rejection 5.0), ready for the backward
+        # the forward with the GRPO weight dL/dlogprob of each compact row computed in its last kernel (the
+        # reference's decoupled objective: proximal logprobs = the forward's own, behaviour weight against the
+        # rollout's logprobs, eps 0.2 / 0.28, rejection 5.0), ready for the backward
         idx, count = head_op.compact_rows(b.scored)
         out, lse, g, loss = head_op.head_fwd_grpo(h, W, b.w_scale, y, idx, count, inv_T, 1.0, 1.0, False, True,
-                                                  True, old, None, b.adv, mask_f, 0.2, 0.28, 5.0)
+                                                  True, None, old, b.adv, mask_f, 0.2, 0.28, 5.0)
         return idx, count, out, lse, g
 
     def backward(idx, count, lse, g):
@@ -323,8 +331,22 @@ def main() -> int:
     def fused_step():
         # forward, GRPO weight and loss, grad_hidden and grad_W in one call, the logits computed once per row pass
         idx, count = head_op.compact_rows(b.scored)
-        return head_op.head_step_grpo(h, W, b.w_scale, y, idx, count, inv_T, 1.0, 1.0, False, True, True, old,
-                                      None, b.adv, mask_f, 0.2, 0.28, 5.0, True, need_w)
+        return head_op.head_step_grpo(h, W, b.w_scale, y, idx, count, inv_T, 1.0, 1.0, False, True, True, None,
+                                      old, b.adv, mask_f, 0.2, 0.28, 5.0, True, need_w)
+
+    # the bound route: the trainer's unchanged call path (bind_head's pre-hook binds the GRPO inputs; AReaL's loss on
+    # the head's logprob column; loss.backward()), here the head's forward as the bound model runs it, the objective
+    # (grpo_loss, the same reference objective) and autograd's backward, gradients set to None before each step
+    hb = h.detach().clone().requires_grad_(True)
+    Wb = W.detach().clone().requires_grad_(need_w and not cfg.fp8_weight)
+    grpo_in = head_op.GrpoInputs(adv=b.adv, old=old, prox=None, mask=mask_f)
+
+    def bound_step():
+        hb.grad, Wb.grad = None, None
+        idx, count = head_op.compact_rows(b.scored)
+        out = head_op.grpo_bound_head(hb, Wb, y, cfg.temperature, grpo_in, idx=idx, count=count, w_scale=b.w_scale)
+        loss, _ = head_op.grpo_loss(out[:, 0], None, old, b.adv, mask_f, 0.2, 0.28, 5.0)
+        loss.backward()
 
     fused = cfg.backward != "none" and not args.two_call
 
@@ -375,6 +397,18 @@ def main() -> int:
         bwd_ms.append(ev[2].elapsed_time(ev[3]))
     fwd_ms = sorted(fwd_ms)[reps // 2] if reps else None
     bwd_ms = sorted(bwd_ms)[reps // 2] if reps else None
+    bound_ms = None
+    if fused and reps:  # the bound route, same timing: one warm-up, the median of 3
+        bound_step()
+        torch.cuda.synchronize()
+        runs = []
+        for _ in range(3):
+            ev[0].record()
+            bound_step()
+            ev[1].record()
+            torch.cuda.synchronize()
+            runs.append(ev[0].elapsed_time(ev[1]))
+        bound_ms = sorted(runs)[1]
 
     n, d, V = scored_rows, cfg.d, cfg.V
     alg_flop = {"full": 6, "hidden": 4, "none": 2}[cfg.backward] * n * d * V
@@ -403,14 +437,33 @@ def main() -> int:
     for name, k in kernels.items():  # fabric (HBM side of L2) bytes per launch from the recorded rocprof counters
         t = recorded_traffic(name, cfg.name, fused)
         k["traffic_GBps"] = t / (k["avg_ms"] / 1e3) / 1e9 if t else None
-    # the weight stream: the logits GEMM reads W (its MFMA operand: bf16, fp8 weights widened) once per launch
+    # the weight stream: the logits GEMM reads W (its MFMA operand: bf16, fp8 weights widened) once per launch that
+    # has rows to score. The fused step's launches past the device row count end at once and read nothing, so W is
+    # read once per row pass holding scored rows (ceil(n / rows per pass) of them); the forward reads it once.
     w_bytes = V * d * (4 if cfg.dtype == torch.float32 else 2)
     weight_stream = None
     if "gemm_stats" in kernels:
         ks = kernels["gemm_stats"]
-        weight_stream = {"bytes_per_launch": w_bytes, "kernel": "gemm_stats",
-                         "GBps": w_bytes / (ks["avg_ms"] / 1e3) / 1e9,
+        reads = 1
+        if fused:
+            w_code = _lib.FP8E4M3 if cfg.fp8_weight else {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16,
+                                                           torch.float32: _lib.F32}[cfg.dtype]
+            fl = _lib.WS_STEP | (0 if need_w else _lib.WS_NO_GRADW)
+            ws = head_op.STEP_WORKSPACE_BYTES or _lib.workspace_bytes(cfg.N, d, V, w_code, fl)
+            rows_per_pass = _lib.bwd_plan(cfg.N, d, V, w_code, fl, ws)[0]
+            reads = -(-n // rows_per_pass)
+        weight_stream = {"bytes_per_read": w_bytes, "kernel": "gemm_stats", "reads_per_step": reads,
+                         "GBps": w_bytes * reads / (ks["ms_per_step"] / 1e3) / 1e9,
                          "fabric_GBps_all_operands": ks["traffic_GBps"]}
+    # fabric traffic of one full row pass (the launches' averages include passes with fewer or no rows) against the
+    # bytes the pass must move at least, recorded with the rocprof counters
+    for name, k in kernels.items():
+        full = recorded_traffic(name, cfg.name, fused, key="traffic_full_pass")
+        alg = recorded_traffic(name, cfg.name, fused, key="algorithmic_full_pass")
+        if full and alg:
+            k["traffic_full_pass"] = full
+            k["algorithmic_full_pass"] = alg
+            k["traffic_ratio_full_pass"] = full / alg
     # The roofline kernel: the one with the most time per step among those whose FLOP are algorithmic work of the
     # metric (the forward logits GEMM and the two gradient GEMMs); gemm_dz recomputes the logits (executed, not
     # algorithmic work) and is never credited. The whole path's algorithmic and executed fractions sit beside it.
@@ -440,7 +493,8 @@ def main() -> int:
                    "parallelism": "single GPU"},
         "mfma_frac_algorithmic": alg_flop / step_s / peak,
         "mfma_frac_executed": exe_flop / step_s / peak,
-        "phase_ms": ({"two_call_forward": fwd_ms, "two_call_backward": bwd_ms, "two_call_step": fwd_ms + bwd_ms}
+        "phase_ms": ({"two_call_forward": fwd_ms, "two_call_backward": bwd_ms, "two_call_step": fwd_ms + bwd_ms,
+                      "bound_step": bound_ms}
                      if fused and reps else {} if fused else {"forward": fwd_ms, "backward": bwd_ms}),
         "kernels": kernels,
         "weight_stream": weight_stream,

@@ -41,6 +41,11 @@
  *                                                     backward in one call, the logits computed once per
  *                                                     row pass); over a tree's pair rows (tree_head_output,
  *                                                     prefix_tree.py:416-421): octo_head_step_grpo_pairs
+ *   octopus/rl/actor.py:166-171, 343-347 unchanged (bind_head's own pre-hook binds the micro-batch's GRPO
+ *     inputs; AReaL's loss.backward() reaches the head's backward) -> octo_head_step_grpo in the forward,
+ *                                                     and in the backward octo_scale_add of its gradients
+ *                                                     plus octo_head_bwd of the rest of dL/dlogprob (its
+ *                                                     kernels end at once when that rest is negligible)
  */
 #ifndef OCTO_HEAD_H
 #define OCTO_HEAD_H
@@ -78,6 +83,7 @@ extern "C" {
                                  /* (m2 + l2S) ln 2; the backward then repeats the forward's rounding    */
                                  /* (exact dz row sums when the logits sit far from zero)                */
 #define OCTO_WS_STEP        128  /* octo_head_workspace_bytes / octo_head_bwd_plan: for octo_head_step_grpo */
+#define OCTO_WS_NO_GRADH    256  /* octo_head_workspace_bytes / octo_head_bwd_plan: without grad_h        */
 #define OCTO_PAIRS_NONE_AS_COUNT 1 /* octo_label_pairs: positions without a pair get the pair count  */
 
 const char *octo_version(void);
@@ -93,18 +99,19 @@ int octo_timing_enable(int on);
 int octo_timing_read(const char *kernel, int *launches, double *total_ms);
 
 /* Workspace bytes for octo_head_fwd (flags without OCTO_WS_BACKWARD) or octo_head_bwd
- * (OCTO_WS_BACKWARD [| OCTO_WS_NO_GRADW]) at n_max rows, width d, vocabulary V. With idx, a hidden matrix of
+ * (OCTO_WS_BACKWARD [| OCTO_WS_NO_GRADW | OCTO_WS_NO_GRADH]) at n_max rows, width d, vocabulary V. With idx, a hidden matrix of
  * 2 GiB or more (h_rows * ldh * element bytes >= 2^31) is first gathered into the workspace (the GEMMs address
  * mapped rows with 32-bit offsets): add OCTO_WS_GATHER for those calls.
  * Backward: the size of its plan at a 2 GiB staging budget (see octo_head_bwd); a smaller workspace is accepted
- * down to the plan at a 1 MiB budget, a larger one may run fewer chunks. OCTO_WS_STEP [| OCTO_WS_NO_GRADW]: the
+ * down to the plan at a 1 MiB budget, a larger one may run fewer chunks. OCTO_WS_STEP [| OCTO_WS_NO_GRADW |
+ * OCTO_WS_NO_GRADH]: the
  * same for octo_head_step_grpo and octo_head_step_grpo_pairs (n_max = the pair rows), whose plan has row passes
  * only; for fp32 operands the larger of the forward's and the backward's. */
 int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes);
 
 /* The chunking octo_head_bwd runs in ws_bytes of workspace (a planning aid; no counterpart in the reference):
  * plan[0] rows per pass, plan[1] passes, plan[2] vocabulary columns per chunk, plan[3] chunks. flags as for
- * octo_head_workspace_bytes (OCTO_WS_NO_GRADW, OCTO_WS_GATHER); grad_h is assumed asked for. With OCTO_WS_STEP, the
+ * octo_head_workspace_bytes (OCTO_WS_NO_GRADW, OCTO_WS_NO_GRADH, OCTO_WS_GATHER). With OCTO_WS_STEP, the
  * fused step's plan: {rows per pass, passes, V rounded up to 256, 1}. OCTO_EWORKSPACE when no plan fits. */
 int octo_head_bwd_plan(int64_t n_max, int d, int V, int w_dtype, int flags, size_t ws_bytes, int64_t plan[4]);
 
@@ -213,6 +220,14 @@ int octo_rows_scatter(const void *src, int64_t ld_src, int src_dtype, const int6
                       const int32_t *count, int64_t n_max, int d,
                       void *dst, int64_t ld_dst, int dst_dtype, int accumulate, void *stream);
 
+/* y[i] = c y[i] + x[i] for i < n, with c = *c read on the device, formed in fp32 and rounded once to dtype (BF16, F16
+ * or F32); while skip_x is given and *skip_x != 0, x counts as zero and is not read (c = 1 then leaves y as it is at
+ * once). y and x 16-byte aligned. No counterpart in the reference, whose autograd sums the chunks' gradients: the
+ * backward of the bound GRPO step (octopus_amd/head_op.py) uses it to scale the gradients its forward computed by the
+ * incoming gradient's multiple of the head's own GRPO weight and add the backward of the rest. */
+int octo_scale_add(void *y, const void *x, int dtype, int64_t n, const float *c, const int32_t *skip_x,
+                   void *stream);
+
 /* out[r] = src[idx[r] * ld_src] (fp32) for r < *count, 0 for count <= r < n_max. */
 int octo_gather_f32(const float *src, int64_t ld_src, const int64_t *idx, const int32_t *count,
                     int64_t n_max, float *out, void *stream);
@@ -268,7 +283,8 @@ int octo_head_fwd_grpo(const void *h, int64_t h_rows, int64_t ldh, int h_dtype,
  * grad_W run as in octo_head_bwd (both in one launch per pass). The logits are computed once instead of twice; dz
  * differs from octo_head_bwd's by the rounding of the stored value (bf16: 2^-9 relative, in place of the backward's
  * rounding of dz; f16: 2^-11 relative, besides it), and bf16 grad_W by the rounding of the scaled h^T as well.
- * Workspace: octo_head_workspace_bytes with OCTO_WS_STEP [| OCTO_WS_NO_GRADW | OCTO_WS_GATHER], the plan at a
+ * Workspace: octo_head_workspace_bytes with OCTO_WS_STEP [| OCTO_WS_NO_GRADW | OCTO_WS_NO_GRADH | OCTO_WS_GATHER],
+ * matching the gradients asked for, the plan at a
  * 2 GiB staging budget ([rows, V] of one pass); outside the staging are the pass's statistics per vocabulary tile,
  * h^T of a pass, fp32 grad_w partials [V, d] over several passes, and once per call W widened to bf16 (fp8 weights)
  * and W^T (16-bit weights with V % 64 or d % 256 not 0; and, for speed, when grad_h is the only gradient and

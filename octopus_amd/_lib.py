@@ -20,6 +20,7 @@ OK, EINVAL, EWORKSPACE, EUNSUPPORTED, EHIP = 0, -1, -2, -3, -4
 BF16, F16, F32, FP8E4M3 = 0, 1, 2, 3
 ROWS_VIA_IDX, OUT_SCATTER, GRADW_ACCUMULATE, WS_BACKWARD, WS_NO_GRADW, WS_GATHER, LSE_PAIR = 1, 2, 4, 8, 16, 32, 64
 WS_STEP = 128
+WS_NO_GRADH = 256
 PAIRS_NONE_AS_COUNT = 1
 
 _p = ctypes.c_void_p
@@ -65,6 +66,7 @@ SIGNATURES = {
     "octo_pairs_grad": [_p, _i64, _i32, _p, _i64, _p, _p],
     "octo_rows_scatter": [_p, _i64, _i32, _p, _p, _i64, _i32, _p, _i64, _i32, _i32, _p],
     "octo_gather_f32": [_p, _i64, _p, _p, _i64, _p, _p],
+    "octo_scale_add": [_p, _p, _i32, _i64, _p, _p, _p],
     "octo_label_pairs_workspace_bytes": [_i64, _i64, ctypes.POINTER(_sz)],
     "octo_label_pairs": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i32, _p, _sz, _p],
     "octo_quantise_fp8_rows": [_p, _i64, _i32, _i64, _i32, _p, _i64, _p, _p],

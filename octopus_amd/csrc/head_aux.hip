@@ -354,12 +354,18 @@ int launch_row_offsets(const RowOffArgs &a, hipStream_t st) {
   return OCTO_OK;
 }
 
-// After a pass's merge: every workgroup sets the dz scales of a strided slice of the pass's rows, then takes the
-// flagged rows in turn (none in the usual case, so each workgroup then reads the count and ends). A flagged row is
-// rescaled in place to its new offset (the merge set xuse = m2), 16 bytes per thread and step, by its half tiles'
-// factors (8 columns never straddle a 128-column half tile): the stored value of half tile h is e exp2(min(m_h - xoff,
-// kExClamp)) with e = exp2(c t - m_h), and exp2(c t - m2) = that x exp2(m_h - m2 - min(m_h - xoff, kExClamp)).
-constexpr int kExFixBlocks = 64;
+// After a pass's merge: the workgroups set the dz scales of a strided slice of the pass's rows, then share the
+// rescale of the flagged rows (none in the usual case: each workgroup then reads the count and ends). The rescale is
+// cut into work items of one flagged row x kExFixCols columns, dealt to the workgroups in turn, so that at a low
+// temperature, where most rows are flagged, it streams at the HBM rate: each thread issues its four 16-byte loads
+// before the first store. A flagged row is rescaled in place to its new offset (the merge set xuse = m2) by its half
+// tiles' factors (8 columns never straddle a 128-column half tile): the stored value of half tile h is
+// e exp2(min(m_h - xoff, kExClamp)) with e = exp2(c t - m_h), and exp2(c t - m2) = that x exp2(m_h - m2 - min(m_h -
+// xoff, kExClamp)). Same box, 24,576 of 32,768 rows at d 2560, V 151,936, T 0.012 (almost every row flagged): the
+// 64-workgroup form that took one whole row per workgroup at a time ran 17.5 ms per step.
+constexpr int kExFixBlocks = 2048;        // 8 per CU
+constexpr int kExFixLoads = 4;            // 16-byte chunks per thread and work item
+constexpr int kExFixCols = 256 * 8 * kExFixLoads;
 __global__ __launch_bounds__(256) void ex_fix_kernel(ExFixArgs a) {
   const int64_t cnt = a.count ? min((int64_t)(*a.count), a.n_max) : a.n_max;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < a.rows; i += (int64_t)gridDim.x * 256) {
@@ -372,23 +378,34 @@ __global__ __launch_bounds__(256) void ex_fix_kernel(ExFixArgs a) {
     }
     a.scale[i] = s;
   }
-  const int nf = *a.flag_cnt;
-  for (int k = blockIdx.x; k < nf; k += gridDim.x) {
-    const int64_t i = a.flag_rows[k], r = a.r0 + i;
+  const int64_t nf = *a.flag_cnt;
+  const int64_t chunks = (a.V_pad + kExFixCols - 1) / kExFixCols;
+  for (int64_t k = blockIdx.x; k < nf * chunks; k += gridDim.x) {
+    const int64_t f = k / chunks, cbase = (k - f * chunks) * kExFixCols;
+    const int64_t i = a.flag_rows[f], r = a.r0 + i;
     const float xo = a.xoff[r], xn = a.xuse[i];
     float m2, l2s;
     row_state(a.lse, a.lse_pair, r, m2, l2s);
     const int64_t y = a.labels[a.label_idx ? a.label_idx[r] : r];
     const f32x4 *pr = a.part + i * a.mtiles;
     char *row = (char *)a.ex + i * a.ldx * 2;
-    for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < a.V_pad; c0 += 256 * 8) {
+    i32x4 v[kExFixLoads];
+#pragma unroll
+    for (int u = 0; u < kExFixLoads; ++u) {
+      const int64_t c0 = cbase + (int64_t)(u * 256 + threadIdx.x) * 8;
+      if (c0 < a.V_pad) v[u] = *(const i32x4 *)(row + c0 * 2);
+    }
+#pragma unroll
+    for (int u = 0; u < kExFixLoads; ++u) {
+      const int64_t c0 = cbase + (int64_t)(u * 256 + threadIdx.x) * 8;
+      if (c0 >= a.V_pad) continue;
       const f32x4 q = pr[c0 >> 8];
       const float mh = (c0 & 128) ? q[3] : q[0];  // -inf: no column of the half lies below V (stored zeros)
-      const float f = mh == -INFINITY ? 0.f : fexp2(mh - xn - fminf(mh - xo, kExClamp));
+      const float fac = mh == -INFINITY ? 0.f : fexp2(mh - xn - fminf(mh - xo, kExClamp));
       float x[8];
-      unpack8(*(const i32x4 *)(row + c0 * 2), false, x);
+      unpack8(v[u], false, x);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] *= f;
+      for (int e = 0; e < 8; ++e) x[e] *= fac;
       if (y >= c0 && y < c0 + 8 && y < a.V) x[y - c0] = -a.hit[i] * fexp2(m2 - xn + l2s);
       *(i32x4 *)(row + c0 * 2) = pack8(x, false);
     }
@@ -402,6 +419,43 @@ int launch_ex_fix(const ExFixArgs &a, hipStream_t st) {
   hipLaunchKernelGGL(ex_fix_kernel, dim3(kExFixBlocks), dim3(256), 0, st, a);
   OCTO_CHECK_LAUNCH("ex_fix");
   return OCTO_OK;
+}
+
+// ---- y = c y + x over a vector (the bound GRPO step's backward) ------------------------------------------------------
+// c is read from device memory, and so is `skip_x` (when given): while it is non-zero x counts as zero and is not read.
+// The product and the sum are formed in fp32 and rounded once to the vector's type. With c = 1 and x skipped, y is
+// already the result and every workgroup ends at once. 16 bytes per thread and step.
+__global__ __launch_bounds__(256) void scale_add_kernel(void *y, const void *x, int dtype, int64_t n, const float *c,
+                                                        const int32_t *skip_x) {
+  const float s = *c;
+  const bool add = !(skip_x && *skip_x);
+  if (s == 1.f && !add) return;
+  const int per = dtype == OCTO_F32 ? 4 : 8;  // elements per 16-byte chunk
+  const int64_t chunks = n / per;
+  for (int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x; k < chunks; k += (int64_t)gridDim.x * 256) {
+    i32x4 *yp = (i32x4 *)((char *)y + k * 16);
+    const i32x4 xv = add ? *(const i32x4 *)((const char *)x + k * 16) : i32x4{0, 0, 0, 0};
+    if (dtype == OCTO_F32) {
+      f32x4 a = __builtin_bit_cast(f32x4, *yp);
+      const f32x4 b = __builtin_bit_cast(f32x4, xv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[e] = __builtin_fmaf(s, a[e], b[e]);
+      *yp = __builtin_bit_cast(i32x4, a);
+    } else {
+      const bool f16 = dtype == OCTO_F16;
+      float a[8], b[8];
+      unpack8(*yp, f16, a);
+      unpack8(xv, f16, b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = __builtin_fmaf(s, a[e], b[e]);
+      *yp = pack8(a, f16);
+    }
+  }
+  if (blockIdx.x == 0 && threadIdx.x < n - chunks * per) {  // the last n % per elements
+    const int64_t i = chunks * per + threadIdx.x;
+    const float b = add ? load_as_f32(x, dtype, i) : 0.f;
+    store_from_f32(y, dtype, i, __builtin_fmaf(s, load_as_f32(y, dtype, i), b));
+  }
 }
 
 // ---- the fused step's GRPO tail over prefix-tree pair rows ----------------------------------------------
@@ -1000,6 +1054,21 @@ int octo_rows_scatter(const void *src, int64_t ld_src, int src_dtype, const int6
   hipLaunchKernelGGL(rows_scatter_kernel, dim3((unsigned)n_max), dim3(256), 0, (hipStream_t)stream, src, ld_src,
                      src_dtype, idx, count, n_max, d, dst, ld_dst, dst_dtype, accumulate);
   OCTO_CHECK_LAUNCH("rows_scatter");
+  return OCTO_OK;
+}
+
+int octo_scale_add(void *y, const void *x, int dtype, int64_t n, const float *c, const int32_t *skip_x,
+                   void *stream) {
+  OCTO_CHECK_ARG(n >= 0, "scale_add: n < 0");
+  OCTO_CHECK_ARG(dtype == OCTO_BF16 || dtype == OCTO_F16 || dtype == OCTO_F32, "scale_add: dtype %d", dtype);
+  if (n == 0) return OCTO_OK;
+  OCTO_CHECK_ARG(y && x && c, "scale_add: null pointer");
+  OCTO_CHECK_ARG(((uintptr_t)y) % 16 == 0 && ((uintptr_t)x) % 16 == 0, "scale_add: vectors must be 16-byte aligned");
+  const int64_t chunks = n / (dtype == OCTO_F32 ? 4 : 8);
+  const int64_t blocks = cdiv(chunks, 256);
+  hipLaunchKernelGGL(scale_add_kernel, dim3((unsigned)(blocks < 1 ? 1 : (blocks > 2048 ? 2048 : blocks))), dim3(256),
+                     0, (hipStream_t)stream, y, x, dtype, n, c, skip_x);
+  OCTO_CHECK_LAUNCH("scale_add");
   return OCTO_OK;
 }
 

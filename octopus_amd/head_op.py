@@ -59,6 +59,16 @@ def _index(t: Optional[Tensor]) -> Optional[Tensor]:
     return t.to(torch.int64).contiguous()
 
 
+def _zeros(like: Tensor) -> Tensor:
+    """Zeros of like's shape, dtype and device in the contiguous (row-major) layout the library writes, whatever
+    like's own strides."""
+    return torch.zeros(like.shape, dtype=like.dtype, device=like.device)
+
+
+def _empty(like: Tensor) -> Tensor:
+    return torch.empty(like.shape, dtype=like.dtype, device=like.device)
+
+
 def _workspace(nbytes: int, like: Tensor) -> Tensor:
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=like.device)
 
@@ -162,15 +172,16 @@ def head_bwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
     labels, idx = _index(labels), _index(idx)
     n_max = idx.numel() if idx is not None else rows2.shape[0]
     V, d = weight2.shape
-    grad_rows = torch.zeros_like(rows) if need_rows else rows.new_empty(0)
+    grad_rows = _zeros(rows) if need_rows else rows.new_empty(0)
     grad_w = weight.new_empty(0)
     if n_max == 0 or not (need_rows or need_weight):
         if need_weight:
-            grad_w = torch.zeros_like(weight)
+            grad_w = _zeros(weight)
         return grad_rows, grad_w
     w_code = _dtype_code(weight2)
     flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | _lib.LSE_PAIR
-    ws_flags = _lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, idx)
+    ws_flags = (_lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW) | (0 if need_rows else _lib.WS_NO_GRADH)
+                | _gather_flag(rows2, idx))
     nbytes = _lib.workspace_bytes(n_max, d, V, w_code, ws_flags)
     if BWD_WORKSPACE_BYTES is not None:
         nbytes = int(BWD_WORKSPACE_BYTES)
@@ -197,8 +208,8 @@ def head_bwd(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labels: Te
 @head_bwd.register_fake
 def _(rows, weight, w_scale, labels, idx, count, lse, g, inv_T, pre, post, use_tanh, labels_via_idx,
       need_rows, need_weight):
-    return (torch.empty_like(rows) if need_rows else rows.new_empty(0),
-            torch.empty_like(weight) if need_weight else weight.new_empty(0))
+    return (_empty(rows) if need_rows else rows.new_empty(0),
+            _empty(weight) if need_weight else weight.new_empty(0))
 
 
 # Bytes of workspace head_step_grpo gives the library (None: octo_head_workspace_bytes with OCTO_WS_STEP, the plan at
@@ -226,8 +237,8 @@ def head_step_grpo(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labe
     lse = torch.zeros(n_max, 2, dtype=torch.float32, device=dev)
     g = torch.zeros(n_max, dtype=torch.float32, device=dev)
     loss = torch.zeros((), dtype=torch.float32, device=dev)
-    grad_rows = torch.zeros_like(rows) if need_rows else rows.new_empty(0)
-    grad_w = (torch.zeros_like(weight) if n_max == 0 else torch.empty_like(weight)) if need_weight \
+    grad_rows = _zeros(rows) if need_rows else rows.new_empty(0)
+    grad_w = (_zeros(weight) if n_max == 0 else _empty(weight)) if need_weight \
         else weight.new_empty(0)
     if n_max == 0:
         return out, lse, g, loss, grad_rows, grad_w
@@ -237,7 +248,8 @@ def head_step_grpo(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor], labe
                          _p(g), _p(loss))
     w_code = _dtype_code(weight2)
     if need_rows or need_weight:
-        ws_flags = _lib.WS_STEP | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, idx)
+        ws_flags = (_lib.WS_STEP | (0 if need_weight else _lib.WS_NO_GRADW) | (0 if need_rows else _lib.WS_NO_GRADH)
+                    | _gather_flag(rows2, idx))
     else:  # no gradient: the library runs the forward with its GRPO tail, in the forward's workspace
         ws_flags = _gather_flag(rows2, idx)
     nbytes = _lib.workspace_bytes(n_max, d, V, w_code, ws_flags)
@@ -267,8 +279,8 @@ def _(rows, weight, w_scale, labels, idx, count, inv_T, pre, post, use_tanh, lab
     out = rows.new_empty(rows.shape[0] if scatter else n_max, 2, dtype=torch.float32)
     return (out, rows.new_empty(n_max, 2, dtype=torch.float32), rows.new_empty(n_max, dtype=torch.float32),
             rows.new_empty((), dtype=torch.float32),
-            torch.empty_like(rows) if need_rows else rows.new_empty(0),
-            torch.empty_like(weight) if need_weight else weight.new_empty(0))
+            _empty(rows) if need_rows else rows.new_empty(0),
+            _empty(weight) if need_weight else weight.new_empty(0))
 
 
 @torch.library.custom_op("octohead::head_step_grpo_pairs", mutates_args=(), device_types="cuda")
@@ -291,15 +303,16 @@ def head_step_grpo_pairs(rows: Tensor, weight: Tensor, w_scale: Optional[Tensor]
     lse = torch.zeros(n_pairs, 2, dtype=torch.float32, device=dev)
     g = torch.zeros(n_pairs, dtype=torch.float32, device=dev)
     loss = torch.zeros((), dtype=torch.float32, device=dev)
-    grad_rows = torch.zeros_like(rows) if need_rows else rows.new_empty(0)
-    grad_w = (torch.zeros_like(weight) if n_pairs == 0 else torch.empty_like(weight)) if need_weight \
+    grad_rows = _zeros(rows) if need_rows else rows.new_empty(0)
+    grad_w = (_zeros(weight) if n_pairs == 0 else _empty(weight)) if need_weight \
         else weight.new_empty(0)
     f = lambda t: None if t is None else t.float().contiguous().reshape(-1)  # noqa: E731
     prox_, old_, adv_, mask_ = f(prox), f(old), f(adv), f(mask)
     tail = _lib.GrpoTail(_p(prox_), _p(old_), _p(adv_), _p(mask_), adv_.numel(), eps_lo, eps_hi, reject_upper,
                          _p(g), _p(loss))
     w_code = _dtype_code(weight2)
-    ws_flags = _lib.WS_STEP | (0 if need_weight else _lib.WS_NO_GRADW) | _gather_flag(rows2, pair_pos)
+    ws_flags = (_lib.WS_STEP | (0 if need_weight else _lib.WS_NO_GRADW) | (0 if need_rows else _lib.WS_NO_GRADH)
+                | _gather_flag(rows2, pair_pos))
     nbytes = _lib.workspace_bytes(n_pairs, d, V, w_code, ws_flags)
     if STEP_WORKSPACE_BYTES is not None:
         nbytes = int(STEP_WORKSPACE_BYTES)
@@ -324,8 +337,8 @@ def _(rows, weight, w_scale, pair_label, pair_pos, pair_count, flat_pair, inv_T,
     return (rows.new_empty(flat_pair.shape[0], 2, dtype=torch.float32),
             rows.new_empty(n_pairs, 2, dtype=torch.float32), rows.new_empty(n_pairs, dtype=torch.float32),
             rows.new_empty((), dtype=torch.float32),
-            torch.empty_like(rows) if need_rows else rows.new_empty(0),
-            torch.empty_like(weight) if need_weight else weight.new_empty(0))
+            _empty(rows) if need_rows else rows.new_empty(0),
+            _empty(weight) if need_weight else weight.new_empty(0))
 
 
 def _step_setup(ctx, inputs, output):
@@ -342,8 +355,10 @@ def _step_backward(ctx, _gout, _glse, _gg, gloss, _ggr, _ggw):
     the incoming gradient of the loss (1 for loss.backward())."""
     grad_rows, grad_w = ctx.grads
     need_rows, need_weight = ctx.need
-    gr = grad_rows * gloss.to(grad_rows.dtype) if need_rows and ctx.needs_input_grad[0] else None
-    gw = grad_w * gloss.to(grad_w.dtype) if need_weight and ctx.needs_input_grad[1] else None
+    # the product in fp32, rounded once to the gradient's dtype (a scale such as 1/3 is not exact in bf16)
+    scale = gloss.float()
+    gr = (grad_rows.float() * scale).to(grad_rows.dtype) if need_rows and ctx.needs_input_grad[0] else None
+    gw = (grad_w.float() * scale).to(grad_w.dtype) if need_weight and ctx.needs_input_grad[1] else None
     return (gr, gw) + (None,) * (ctx.n_inputs - 2)
 
 
@@ -439,6 +454,132 @@ def fused_grpo_tree_head(hidden: Tensor, weight: Tensor, meta, temperature: floa
         1.0 / float(temperature), float(post.pre), float(post.post), bool(post.tanh), prox, old, adv, mask,
         float(eps_lo), float(eps_hi), float(reject_upper), need_rows, need_weight)
     return loss, out.detach().unsqueeze(0)
+
+
+# ---- the bound GRPO step: the fused step behind the head's ordinary columns ---------------------------------
+
+# The part of the incoming dL/dlogprob that is not a multiple of the bound step's own GRPO weight, relative (L2) to
+# the whole, at or below which the backward only scales the gradients its forward computed. The gradients are linear
+# in dL/dlogprob, so leaving that part out changes them by about the same relative amount: 1e-5, far below bf16's
+# 2^-9 rounding of dz. Two fp32 evaluations of one objective in a different operation order differ by a few ulp
+# (about 1e-7 relative).
+SPEC_TOL = 1e-5
+
+
+class GrpoInputs(NamedTuple):
+    """The micro-batch's GRPO inputs per flat position (the head's rows): advantages, behaviour logprobs (`old`),
+    proximal logprobs (`prox`; None: the head's own logprobs, reuse_train_logp) and the loss mask, with AReaL's
+    constants (grpo.yaml:103-118)."""
+    adv: Tensor
+    old: Optional[Tensor]
+    prox: Optional[Tensor]
+    mask: Tensor
+    eps_lo: float = 0.2
+    eps_hi: float = 0.28
+    reject_upper: float = 5.0
+
+
+def _spec_split(g_act: Tensor, g_head: Tensor, count: Tensor):
+    """(c, rest, count_rest, skip): c g_head is the least-squares multiple of the head's own GRPO weight in the
+    incoming dL/dlogprob g_act (both per compact row), rest = g_act - c g_head, count_rest = 0 where rest is
+    negligible (SPEC_TOL), else count, so that the residual backward's kernels end at once; skip [1] int32 = 1 then.
+    Everything stays on the device."""
+    g_act, g_head = g_act.float().reshape(-1), g_head.float().reshape(-1)
+    den = torch.dot(g_head, g_head)
+    c = torch.where(den > 0, torch.dot(g_act, g_head) / den, torch.zeros_like(den)).reshape(1)
+    rest = g_act - c * g_head
+    small = torch.linalg.vector_norm(rest) <= SPEC_TOL * torch.linalg.vector_norm(g_act)
+    count_rest = torch.where(small, torch.zeros_like(count), count).to(torch.int32)
+    return c.contiguous(), rest.contiguous(), count_rest.contiguous(), small.to(torch.int32).reshape(1).contiguous()
+
+
+def _scale_add(held: Tensor, rest: Tensor, c: Tensor, skip: Tensor) -> Tensor:
+    """held = c held + rest in place (rest not read while skip is set); returns held."""
+    if held.numel():
+        rest = rest.contiguous()
+        _lib.call("octo_scale_add", _p(held), _p(rest), _dtype_code(held), held.numel(), _p(c), _p(skip),
+                  _stream(held))
+    return held
+
+
+class _GrpoBound(torch.autograd.Function):
+    """The head's (logprob, entropy) columns from octo_head_step_grpo (or _pairs), which also computes the gradients
+    of the GRPO objective on them; the backward fits the incoming dL/dlogprob as c times the step's own weight g
+    (_spec_split), scales the held gradients by c and adds octo_head_bwd's gradients of the rest, whose kernels end at
+    once when the rest is negligible. A loss that is the objective (times any constant) costs the forward's one pass
+    over the logits; any other loss on the logprob column still gets its exact gradients, at the cost of the
+    recompute backward. The entropy column carries no gradient (lm_head.py:111)."""
+
+    @staticmethod
+    def forward(ctx, rows, weight, w_scale, labels, idx, count, flat_pair, inv_T, post, grpo):
+        need_rows, need_weight = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        pre, pst, tanh = float(post.pre), float(post.post), bool(post.tanh)
+        if flat_pair is None:  # compact rows: row r is rows[idx[r]] (or r), out scattered to the rows
+            out, lse, g, _loss, grad_rows, grad_w = head_step_grpo(
+                rows, weight, w_scale, labels, idx, count, inv_T, pre, pst, tanh, idx is not None, idx is not None,
+                grpo.prox, grpo.old, grpo.adv, grpo.mask, grpo.eps_lo, grpo.eps_hi, grpo.reject_upper, need_rows,
+                need_weight)
+        else:  # tree pair rows: row r is rows[idx[r]] with label labels[r]; out per flat token
+            out, lse, g, _loss, grad_rows, grad_w = head_step_grpo_pairs(
+                rows, weight, w_scale, labels, idx, count, flat_pair, inv_T, pre, pst, tanh, grpo.prox, grpo.old,
+                grpo.adv, grpo.mask, grpo.eps_lo, grpo.eps_hi, grpo.reject_upper, need_rows, need_weight)
+        # the gradients are held on ctx, not saved: an activation-offload pack hook would copy [V, d] to the host
+        ctx.held = (grad_rows.detach(), grad_w.detach())
+        ctx.weight = weight
+        ctx.save_for_backward(rows, w_scale, labels, idx, count, flat_pair, lse, g)
+        ctx.params = (inv_T, pre, pst, tanh)
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        rows, w_scale, labels, idx, count, flat_pair, lse, g_head = ctx.saved_tensors
+        inv_T, pre, pst, tanh = ctx.params
+        grad_rows, grad_w = ctx.held
+        ctx.held = None
+        need_rows, need_weight = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        n = g_head.numel()
+        gout = gout.float()
+        if flat_pair is not None:  # per pair row: the sum over its flat tokens
+            g_act = pairs_grad(gout, flat_pair, n)[:, 0].contiguous()
+        elif idx is not None:  # per compact row: the output gradient at its row idx[r] (0 past the count)
+            col = gout[:, 0].contiguous()
+            g_act = torch.empty(n, dtype=torch.float32, device=gout.device)
+            _lib.call("octo_gather_f32", _p(col), 1, _p(idx), _p(count), n, _p(g_act), _stream(gout))
+        else:
+            g_act = gout[:, 0].contiguous()
+        if count is None:
+            count = torch.full((1,), n, dtype=torch.int32, device=gout.device)
+        c, rest, count_rest, skip = _spec_split(g_act, g_head, count[:1])
+        gr_rest, gw_rest = head_bwd(rows, ctx.weight, w_scale, labels, idx, count_rest, lse, rest, inv_T, pre, pst,
+                                    tanh, idx is not None and flat_pair is None, need_rows, need_weight)
+        gr = _scale_add(grad_rows, gr_rest, c, skip) if need_rows else None
+        gw = _scale_add(grad_w, gw_rest, c, skip) if need_weight else None
+        return gr, gw, None, None, None, None, None, None, None, None
+
+
+def grpo_bound_head(rows: Tensor, weight: Tensor, labels: Tensor, temperature: float, grpo: GrpoInputs, *,
+                    post: Post = Post(), idx: Optional[Tensor] = None, count: Optional[Tensor] = None,
+                    w_scale: Optional[Tensor] = None) -> Tensor:
+    """fused_head's columns (with idx: [rows, 2], each compact row r at idx[r], 0 elsewhere; labels per row of
+    `rows`), computed by the fused GRPO step on grpo's per-row inputs: a loss that is the GRPO objective on the
+    logprob column, times any constant, gets its gradients from that one call; any other loss gets them from the
+    recompute backward of the difference (_GrpoBound)."""
+    if temperature <= 0:
+        raise ValueError("temperature must be positive")
+    return _GrpoBound.apply(rows, weight, w_scale, labels, idx, count, None, 1.0 / float(temperature), post, grpo)
+
+
+def grpo_bound_tree_head(hidden: Tensor, weight: Tensor, meta, temperature: float, grpo: GrpoInputs, *,
+                         post: Post = Post(), w_scale: Optional[Tensor] = None) -> Tensor:
+    """tree_head_output's [1, T_flat, 2] columns over a prefix tree's pair rows (meta: a TreeMeta) from the fused GRPO
+    step over those rows (octo_head_step_grpo_pairs), grpo's inputs per flat token; the backward as grpo_bound_head's,
+    with each pair row's dL/dlogprob summed over its flat tokens."""
+    if temperature <= 0:
+        raise ValueError("temperature must be positive")
+    rows = hidden[0] if hidden.dim() == 3 else hidden
+    out = _GrpoBound.apply(rows, weight, w_scale, meta.pair_label, meta.pair_pos, meta.pair_count, meta.flat_pair,
+                           1.0 / float(temperature), post, grpo)
+    return out.unsqueeze(0)
 
 
 # ---- _head_columns over materialised logits ------------------------------------------------------

@@ -268,23 +268,90 @@ def _pair_rows(self):
     return rows_fn
 
 
+# AReaL's micro-batch keys of the GRPO objective's per-token inputs, which the model's forward receives beside
+# input_ids and loss_mask (actor.py:80-91 reads loss_mask there): the advantages (actor.py:293-303), the behaviour
+# logprobs (spool.py:29-30) and the proximal logprobs, absent under prox_logp_method reuse_train_logp
+# (grpo.yaml:103-118, whose constants GrpoInputs carries). Under ppo_update all of them are rolled onto the position
+# that scores each token, as the loss mask is (actor.py:80-91).
+GRPO_KEYS = ("advantages", "logprobs", "loss_mask")
+
+
+def grpo_inputs(kwargs: dict):
+    """The GRPO inputs of a micro-batch's model kwargs (head_op.GrpoInputs, flat per position), or None when any of
+    GRPO_KEYS is missing (compute_logp's batch, or a forward outside training)."""
+    if any(kwargs.get(k) is None for k in GRPO_KEYS):
+        return None
+    from octopus_amd.head_op import GrpoInputs
+    prox = kwargs.get("prox_logp")
+    return GrpoInputs(adv=kwargs["advantages"].reshape(-1), old=kwargs["logprobs"].reshape(-1),
+                      prox=None if prox is None else prox.reshape(-1), mask=kwargs["loss_mask"].reshape(-1))
+
+
+def _bound_grpo(self, hidden: torch.Tensor, n_flat: int):
+    """The micro-batch's GRPO inputs when this call takes the fused GRPO step: HIP tensors, a gradient asked for,
+    inputs bound for n_flat positions and the step switched on (head.octopus_grpo_step)."""
+    grpo = getattr(self, "octopus_grpo", None)
+    if grpo is None or not getattr(self, "octopus_grpo_step", True) or not hidden.is_cuda:
+        return None
+    if not torch.is_grad_enabled() or not (hidden.requires_grad or self.weight.requires_grad):
+        return None
+    return grpo if grpo.adv.numel() == n_flat else None
+
+
 def _chunked_head_forward(self, hidden: torch.Tensor) -> torch.Tensor:
     """[1, T, H] hidden -> [1, T_flat, 2]. The model's own post-head ops then leave the output as it is
-    (they ran inside the head). A tree micro-batch (self.octopus_tree) scores its label pairs."""
-    if self.octopus_tree is not None:
-        out = tree_head_output(_pair_rows(self), hidden, self.octopus_tree)
+    (they ran inside the head). A tree micro-batch (self.octopus_tree) scores its label pairs.
+
+    With the micro-batch's GRPO inputs bound (bind_head's pre-hook) and a gradient asked for, HIP tensors take the
+    fused GRPO step (head_op.grpo_bound_head / grpo_bound_tree_head): the same columns, whose backward only scales the
+    gradients the step computed when the trainer's loss is the GRPO objective, and adds the recompute backward of any
+    other part of dL/dlogprob."""
+    tree = self.octopus_tree
+    if tree is not None:
+        grpo = _bound_grpo(self, hidden, tree.flat_pair.numel())
+        if grpo is not None:
+            from octopus_amd.head_op import grpo_bound_tree_head
+            out = grpo_bound_tree_head(hidden, self.weight, tree, self.octopus_temperature, grpo,
+                                       post=_fused_post(self.octopus_post), w_scale=getattr(self, "octopus_w_scale",
+                                                                                           None))
+        else:
+            out = tree_head_output(_pair_rows(self), hidden, tree)
     else:
-        out = _scored_rows(self, hidden.reshape(-1, hidden.shape[-1]), self.octopus_labels).reshape(
-            *hidden.shape[:-1], 2)
+        rows = hidden.reshape(-1, hidden.shape[-1])
+        grpo = _bound_grpo(self, hidden, rows.shape[0])
+        if grpo is not None:
+            from octopus_amd.head_op import compact_rows, grpo_bound_head
+            kw = {}
+            if self.octopus_scored is not None:
+                kw["idx"], kw["count"] = compact_rows(self.octopus_scored)
+            out = grpo_bound_head(rows, self.weight, self.octopus_labels, self.octopus_temperature, grpo,
+                                  post=_fused_post(self.octopus_post), w_scale=getattr(self, "octopus_w_scale", None),
+                                  **kw)
+        else:
+            out = _scored_rows(self, rows, self.octopus_labels)
+        out = out.reshape(*hidden.shape[:-1], 2)
     return _skipping(out, len(self.octopus_post))
 
 
 def bind_head(model, temperature: float):
     """Install the chunked head as the model's lm_head forward at this temperature, with the model's own
-    post-head ops applied to the logits before the softmax. Returns the head module."""
+    post-head ops applied to the logits before the softmax. Returns the head module.
+
+    Also installs a forward pre-hook on the model (once; a later bind_head replaces it) that binds each call's GRPO
+    inputs from its kwargs to head.octopus_grpo (grpo_inputs: None unless the micro-batch carries them), as the
+    actor's own pre-hook binds the labels (actor.py:166-171). head.octopus_grpo_step = False keeps the plain route."""
     head = model.get_output_embeddings()
     head.octopus_post = _post_head_ops(model, head)
     head.octopus_temperature = temperature
     head.octopus_scored = None
+    head.octopus_grpo = None
     head.forward = types.MethodType(_chunked_head_forward, head)
+    old = getattr(head, "_octopus_grpo_hook", None)
+    if old is not None:
+        old.remove()
+
+    def stash_grpo(_module, _args, kwargs):
+        head.octopus_grpo = grpo_inputs(kwargs)
+
+    head._octopus_grpo_hook = model.register_forward_pre_hook(stash_grpo, with_kwargs=True)
     return head

@@ -170,6 +170,27 @@ def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
         assert (P, passes) == (6400, 6)  # 250 grad_h tiles a pass: one round each
 
 
+@pytest.mark.parametrize("grads", ["both", "grad_h", "grad_W"])
+def test_queried_size_runs_the_default_plan_for_each_gradient_set(grads):
+    """The size the query returns for a set of gradients runs that set's plan at the 2 GiB staging budget (not a
+    smaller budget's): the step and the backward, at 32,768 rows of d 2560, V 151,936."""
+    n, d, V = 32768, 2560, 151936
+    Vp = (V + 255) // 256 * 256
+    flags = {"both": 0, "grad_h": _lib.WS_NO_GRADW, "grad_W": _lib.WS_NO_GRADH}[grads]
+    ws = _lib.workspace_bytes(n, d, V, _lib.BF16, _lib.WS_STEP | flags)
+    P, passes, _, _ = _lib.bwd_plan(n, d, V, _lib.BF16, _lib.WS_STEP | flags, ws)
+    pmax = BUDGET // (Vp * 2) // 256 * 256
+    if grads == "grad_W":  # rows balanced over the fewest passes that fit
+        k = -(-n // pmax)
+        assert (P, passes) == (-(-(-(-n // k)) // 256) * 256, k) == (6656, 5)
+    else:  # the fewest grad_h rounds
+        assert (P, passes) == (6400, 6)
+    # the backward: the queried size is the least that runs its plan
+    bw = _lib.workspace_bytes(n, d, V, _lib.BF16, _lib.WS_BACKWARD | flags)
+    plan = _lib.bwd_plan(n, d, V, _lib.BF16, flags, bw)
+    assert plan[0] * plan[1] >= n and _lib.bwd_plan(n, d, V, _lib.BF16, flags, bw - 256) != plan
+
+
 def test_step_plan_follows_the_workspace_and_fp32_falls_back():
     n, d, V = 3000, 256, 5120
     big = _lib.workspace_bytes(n, d, V, _lib.BF16, _lib.WS_STEP)

@@ -394,13 +394,14 @@ def test_pair_gather_and_expansion_match_the_reference_composition():
 
 def test_bound_head_on_a_model_matches_its_own_logits():
     """The property of reference tests/test_lm_head.py:11-34 on the GPU, through the fused HIP head: once bound, a
-    Llama and a softcapped Gemma2 return each position's next-token log-probability and the entropy of their own fp32
-    logits (torch.distributions.Categorical), at T 1.0 and 0.7, to 1e-5."""
+    Llama, a softcapped Gemma2 and a Qwen3.5 (the reference's trained model: gated-delta-net linear attention and full
+    attention layers) return each position's next-token log-probability and the entropy of their own fp32 logits
+    (torch.distributions.Categorical), at T 1.0 and 0.7, to 1e-5."""
     from transformers import AutoModelForCausalLM
     from octopus_amd.rl.lm_head import bind_head
     from tests.tiny_models import families
     for name, config, _ in families():
-        if name not in ("llama", "gemma2"):
+        if name not in ("llama", "gemma2", "qwen3_5"):
             continue
         torch.manual_seed(3)
         model = AutoModelForCausalLM.from_config(config, attn_implementation="eager").to(DEV)

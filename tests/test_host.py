@@ -11,7 +11,7 @@ from octopus_amd.rl import lm_head, prefix_tree, seq_tiles
 from octopus_amd.rl.lm_head import _fused_post, bind_head
 from octopus_amd.rl.prefix_tree import TreeMeta, build_tree, tree_head_output
 from oracle import pairs as opairs
-from tests.tiny_models import TINY, families, packed
+from tests.tiny_models import NAMES, TINY, families, packed
 
 
 def _random_forest(rng, n_seq):
@@ -96,7 +96,7 @@ def test_tree_head_output_gives_each_position_its_own_next_token(case):
 
 
 
-@pytest.mark.parametrize("k", range(4), ids=["llama", "granitemoehybrid", "gemma2", "falcon_h1"])
+@pytest.mark.parametrize("k", range(len(NAMES)), ids=NAMES)
 def test_bound_head_reproduces_each_familys_softmax(k):
     """The property of reference tests/test_lm_head.py:11-34: once bound, the model returns for each position the
     log-probability of its next token and the entropy of the softmax of its OWN logits (post-head ops included) at
@@ -120,9 +120,41 @@ def test_bound_head_reproduces_each_familys_softmax(k):
         want = torch.distributions.Categorical(logits=own / temperature)
         assert (cols[:, 0] - want.log_prob(nxt)).abs().max().item() <= 1e-5, temperature
         assert (cols[:, 1] - want.entropy()).abs().max().item() <= 1e-5, temperature
-    assert (len(head.octopus_post) > 0) == (config.model_type != "llama")
+    assert (len(head.octopus_post) > 0) == ((pre, post, tanh) != (1.0, 1.0, False))
     fp = _fused_post(head.octopus_post)
     assert abs(fp.pre - pre) < 1e-12 and abs(fp.post - post) < 1e-12 and fp.tanh == tanh
+
+
+def test_bind_head_binds_each_calls_grpo_inputs():
+    """bind_head's pre-hook binds the micro-batch's GRPO inputs from each call's kwargs (advantages, behaviour
+    logprobs, loss mask, and proximal logprobs when given) to head.octopus_grpo, flat per position, and None for a call
+    without them (compute_logp's batch); binding again replaces the hook. CPU tensors take the composite route with
+    the inputs bound: the same columns as without them."""
+    from transformers import AutoModelForCausalLM
+    _, config, _ = families()[0]
+    torch.manual_seed(3)
+    model = AutoModelForCausalLM.from_config(config, attn_implementation="eager").eval()
+    bind_head(model, 1.0)
+    head = bind_head(model, 0.7)
+    assert len(model._forward_pre_hooks) == 1
+    ids = torch.randint(0, config.vocab_size, (1, 11), generator=torch.Generator().manual_seed(4))
+    head.octopus_labels, head.octopus_tree = ids[0].roll(-1), None
+    adv, old, mask = torch.randn(1, 11), torch.randn(1, 11), (torch.rand(1, 11) < 0.6).float()
+    with torch.no_grad():
+        plain = model(input_ids=ids).logits
+        assert head.octopus_grpo is None
+        bound = model(input_ids=ids, advantages=adv, logprobs=old, loss_mask=mask).logits
+    g = head.octopus_grpo
+    assert g is not None and g.prox is None and (g.eps_lo, g.eps_hi, g.reject_upper) == (0.2, 0.28, 5.0)
+    assert torch.equal(g.adv, adv.reshape(-1)) and torch.equal(g.old, old.reshape(-1))
+    assert torch.equal(g.mask, mask.reshape(-1))
+    assert torch.equal(plain, bound)
+    with torch.no_grad():
+        model(input_ids=ids, advantages=adv, logprobs=old, loss_mask=mask, prox_logp=old * 0.5)
+    assert torch.equal(head.octopus_grpo.prox, (old * 0.5).reshape(-1))
+    with torch.no_grad():
+        model(input_ids=ids, advantages=adv, loss_mask=mask)  # no behaviour logprobs: nothing bound
+    assert head.octopus_grpo is None
 
 
 def _llama_with_tail(after_head):

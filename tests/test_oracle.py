@@ -12,6 +12,7 @@ from oracle import fp8 as ofp8
 from oracle import grpo as ogrpo
 from oracle import head as ohead
 from oracle import pairs as opairs
+from tests.tiny_models import NAMES
 
 F64 = torch.float64
 
@@ -43,7 +44,7 @@ def test_columns_closed_forms():
     assert abs(lp[1].item() + 200.0) < 1e-9  # a label that is not the peak
 
 
-@pytest.mark.parametrize("k", range(4), ids=["llama", "granitemoehybrid", "gemma2", "falcon_h1"])
+@pytest.mark.parametrize("k", range(len(NAMES)), ids=NAMES)
 def test_head_forward_matches_the_models_own_logits(k):
     """The oracle on the lm_head input, with the family's post-head transform, gives the log-probability of each
     position's next token and the entropy of the model's own logits (the property of reference
