@@ -244,6 +244,10 @@ def main() -> int:
     ap.add_argument("--two-call", action="store_true",
                     help="run the forward and the backward as two calls (octo_head_fwd_grpo, octo_head_bwd: the "
                          "autograd route, logits recomputed in the backward) instead of the fused step")
+    ap.add_argument("--bound", action="store_true",
+                    help="time the bound route instead of the fused step: the head's columns from the fused step "
+                         "under autograd, the GRPO objective on them and loss.backward() (the trainer's unchanged call "
+                         "path after bind_head)")
     ap.add_argument("--no-context", action="store_true",
                     help="skip the two-call route's timing after the fused step's (profiling runs)")
     ap.add_argument("--hipblaslt", action="store_true",
@@ -353,6 +357,8 @@ def main() -> int:
     def step():
         if cfg.backward == "none":  # a forward-only workload: logprob and entropy of every scored row
             return forward()[2]
+        if args.bound:
+            return bound_step()
         return fused_step() if fused else two_call()
 
     for _ in range(args.warmup):
@@ -485,7 +491,9 @@ def main() -> int:
         "dtype": "bf16" if cfg.dtype == torch.bfloat16 else str(cfg.dtype).replace("torch.", ""),
         "data": "synthetic (seeded: hidden N(0,1) RMS-normalised, W N(0,0.02), Zipf(1.1) targets)",
         "config": {"workload": f"{cfg.name}: packed tree micro-batch, "
-                               + ("fused fwd+bwd GRPO logprob head (one call)" if fused else
+                               + ("bound GRPO head (fused step behind the columns, loss.backward())" if fused and
+                                  args.bound else
+                                  "fused fwd+bwd GRPO logprob head (one call)" if fused else
                                   "GRPO logprob head, forward then backward (two calls)" if cfg.backward != "none"
                                   else "logprob head forward"),
                    "N_packed": cfg.N, "scored_rows": n, "d": d, "V": V, "temperature": cfg.temperature,

@@ -26,6 +26,7 @@
 #pragma once
 
 #include "octo_common.h"
+#include "tile_order.h"
 
 namespace octo {
 
@@ -56,21 +57,9 @@ struct GemmShape {
   int64_t count_off;
 };
 
-// Block -> (mt, nt). Blocks run on XCD b % 8. The first 8 * floor(M-tiles / 8) M-tiles are dealt to the XCDs
-// round-robin (XCD x owns mt = x, x + 8, ...), and each XCD walks its own in groups of group_m across all N-tiles, so
-// the ~32 workgroups resident on an XCD run 4 M-tiles x 8 N-tiles and share A and B K-slices in its L2, while the 8
-// XCDs sweep the N-tiles in step (at 114,688 hidden rows, 0.59 GB, more than the 256 MB Infinity Cache, XCDs out of
-// step made the forward 6% slower). The tiles of the last M-tiles % 8 M-tiles are cut into 8 contiguous segments of
-// equal length (+-1), one per XCD, so every XCD holds the same number of tiles whatever the shape (whole M-tile rows
-// for those too gave an XCD with one more row a whole extra round: 99 M-tiles x 10 N-tiles ran 5 rounds of 32 tiles on
-// three XCDs against 4 on the others). Per XCD that is floor(M / 8) N + ceil((M % 8) N / 8) = ceil(M N / 8) tiles.
-// A device-side row count that bounds M or N shrinks the tile grid (read once per block), so the idle blocks all come
-// after the working ones instead of between them: interleaved idle blocks retire instantly and stagger the working
-// workgroups at every group start, which breaks their L2 sharing. The grid is 8 * ceil(bound-free tiles / 8); blocks
-// past their XCD's tiles return false.
-__host__ __device__ inline int64_t tile_grid(int mtiles, int ntiles) {
-  return 8 * (((int64_t)mtiles * ntiles + 7) / 8);
-}
+// Block -> (mt, nt): the order of tile_order.h, block b being XCD b % 8's (b / 8)-th tile. A device-side row count
+// that bounds M or N shrinks the tile grid (read once per block), so the idle blocks all come after the working ones.
+__host__ __device__ inline int64_t tile_grid(int mtiles, int ntiles) { return octo_tiles::tile_grid(mtiles, ntiles); }
 // The tile grid after a device-side row count's bound (read from memory).
 __device__ __forceinline__ void bounded_tiles(const GemmShape &s, int64_t &mtiles, int64_t &ntiles) {
   mtiles = s.mtiles;
@@ -78,32 +67,10 @@ __device__ __forceinline__ void bounded_tiles(const GemmShape &s, int64_t &mtile
   if (s.count_on == 1) mtiles = min(mtiles, cdiv(dev_count(s.count, s.count_off, s.M), (int64_t)TM));
   if (s.count_on == 2) ntiles = min(ntiles, cdiv(dev_count(s.count, s.count_off, s.N), (int64_t)TN));
 }
-// Tiles XCD x holds in the order below.
-__device__ __forceinline__ int64_t xcd_tiles(int x, int64_t mtiles, int64_t ntiles) {
-  const int64_t T = (mtiles % 8) * ntiles;
-  return (mtiles / 8) * ntiles + (x + 1) * T / 8 - x * T / 8;
-}
 // XCD x's k-th tile; false past its tiles.
 __device__ __forceinline__ bool tile_at(const GemmShape &s, int x, int64_t k, int64_t mtiles, int64_t ntiles, int &mt,
                                         int &nt) {
-  const int64_t mfull = mtiles / 8;  // M-tiles every XCD owns: x, x + 8, ..., x + 8 (mfull - 1)
-  const int64_t main = mfull * ntiles;
-  if (k < main) {
-    const int64_t span = (int64_t)s.group_m * ntiles;
-    const int64_t gid = k / span;
-    const int64_t first = gid * s.group_m;
-    const int64_t gsize = (mfull - first) < s.group_m ? (mfull - first) : s.group_m;
-    const int64_t local = k - gid * span;
-    mt = (int)(x + 8 * (first + local % gsize));
-    nt = (int)(local / gsize);
-    return true;
-  }
-  const int64_t r = mtiles - 8 * mfull, T = r * ntiles;  // the last r M-tiles, M fastest, cut into 8 segments
-  const int64_t L = x * T / 8 + (k - main);
-  if (L >= (x + 1) * T / 8) return false;
-  mt = (int)(8 * mfull + L % r);
-  nt = (int)(L / r);
-  return true;
+  return octo_tiles::tile_at(s.group_m, x, k, mtiles, ntiles, mt, nt);
 }
 // The one-shot grid's block -> (mt, nt): block b is XCD b % 8's (b / 8)-th tile.
 __device__ __forceinline__ bool tile_of(const GemmShape &s, int &mt, int &nt) {

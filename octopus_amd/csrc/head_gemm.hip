@@ -52,45 +52,28 @@ template <int NJ> struct DzSwz<Acc16N<NJ>> {
 
 // ---- epilogue: online softmax statistics ----------------------------------------------------
 
-// acc *= per-vocab-row scale (fp8 weights), then the softcap tanh if any; then stats per token.
-// wsl (optional): the tile's row scales staged in LDS (0 past V), read instead of wscale.
+// The softcap's tanh of every accumulator in place, acc = tanh(pre z), with z = acc times its vocabulary row's scale for
+// fp8 weights (the tile's scales staged in LDS at wsl, 0 past V). Without the softcap nothing is done here: stats_cols
+// applies an fp8 row scale as it reads each accumulator (the same fp32 product; an in-place multiply here made the
+// compiler spill accumulators: 112-136 bytes per lane against 24).
 template <class L, bool A_FP8, bool TANH>
-__device__ __forceinline__ void pre_transform(typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int lane,
-                                              const float *wscale, int64_t V, float pre,
+__device__ __forceinline__ void pre_transform(typename L::V (&acc)[L::NI][L::NJ], int wm, int lane, float pre,
                                               const __attribute__((address_space(3))) f32x4 *wsl = nullptr) {
-  if constexpr (A_FP8) {
-#pragma unroll
-    for (int i = 0; i < L::NI; ++i) {
-      float sc[L::NV];
-#pragma unroll
-      for (int g4 = 0; g4 < L::NV / 4; ++g4) {
-        int64_t row = m0 + L::row(wm, i, 4 * g4, lane);
-        if (wsl) {
-          const f32x4 q = wsl[L::row(wm, i, 4 * g4, lane) >> 2];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) sc[4 * g4 + u] = q[u];
-        } else if (row + 3 < V) {
-          f32x4 q = *(const f32x4 *)(wscale + row);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) sc[4 * g4 + u] = q[u];
-        } else {
-#pragma unroll
-          for (int u = 0; u < 4; ++u) sc[4 * g4 + u] = (row + u < V) ? wscale[row + u] : 0.f;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < L::NJ; ++j)
-#pragma unroll
-        for (int v = 0; v < L::NV; ++v) acc[i][j][v] *= sc[v];
-    }
-  }
+  static_assert(!A_FP8 || L::NV == 4, "fp8 weights run the 16 x 16 accumulator layout");
   if constexpr (TANH) {
 #pragma unroll
-    for (int i = 0; i < L::NI; ++i)
+    for (int i = 0; i < L::NI; ++i) {
+      f32x4 q;
+      if constexpr (A_FP8) q = wsl[L::row(wm, i, 0, lane) >> 2];
 #pragma unroll
       for (int j = 0; j < L::NJ; ++j)
 #pragma unroll
-        for (int v = 0; v < L::NV; ++v) acc[i][j][v] = ftanh(pre * acc[i][j][v]);
+        for (int v = 0; v < L::NV; ++v) {
+          float x = acc[i][j][v];
+          if constexpr (A_FP8) x *= q[v & 3];
+          acc[i][j][v] = ftanh(pre * x);
+        }
+    }
   }
 }
 
@@ -102,22 +85,29 @@ typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 // staging tile, laid out as dz_stage lays out dz (zero past V and for tokens at or past nvalid). EXM 1: as f16,
 // relative to the wave's own maximum, which the tile's part keeps. EXM 2: as bf16, times exp2(min(m2 - xoff[token],
 // kExClamp)) (and the fp8 row scale when A_FP8, from the tile's 256 scales staged in LDS at wsl), i.e. relative to
-// the token's offset (StatsArgs::xoff; xoff here points at the tile's first token).
+// the token's offset (StatsArgs::xoff; xoff here points at the tile's first token). fp8 weights without the softcap:
+// acc holds the raw e4m3 products, and each is multiplied by its row's scale (wsl) as it is read.
 template <class L, bool MASK, int EXM = 0, bool TANH = false, bool A_FP8 = false>
 __device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::NJ], int64_t m0, int wm, int wn,
                                            int lane, int64_t V, float c, lds_f32x4 *red, lds_char *tile = nullptr,
                                            int64_t nvalid = 0, const float *xoff = nullptr,
                                            const lds_f32x4 *wsl = nullptr) {
+  constexpr bool SCALE = A_FP8 && !TANH;  // the fp8 row scale applied here (with TANH, pre_transform applied it)
 #pragma unroll
   for (int j = 0; j < L::NJ; ++j) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < L::NI; ++i)
+    for (int i = 0; i < L::NI; ++i) {
+      f32x4 q;
+      if constexpr (SCALE) q = wsl[L::row(wm, i, 0, lane) >> 2];
 #pragma unroll
       for (int v = 0; v < L::NV; ++v) {
         const bool ok = !MASK || (m0 + L::row(wm, i, v, lane) < V);
-        if (ok) mx = fmaxf(mx, acc[i][j][v]);
+        float x = acc[i][j][v];
+        if constexpr (SCALE) x *= q[v & 3];
+        if (ok) mx = fmaxf(mx, x);
       }
+    }
     mx = L::col_max(mx);
     const float m2 = mx * c;
     const int tt = L::col(wn, j, lane);
@@ -130,11 +120,15 @@ __device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::
     for (int i = 0; i < L::NI; ++i)
 #pragma unroll
       for (int g4 = 0; g4 < L::NV / 4; ++g4) {
+        f32x4 q;  // fp8 weights: the scales of this lane's 4 vocab rows (LDS, 0 past V)
+        if constexpr (A_FP8) q = wsl[L::row(wm, i, 4 * g4, lane) >> 2];
         float x4[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int v = 4 * g4 + u;
-          const float t = __builtin_fmaf(acc[i][j][v], c, -m2);
+          float xs = acc[i][j][v];
+          if constexpr (SCALE) xs *= q[u];
+          const float t = __builtin_fmaf(xs, c, -m2);
           float e = fexp2(t);
           if (MASK) {
             const bool ok = m0 + L::row(wm, i, v, lane) < V;
@@ -150,8 +144,7 @@ __device__ __forceinline__ void stats_cols(const typename L::V (&acc)[L::NI][L::
         }
         if constexpr (EXM != 0) {
           const int rl = L::row(wm, i, 4 * g4, lane);  // first of this lane's 4 vocab rows in the tile
-          if constexpr (EXM == 2 && A_FP8) {  // d/d(raw e4m3 product): times the rows' scales (LDS, 0 past V)
-            const f32x4 q = wsl[rl >> 2];
+          if constexpr (EXM == 2 && A_FP8) {  // d/d(raw e4m3 product): times the rows' scales
 #pragma unroll
             for (int u = 0; u < 4; ++u) x4[u] *= q[u];
           }
@@ -193,7 +186,7 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   f32x16 acc[4][4];
   mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, s.K, smem, acc);
   const int64_t ma = e.v0 + m0;  // first vocabulary row of the tile
-  pre_transform<Acc32, false, TANH>(acc, ma, wm, lane, e.wscale, e.V, e.pre);
+  pre_transform<Acc32, false, TANH>(acc, wm, lane, e.pre);
   if (ma + TM > e.V) stats_cols<Acc32, true>(acc, ma, wm, wn, lane, e.V, e.c, red);
   else stats_cols<Acc32, false>(acc, ma, wm, wn, lane, e.V, e.c, red);
   __syncthreads();
@@ -535,6 +528,13 @@ __device__ __forceinline__ void store_any(const typename L::V (&acc)[L::NI][L::N
   }
 }
 
+// True when a tile with no K to contract (a device count of 0 rows) would only add zeros to what C or the partials
+// already hold: it can end before its mainloop. A store that overwrites, or adds an addend, still runs.
+__device__ __forceinline__ bool adds_nothing(const StoreArgs &e, int which, int64_t K_eff) {
+  if (K_eff > 0) return false;
+  return which == 1 ? (e.accumulate && !e.addend) : (which == 2 && e.part_accumulate);
+}
+
 // Which store a row pass's GEMM makes (StoreArgs pass_count / part): 0 none, 1 the final C, 2 the fp32 partials.
 __device__ __forceinline__ int pass_store(const StoreArgs &e) {
   if (!e.pass_count) return 1;
@@ -597,6 +597,42 @@ __device__ __forceinline__ void store_pass(const typename L::V (&acc)[L::NI][L::
   }
 }
 
+// The fp32 GEMMs' store: C = rs[row] x acc (+ addend) (+ C when accumulate), one loop with the run-time choices
+// inside it. Separate loops per choice (store_any) made the compiler move all 256 accumulators out of the AGPRs into
+// VGPRs ahead of the branches: 376 bytes of spills per lane, against none here. fp32 operands store no partials (their
+// sums across passes accumulate into the fp32 output), so `which` is 1 here.
+template <class L, typename OT>
+__device__ __forceinline__ void store_rt(const typename L::V (&acc)[L::NI][L::NJ], const StoreArgs &e, int64_t m0,
+                                         int64_t n0, int64_t mvalid, int64_t nvalid) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = L::wm(w), wn = L::wn(w);
+  OT *C = (OT *)e.C;
+  const bool acc_c = e.accumulate != 0, add = e.addend != nullptr;
+  const bool atomic = OCTO_PART_ATOMIC && acc_c && std::is_same<OT, float>::value;
+#pragma unroll
+  for (int i = 0; i < L::NI; ++i)
+#pragma unroll
+    for (int v = 0; v < L::NV; ++v) {
+      const int rr = L::row(wm, i, v, lane);
+      if (rr >= mvalid) continue;
+      OT *crow = C + (m0 + rr) * e.ldc + n0;
+      const float *arow = add ? e.addend + (m0 + rr) * e.ld_add + n0 : nullptr;
+      const float sc = e.row_scale ? e.row_scale[m0 + rr] : 1.f;
+#pragma unroll
+      for (int j = 0; j < L::NJ; ++j) {
+        const int cc = L::col(wn, j, lane);
+        if (cc >= nvalid) continue;
+        float x = acc[i][j][v] * sc;
+        if (add) x += arow[cc];
+        if (atomic) {
+          __hip_atomic_fetch_add((float *)crow + cc, x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else {
+          if (acc_c) x += (float)crow[cc];
+          crow[cc] = (OT)x;
+        }
+      }
+    }
+}
+
 // fp32 gradient GEMMs (4-stage loop, 32 x 32 MFMAs).
 template <int DT, int OT>
 __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_store_kernel(Operand A, Operand B, GemmShape s, StoreArgs e) {
@@ -611,10 +647,10 @@ __global__ __launch_bounds__(NTHREADS, 1) __attribute__((amdgpu_waves_per_eu(1, 
   int64_t mvalid = s.M - m0, nvalid = s.N - n0, K_eff = s.K;
   if (s.count_on == 1) mvalid = dev_count(s.count, s.count_off + m0, mvalid);
   if (s.count_on == 3) K_eff = round_up(dev_count(s.count, s.count_off, s.K), 64);
-  if (mvalid <= 0 || nvalid <= 0) return;
+  if (mvalid <= 0 || nvalid <= 0 || adds_nothing(e, which, K_eff)) return;
   f32x16 acc[4][4];
   mainloop_dma<DT, OpRows, OpRows>(A, B, m0, n0, K_eff, smem, acc);
-  store_pass<Acc32, typename Elem<OT>::T>(acc, e, which, m0, n0, mvalid, nvalid);
+  store_rt<Acc32, typename Elem<OT>::T>(acc, e, m0, n0, mvalid, nvalid);
 }
 
 // The 16-bit gradient GEMMs' 8-wave form: 512 threads, two waves per SIMD, each 128 x 64 of the tile; the second
@@ -631,7 +667,7 @@ __device__ __forceinline__ void store8_tile(const Operand &A, const Operand &B, 
   int64_t mvalid = s.M - m0, nvalid = s.N - n0, K_eff = s.K;
   if (s.count_on == 1) mvalid = dev_count(s.count, s.count_off + m0, mvalid);
   if (s.count_on == 3) K_eff = round_up(dev_count(s.count, s.count_off, s.K), 64);
-  if (mvalid <= 0 || nvalid <= 0) return;
+  if (mvalid <= 0 || nvalid <= 0 || adds_nothing(e, which, K_eff)) return;
   f32x4 acc[8][4];
   if constexpr (KM == KM_A) mainloop_ring5<DT, OpColsN<8, 128>, OpRowsN<8, 64>>(A, B, m0, n0, K_eff, smem, acc);
   else if constexpr (KM == KM_B) mainloop_ring5<DT, OpRowsN<8, 128>, OpColsN<8, 64>, true>(A, B, m0, n0, K_eff, smem, acc);
@@ -730,7 +766,7 @@ __global__ __launch_bounds__(2 * NTHREADS, 1) __attribute__((amdgpu_waves_per_eu
     }
     __syncthreads();
   }
-  pre_transform<L, A_FP8, TANH>(acc, ma, wm, lane, e.wscale, e.V, e.pre, A_FP8 ? wsl : nullptr);
+  pre_transform<L, A_FP8, TANH>(acc, wm, lane, e.pre, wsl);
   const float *xo = EX == 2 ? e.xoff + n0 : nullptr;
   if (ma + TM > e.V) stats_cols<L, true, EX, TANH, A_FP8>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid, xo, wsl);
   else stats_cols<L, false, EX, TANH, A_FP8>(acc, ma, wm, wn, lane, e.V, e.c, red, smem, nvalid, xo, wsl);
@@ -900,6 +936,8 @@ int launch_gemm_grads(int dt, const Operand &Ah, const Operand &Bh, const GemmSh
 int launch_gemm_store(int dt, const Operand &A, const Operand &B, const GemmShape &s, const StoreArgs &e,
                       hipStream_t st, int kmajor) {
   if (!e.C || !A.base || !B.base) return octo_fail(OCTO_EINVAL, "gemm_store: null operand or output");
+  if (dt == OCTO_F32 && (e.part || e.part_blocked))
+    return octo_fail(OCTO_EUNSUPPORTED, "gemm_store: fp32 operands store no partials");
   if (kmajor != KM_NONE) {
     if (!kmajor_layout_ok(kmajor == KM_A ? A : B)) return octo_fail(OCTO_EINVAL, "gemm_store: K-major operand layout");
     switch (dt) {

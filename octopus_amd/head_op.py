@@ -538,23 +538,71 @@ class _GrpoBound(torch.autograd.Function):
         ctx.held = None
         need_rows, need_weight = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         n = g_head.numel()
+        dev = gout.device
         gout = gout.float()
         if flat_pair is not None:  # per pair row: the sum over its flat tokens
             g_act = pairs_grad(gout, flat_pair, n)[:, 0].contiguous()
         elif idx is not None:  # per compact row: the output gradient at its row idx[r] (0 past the count)
             col = gout[:, 0].contiguous()
-            g_act = torch.empty(n, dtype=torch.float32, device=gout.device)
+            g_act = torch.empty(n, dtype=torch.float32, device=dev)
             _lib.call("octo_gather_f32", _p(col), 1, _p(idx), _p(count), n, _p(g_act), _stream(gout))
         else:
             g_act = gout[:, 0].contiguous()
         if count is None:
-            count = torch.full((1,), n, dtype=torch.int32, device=gout.device)
+            count = torch.full((1,), n, dtype=torch.int32, device=dev)
         c, rest, count_rest, skip = _spec_split(g_act, g_head, count[:1])
-        gr_rest, gw_rest = head_bwd(rows, ctx.weight, w_scale, labels, idx, count_rest, lse, rest, inv_T, pre, pst,
-                                    tanh, idx is not None and flat_pair is None, need_rows, need_weight)
-        gr = _scale_add(grad_rows, gr_rest, c, skip) if need_rows else None
-        gw = _scale_add(grad_w, gw_rest, c, skip) if need_weight else None
-        return gr, gw, None, None, None, None, None, None, None, None
+        # the held gradients times c (no work at all when c is 1), then the rest's gradients added into them by the
+        # recompute backward (its kernels end at once, and add nothing, when the rest is negligible)
+        always = torch.ones(1, dtype=torch.int32, device=dev)
+        if need_weight:
+            _scale_add(grad_w, grad_w, c, always)
+        if need_rows:
+            _scale_add(grad_rows, grad_rows, c, always)
+        _rest_backward(rows, ctx.weight, w_scale, labels, idx, count_rest, lse, rest, inv_T, pre, pst, tanh,
+                       idx is not None and flat_pair is None, grad_rows if need_rows else None,
+                       grad_w if need_weight else None, skip)
+        return (grad_rows if need_rows else None, grad_w if need_weight else None,
+                None, None, None, None, None, None, None, None)
+
+
+def _rest_backward(rows, weight, w_scale, labels, idx, count, lse, g, inv_T, pre, post, use_tanh, labels_via_idx,
+                   grad_rows, grad_w, skip):
+    """octo_head_bwd of g over the compact rows below the device count, ADDED into grad_rows ([rows, d], compact
+    rows scattered to idx) and grad_w ([V, d], OCTO_GRADW_ACCUMULATE); either may be None. With a count of 0 the
+    kernels end at once and nothing is added (skip [1] int32 = 1 then: the scatter's row-wise add reads nothing)."""
+    rows2, weight2 = _rows2d(rows), _rows2d(weight)
+    labels, idx = _index(labels), _index(idx)
+    n_max = idx.numel() if idx is not None else rows2.shape[0]
+    V, d = weight2.shape
+    need_rows, need_weight = grad_rows is not None, grad_w is not None
+    if n_max == 0 or not (need_rows or need_weight):
+        return
+    w_code = _dtype_code(weight2)
+    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | _lib.LSE_PAIR | (_lib.GRADW_ACCUMULATE if need_weight
+                                                                             else 0)
+    ws_flags = (_lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW) | (0 if need_rows else _lib.WS_NO_GRADH)
+                | _gather_flag(rows2, idx))
+    nbytes = _lib.workspace_bytes(n_max, d, V, w_code, ws_flags)
+    if BWD_WORKSPACE_BYTES is not None:
+        nbytes = int(BWD_WORKSPACE_BYTES)
+    ws = _workspace(nbytes, rows2)
+    gh = None
+    if need_rows:  # compact rows; without idx, rows past the count are added as they are: zeros
+        gh = (torch.empty if idx is not None else torch.zeros)(n_max, d, dtype=rows2.dtype, device=rows2.device)
+    lse_c, g_c = lse.contiguous(), g.contiguous()
+    _lib.call("octo_head_bwd", _p(rows2), rows2.shape[0], rows2.stride(0), _dtype_code(rows2),
+              _p(weight2), weight2.stride(0), w_code, _p(w_scale), _p(labels), _p(idx), _p(count),
+              n_max, d, V, flags, inv_T, pre, post, int(use_tanh), _p(lse_c),
+              _p(g_c), _p(gh), d, _dtype_code(rows2) if need_rows else _lib.F32,
+              _p(grad_w), _dtype_code(grad_w) if need_weight else _lib.F32,
+              _p(ws), ws.numel(), _stream(rows2))
+    if need_rows:
+        if idx is not None:  # rows of one idx summed in fp32, added to grad_rows; nothing past the count
+            _lib.call("octo_rows_scatter", _p(gh), d, _dtype_code(gh), _p(idx), _p(count), n_max, d,
+                      _p(grad_rows), grad_rows.stride(0), _dtype_code(grad_rows), 1, _stream(rows2))
+        else:  # compact row r is row r: grad_rows += gh (gh not read while skip is set)
+            one = torch.ones(1, dtype=torch.float32, device=rows2.device)
+            _scale_add(grad_rows, gh, one, skip)
 
 
 def grpo_bound_head(rows: Tensor, weight: Tensor, labels: Tensor, temperature: float, grpo: GrpoInputs, *,
