@@ -473,6 +473,65 @@ def test_fused_grpo_head_autograd_matches_the_two_call_route():
     assert torch.equal(out3, out1) and not loss3.requires_grad
 
 
+def test_fused_grpo_head_rounds_a_scaled_gradient_once():
+    """A loss scale that bf16 cannot hold (1/3, a micro-batch normalisation) scales the held bf16 gradients with one
+    rounding: (loss / 3).backward() gives exactly the unscaled call's gradients times fp32(1/3), rounded once to bf16.
+    Rounding the scale to bf16 first would bias every element by bf16(1/3) / (1/3) - 1 = +0.2%."""
+    from octopus_amd.head_op import fused_grpo_head
+    N, d, V, T = 1500, 256, 4096, 1.0
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, torch.bfloat16, seed=17)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    idx, count = head_op.compact_rows(scored.to(DEV))
+    kw = dict(idx=idx, count=count, labels_via_idx=True, scatter=True)
+    old = (noise.to(DEV) - 8.0).detach()
+    advd, maskd = adv.to(DEV), mask.to(DEV)
+    grads = []
+    for scale in (1.0, 1 / 3):
+        h1, W1 = hd.clone().requires_grad_(True), Wd.clone().requires_grad_(True)
+        loss, _ = fused_grpo_head(h1, W1, yd, T, advd, maskd, prox=None, old=old, **kw)
+        (loss * scale).backward()
+        grads.append((h1.grad, W1.grad))
+    torch.cuda.synchronize()
+    third = torch.tensor(1 / 3, dtype=torch.float32, device=DEV)
+    for g1, g3 in zip(*grads):
+        assert g3.dtype == torch.bfloat16 and g1.abs().max() > 0
+        assert torch.equal(g3, (g1.float() * third).to(torch.bfloat16))
+
+
+def test_autograd_routes_take_transposed_views():
+    """Hidden rows and weight handed in as transposed views (dense, column-major): the ops read them through
+    contiguous copies and allocate their gradients row-major, as the library writes them, so the gradients that reach
+    the views' bases are the contiguous run's, bit for bit. fused_head (the recomputing backward) and
+    fused_grpo_head (the fused step)."""
+    from octopus_amd.head_op import fused_grpo_head, fused_head
+    N, d, V, T = 1200, 256, 4096, 0.8
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, torch.bfloat16, seed=23)
+    hd, Wd, yd = h.to(DEV), W.to(DEV), y.to(DEV)
+    idx, count = head_op.compact_rows(scored.to(DEV))
+    kw = dict(idx=idx, count=count, labels_via_idx=True, scatter=True)
+    advd, maskd, old = adv.to(DEV), mask.to(DEV), (noise.to(DEV) - 8.0)
+    wout = torch.randn(N, device=DEV)
+
+    def run(route, transposed):
+        hb = (hd.t().contiguous() if transposed else hd.clone()).requires_grad_(True)
+        Wb = (Wd.t().contiguous() if transposed else Wd.clone()).requires_grad_(True)
+        h1, W1 = (hb.t(), Wb.t()) if transposed else (hb, Wb)
+        if transposed:
+            assert not h1.is_contiguous() and not W1.is_contiguous()
+        if route == "two-call":
+            (fused_head(h1, W1, yd, T, **kw)[:, 0] * wout).sum().backward()
+        else:
+            fused_grpo_head(h1, W1, yd, T, advd, maskd, prox=None, old=old, **kw)[0].backward()
+        gh, gw = hb.grad, Wb.grad
+        return (gh.t(), gw.t()) if transposed else (gh, gw)
+
+    for route in ("two-call", "step"):
+        base, views = run(route, False), run(route, True)
+        torch.cuda.synchronize()
+        for a, b in zip(base, views):
+            assert a.abs().max() > 0 and torch.equal(a, b), route
+
+
 def _tree_batch(seed, n_seq=5, prefix=600, V=4096, d=256):
     """A packed prefix tree (sequences sharing a prefix, random continuations), its per-flat-token GRPO inputs."""
     from octopus_amd.rl.prefix_tree import build_tree
