@@ -534,6 +534,8 @@ class _GrpoBound(torch.autograd.Function):
     def backward(ctx, gout):
         rows, w_scale, labels, idx, count, flat_pair, lse, g_head = ctx.saved_tensors
         inv_T, pre, pst, tanh = ctx.params
+        if ctx.held is None:  # the held gradients were scaled in place and handed to autograd by the first backward
+            raise RuntimeError("the bound GRPO head's backward runs once per forward (retain_graph is not supported)")
         grad_rows, grad_w = ctx.held
         ctx.held = None
         need_rows, need_weight = ctx.needs_input_grad[0], ctx.needs_input_grad[1]

@@ -203,3 +203,15 @@ def test_bound_model_takes_the_step_through_the_trainers_call_path(tree):
             head.octopus_grpo_step = False
             with torch.no_grad():
                 assert torch.equal(plain, model(**batch).logits)
+
+
+def test_bound_route_refuses_a_second_backward():
+    """The held gradients are scaled in place and handed to autograd by the backward, so a second backward through
+    the same graph (retain_graph) raises rather than scaling them again."""
+    h, W, y, scored, mask, adv, hd, Wd, yd, idx, count, old, grpo, T = _flat_case(N=600)
+    h1, W1 = hd.clone().requires_grad_(True), Wd.clone().requires_grad_(True)
+    out = head_op.grpo_bound_head(h1, W1, yd, T, grpo, idx=idx, count=count)
+    loss = _objective(out[:, 0], grpo, 1.0, 0.0)
+    loss.backward(retain_graph=True)
+    with pytest.raises(RuntimeError, match="runs once"):
+        loss.backward()
