@@ -43,9 +43,10 @@
  *                                                     prefix_tree.py:416-421): octo_head_step_grpo_pairs
  *   octopus/rl/actor.py:166-171, 343-347 unchanged (bind_head's own pre-hook binds the micro-batch's GRPO
  *     inputs; AReaL's loss.backward() reaches the head's backward) -> octo_head_step_grpo in the forward,
- *                                                     and in the backward octo_scale_add of its gradients
- *                                                     plus octo_head_bwd of the rest of dL/dlogprob (its
- *                                                     kernels end at once when that rest is negligible)
+ *                                                     and in the backward octo_grpo_fit, octo_scale_add of
+ *                                                     its gradients, and octo_head_bwd of the rest of
+ *                                                     dL/dlogprob (its kernels end at once when that rest
+ *                                                     is negligible)
  */
 #ifndef OCTO_HEAD_H
 #define OCTO_HEAD_H
@@ -221,12 +222,22 @@ int octo_rows_scatter(const void *src, int64_t ld_src, int src_dtype, const int6
                       void *dst, int64_t ld_dst, int dst_dtype, int accumulate, void *stream);
 
 /* y[i] = c y[i] + x[i] for i < n, with c = *c read on the device, formed in fp32 and rounded once to dtype (BF16, F16
- * or F32); while skip_x is given and *skip_x != 0, x counts as zero and is not read (c = 1 then leaves y as it is at
- * once). y and x 16-byte aligned. No counterpart in the reference, whose autograd sums the chunks' gradients: the
+ * or F32); while skip_x is given and *skip_x != 0, or x is NULL, x counts as zero and is not read (c = 1 then leaves y
+ * as it is at once). y and x 16-byte aligned. No counterpart in the reference, whose autograd sums the chunks' gradients: the
  * backward of the bound GRPO step (octopus_amd/head_op.py) uses it to scale the gradients its forward computed by the
  * incoming gradient's multiple of the head's own GRPO weight and add the backward of the rest. */
 int octo_scale_add(void *y, const void *x, int dtype, int64_t n, const float *c, const int32_t *skip_x,
                    void *stream);
+
+/* The bound GRPO step's fit of the incoming dL/dlogprob, on the device: a[r] = src[idx[r] * ld_src] (src[r * ld_src]
+ * without idx) for r < *count (all n without count), 0 past it; c = <a, g_head> / <g_head, g_head> (0 when g_head is
+ * 0); rest[r] = a[r] - c g_head[r] for r < n; and when ||rest|| <= tol ||a||, *count_rest = 0 and *skip = 1 (the
+ * rest's octo_head_bwd then ends at once), else *count_rest = the row count and *skip = 0. One workgroup, sums in a
+ * fixed order. No counterpart in the reference: the backward of the bound GRPO step (octopus_amd/head_op.py) runs it
+ * in place of a dozen small tensor operations. */
+int octo_grpo_fit(const float *src, int64_t ld_src, const int64_t *idx, const float *g_head, int64_t n,
+                  const int32_t *count, float tol, float *c, float *rest, int32_t *count_rest, int32_t *skip,
+                  void *stream);
 
 /* out[r] = src[idx[r] * ld_src] (fp32) for r < *count, 0 for count <= r < n_max. */
 int octo_gather_f32(const float *src, int64_t ld_src, const int64_t *idx, const int32_t *count,

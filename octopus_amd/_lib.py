@@ -67,6 +67,7 @@ SIGNATURES = {
     "octo_rows_scatter": [_p, _i64, _i32, _p, _p, _i64, _i32, _p, _i64, _i32, _i32, _p],
     "octo_gather_f32": [_p, _i64, _p, _p, _i64, _p, _p],
     "octo_scale_add": [_p, _p, _i32, _i64, _p, _p, _p],
+    "octo_grpo_fit": [_p, _i64, _p, _p, _i64, _p, _f32, _p, _p, _p, _p, _p],
     "octo_label_pairs_workspace_bytes": [_i64, _i64, ctypes.POINTER(_sz)],
     "octo_label_pairs": [_p, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p, _p, _i32, _p, _sz, _p],
     "octo_quantise_fp8_rows": [_p, _i64, _i32, _i64, _i32, _p, _i64, _p, _p],

@@ -423,12 +423,12 @@ int launch_ex_fix(const ExFixArgs &a, hipStream_t st) {
 
 // ---- y = c y + x over a vector (the bound GRPO step's backward) ------------------------------------------------------
 // c is read from device memory, and so is `skip_x` (when given): while it is non-zero x counts as zero and is not read.
-// The product and the sum are formed in fp32 and rounded once to the vector's type. With c = 1 and x skipped, y is
-// already the result and every workgroup ends at once. 16 bytes per thread and step.
+// x = NULL: y = c y. The product and the sum are formed in fp32 and rounded once to the vector's type. With c = 1 and
+// no x to add, y is already the result and every workgroup ends at once. 16 bytes per thread and step.
 __global__ __launch_bounds__(256) void scale_add_kernel(void *y, const void *x, int dtype, int64_t n, const float *c,
                                                         const int32_t *skip_x) {
   const float s = *c;
-  const bool add = !(skip_x && *skip_x);
+  const bool add = x && !(skip_x && *skip_x);
   if (s == 1.f && !add) return;
   const int per = dtype == OCTO_F32 ? 4 : 8;  // elements per 16-byte chunk
   const int64_t chunks = n / per;
@@ -506,6 +506,14 @@ int launch_pairs_grpo(const PairsGrpoArgs &a, hipStream_t st) {
 }
 
 // ---- transpose -----------------------------------------------------------------------------------
+// Rows of dst written: all rows_pad without a device count (zeros past rows: a staged W^T is read to the next multiple
+// of 256); with one, the count rounded up to 64, the K extent the gradient GEMMs read of a count-bounded h^T
+// (GemmShape count_on 3), so that columns no GEMM reads are not zero-filled. A whole tile past it ends at once (the
+// check is uniform across the block: r0 is the block's).
+__device__ __forceinline__ int64_t written_rows(const int32_t *count, int64_t valid, int64_t rows_pad) {
+  return count ? min(rows_pad, (valid + 63) / 64 * 64) : rows_pad;
+}
+
 // dst[c, r] = src[row(r), c]: 64 x 64 tiles through LDS (fp32 words, padded against bank conflicts).
 __global__ __launch_bounds__(256) void transpose_kernel(const void *src, int64_t ld_src, int src_dtype,
                                                         const int64_t *map, const int32_t *count,
@@ -514,6 +522,8 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *src, int64_t
   __shared__ float tile[64][65];
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
   const int64_t valid = dev_count(count, count_off, rows);
+  const int64_t lim = written_rows(count, valid, rows_pad);
+  if (r0 >= lim) return;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int i = ty; i < 64; i += 4) {
     const int64_t r = r0 + i, c = c0 + tx;
@@ -528,7 +538,7 @@ __global__ __launch_bounds__(256) void transpose_kernel(const void *src, int64_t
   __syncthreads();
   for (int i = ty; i < 64; i += 4) {
     const int64_t c = c0 + i, r = r0 + tx;
-    if (c < cols && r < rows_pad) store_from_f32(dst, dst_dtype, c * ld_dst + r, tile[tx][i]);
+    if (c < cols && r < lim) store_from_f32(dst, dst_dtype, c * ld_dst + r, tile[tx][i]);
   }
 }
 
@@ -545,6 +555,8 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const char *src, int64
   __attribute__((address_space(3))) char *tile = (__attribute__((address_space(3))) char *)tile_;
   const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
   const int64_t valid = dev_count(count, count_off, rows);
+  const int64_t lim = written_rows(count, valid, rows_pad);
+  if (r0 >= lim) return;
   const int t = threadIdx.x;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
@@ -575,7 +587,7 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const char *src, int64
     const int c = t + 256 * k;  // destination row c0 + (c >> 3), source rows r0 + 8 (c & 7) ..
     const int drow = c >> 3, rc = c & 7;
     const int64_t col = c0 + drow, r = r0 + 8 * rc;
-    if (col < cols && r < rows_pad) {
+    if (col < cols && r < lim) {
       const i32x4 v = *(const lds_i32x4_t *)(tile + drow * 128 + ((rc ^ ((drow >> 3) & 7)) << 4));
       *(i32x4 *)(dst + (col * ld_dst + r) * 2) = v;
     }
@@ -809,6 +821,69 @@ __global__ void gather_f32_kernel(const float *src, int64_t ld, const int64_t *i
   if (r >= n_max) return;
   const int64_t cnt = count ? min((int64_t)(*count), n_max) : n_max;
   out[r] = (r < cnt) ? src[idx[r] * ld] : 0.f;
+}
+
+// ---- the bound GRPO step's fit of the incoming dL/dlogprob -------------------------------------------------------
+// a[r], the incoming dL/dlogprob of compact row r: src[idx[r] ld] (src[r ld] without idx) for r below the count, 0
+// past it; h[r], the step's own GRPO weight of row r. c = <a, h> / <h, h> (0 when h is 0) and rest = a - c h. The rest
+// is negligible when ||rest|| <= tol ||a||: then *count_rest = 0 and *skip = 1, so the rest's backward ends at once,
+// else *count_rest = the row count and *skip = 0. One workgroup; every sum in a fixed order, so equal inputs give
+// equal bits.
+__global__ __launch_bounds__(1024) void grpo_fit_kernel(const float *src, int64_t ld, const int64_t *idx,
+                                                        const float *h, int64_t n, const int32_t *count, float tol,
+                                                        float *c_out, float *rest, int32_t *count_rest,
+                                                        int32_t *skip) {
+  __shared__ float part[3][16];
+  __shared__ float cs;
+  const int64_t cnt = count ? min((int64_t)(*count), n) : n;
+  const int w = threadIdx.x >> 6;
+  float ah = 0.f, hh = 0.f, aa = 0.f;
+  for (int64_t r = threadIdx.x; r < n; r += 1024) {
+    const float a = r < cnt ? src[(idx ? idx[r] : r) * ld] : 0.f, g = h[r];
+    ah = __builtin_fmaf(a, g, ah);
+    hh = __builtin_fmaf(g, g, hh);
+    aa = __builtin_fmaf(a, a, aa);
+  }
+  ah = wave_sum(ah);
+  hh = wave_sum(hh);
+  aa = wave_sum(aa);
+  if ((threadIdx.x & 63) == 0) {
+    part[0][w] = ah;
+    part[1][w] = hh;
+    part[2][w] = aa;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s0 = 0.f, s1 = 0.f;
+    for (int k = 0; k < 16; ++k) {
+      s0 += part[0][k];
+      s1 += part[1][k];
+    }
+    cs = s1 > 0.f ? s0 / s1 : 0.f;
+  }
+  __syncthreads();
+  const float c = cs;
+  float rr = 0.f;
+  for (int64_t r = threadIdx.x; r < n; r += 1024) {
+    const float a = r < cnt ? src[(idx ? idx[r] : r) * ld] : 0.f;
+    const float x = a - c * h[r];
+    rest[r] = x;
+    rr = __builtin_fmaf(x, x, rr);
+  }
+  rr = wave_sum(rr);
+  if ((threadIdx.x & 63) == 0) part[0][w] = rr;  // part[0] was last read by thread 0 before the barrier above
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f, a2 = 0.f;
+    for (int k = 0; k < 16; ++k) {
+      s += part[0][k];
+      a2 += part[2][k];
+    }
+    const bool small = sqrtf(s) <= tol * sqrtf(a2);
+    *c_out = c;
+    *count_rest = small ? 0 : (int32_t)cnt;
+    *skip = small ? 1 : 0;
+  }
 }
 
 // ---- GRPO ----------------------------------------------------------------------------------------
@@ -1062,13 +1137,24 @@ int octo_scale_add(void *y, const void *x, int dtype, int64_t n, const float *c,
   OCTO_CHECK_ARG(n >= 0, "scale_add: n < 0");
   OCTO_CHECK_ARG(dtype == OCTO_BF16 || dtype == OCTO_F16 || dtype == OCTO_F32, "scale_add: dtype %d", dtype);
   if (n == 0) return OCTO_OK;
-  OCTO_CHECK_ARG(y && x && c, "scale_add: null pointer");
+  OCTO_CHECK_ARG(y && c, "scale_add: null pointer");
   OCTO_CHECK_ARG(((uintptr_t)y) % 16 == 0 && ((uintptr_t)x) % 16 == 0, "scale_add: vectors must be 16-byte aligned");
   const int64_t chunks = n / (dtype == OCTO_F32 ? 4 : 8);
   const int64_t blocks = cdiv(chunks, 256);
   hipLaunchKernelGGL(scale_add_kernel, dim3((unsigned)(blocks < 1 ? 1 : (blocks > 2048 ? 2048 : blocks))), dim3(256),
                      0, (hipStream_t)stream, y, x, dtype, n, c, skip_x);
   OCTO_CHECK_LAUNCH("scale_add");
+  return OCTO_OK;
+}
+
+int octo_grpo_fit(const float *src, int64_t ld_src, const int64_t *idx, const float *g_head, int64_t n,
+                  const int32_t *count, float tol, float *c, float *rest, int32_t *count_rest, int32_t *skip,
+                  void *stream) {
+  OCTO_CHECK_ARG(n >= 0 && ld_src >= 1, "grpo_fit: bad shape");
+  OCTO_CHECK_ARG(c && count_rest && skip && (n == 0 || (src && g_head && rest)), "grpo_fit: null pointer");
+  hipLaunchKernelGGL(grpo_fit_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, src, ld_src, idx, g_head, n, count,
+                     tol, c, rest, count_rest, skip);
+  OCTO_CHECK_LAUNCH("grpo_fit");
   return OCTO_OK;
 }
 

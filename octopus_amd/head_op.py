@@ -479,24 +479,29 @@ class GrpoInputs(NamedTuple):
     reject_upper: float = 5.0
 
 
-def _spec_split(g_act: Tensor, g_head: Tensor, count: Tensor):
-    """(c, rest, count_rest, skip): c g_head is the least-squares multiple of the head's own GRPO weight in the
-    incoming dL/dlogprob g_act (both per compact row), rest = g_act - c g_head, count_rest = 0 where rest is
-    negligible (SPEC_TOL), else count, so that the residual backward's kernels end at once; skip [1] int32 = 1 then.
-    Everything stays on the device."""
-    g_act, g_head = g_act.float().reshape(-1), g_head.float().reshape(-1)
-    den = torch.dot(g_head, g_head)
-    c = torch.where(den > 0, torch.dot(g_act, g_head) / den, torch.zeros_like(den)).reshape(1)
-    rest = g_act - c * g_head
-    small = torch.linalg.vector_norm(rest) <= SPEC_TOL * torch.linalg.vector_norm(g_act)
-    count_rest = torch.where(small, torch.zeros_like(count), count).to(torch.int32)
-    return c.contiguous(), rest.contiguous(), count_rest.contiguous(), small.to(torch.int32).reshape(1).contiguous()
+def _fit(src: Tensor, idx: Optional[Tensor], g_head: Tensor, count: Optional[Tensor]):
+    """(c, rest, count_rest, skip) from octo_grpo_fit: the incoming dL/dlogprob per compact row, a[r] = src[idx[r], 0]
+    (src[r, 0] without idx; 0 past the count), fitted as c times the head's own GRPO weight g_head (least squares);
+    rest = a - c g_head; count_rest = 0 and skip [1] int32 = 1 when the rest is negligible (SPEC_TOL), else the count
+    and 0, so that the residual backward's kernels end at once. One kernel; everything stays on the device."""
+    n = g_head.numel()
+    dev = g_head.device
+    c = torch.empty(1, dtype=torch.float32, device=dev)
+    rest = torch.empty(n, dtype=torch.float32, device=dev)
+    count_rest = torch.empty(1, dtype=torch.int32, device=dev)
+    skip = torch.empty(1, dtype=torch.int32, device=dev)
+    src = src.float().contiguous()
+    g_head = g_head.float().contiguous()
+    idx_c = None if idx is None else _index(idx)
+    _lib.call("octo_grpo_fit", _p(src), src.stride(0), _p(idx_c), _p(g_head), n, _p(count), SPEC_TOL, _p(c),
+              _p(rest), _p(count_rest), _p(skip), _stream(g_head))
+    return c, rest, count_rest, skip
 
 
-def _scale_add(held: Tensor, rest: Tensor, c: Tensor, skip: Tensor) -> Tensor:
-    """held = c held + rest in place (rest not read while skip is set); returns held."""
+def _scale_add(held: Tensor, rest: Optional[Tensor], c: Tensor, skip: Optional[Tensor]) -> Tensor:
+    """held = c held + rest in place (rest None, or not read while skip is set: held = c held); returns held."""
     if held.numel():
-        rest = rest.contiguous()
+        rest = None if rest is None else rest.contiguous()
         _lib.call("octo_scale_add", _p(held), _p(rest), _dtype_code(held), held.numel(), _p(c), _p(skip),
                   _stream(held))
     return held
@@ -505,7 +510,7 @@ def _scale_add(held: Tensor, rest: Tensor, c: Tensor, skip: Tensor) -> Tensor:
 class _GrpoBound(torch.autograd.Function):
     """The head's (logprob, entropy) columns from octo_head_step_grpo (or _pairs), which also computes the gradients
     of the GRPO objective on them; the backward fits the incoming dL/dlogprob as c times the step's own weight g
-    (_spec_split), scales the held gradients by c and adds octo_head_bwd's gradients of the rest, whose kernels end at
+    (_fit), scales the held gradients by c and adds octo_head_bwd's gradients of the rest, whose kernels end at
     once when the rest is negligible. A loss that is the objective (times any constant) costs the forward's one pass
     over the logits; any other loss on the logprob column still gets its exact gradients, at the cost of the
     recompute backward. The entropy column carries no gradient (lm_head.py:111)."""
@@ -540,26 +545,17 @@ class _GrpoBound(torch.autograd.Function):
         ctx.held = None
         need_rows, need_weight = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         n = g_head.numel()
-        dev = gout.device
-        gout = gout.float()
+        gout = gout.float().contiguous()
         if flat_pair is not None:  # per pair row: the sum over its flat tokens
-            g_act = pairs_grad(gout, flat_pair, n)[:, 0].contiguous()
-        elif idx is not None:  # per compact row: the output gradient at its row idx[r] (0 past the count)
-            col = gout[:, 0].contiguous()
-            g_act = torch.empty(n, dtype=torch.float32, device=dev)
-            _lib.call("octo_gather_f32", _p(col), 1, _p(idx), _p(count), n, _p(g_act), _stream(gout))
-        else:
-            g_act = gout[:, 0].contiguous()
-        if count is None:
-            count = torch.full((1,), n, dtype=torch.int32, device=dev)
-        c, rest, count_rest, skip = _spec_split(g_act, g_head, count[:1])
+            c, rest, count_rest, skip = _fit(pairs_grad(gout, flat_pair, n), None, g_head, count)
+        else:  # per compact row: the output gradient at its row idx[r] (row r without idx; 0 past the count)
+            c, rest, count_rest, skip = _fit(gout, idx, g_head, count)
         # the held gradients times c (no work at all when c is 1), then the rest's gradients added into them by the
         # recompute backward (its kernels end at once, and add nothing, when the rest is negligible)
-        always = torch.ones(1, dtype=torch.int32, device=dev)
         if need_weight:
-            _scale_add(grad_w, grad_w, c, always)
+            _scale_add(grad_w, None, c, None)
         if need_rows:
-            _scale_add(grad_rows, grad_rows, c, always)
+            _scale_add(grad_rows, None, c, None)
         _rest_backward(rows, ctx.weight, w_scale, labels, idx, count_rest, lse, rest, inv_T, pre, pst, tanh,
                        idx is not None and flat_pair is None, grad_rows if need_rows else None,
                        grad_w if need_weight else None, skip)
@@ -580,8 +576,8 @@ def _rest_backward(rows, weight, w_scale, labels, idx, count, lse, g, inv_T, pre
     if n_max == 0 or not (need_rows or need_weight):
         return
     w_code = _dtype_code(weight2)
-    flags = (_lib.ROWS_VIA_IDX if labels_via_idx else 0) | _lib.LSE_PAIR | (_lib.GRADW_ACCUMULATE if need_weight
-                                                                             else 0)
+    flags = ((_lib.ROWS_VIA_IDX if labels_via_idx else 0) | _lib.LSE_PAIR
+             | (_lib.GRADW_ACCUMULATE if need_weight else 0))
     ws_flags = (_lib.WS_BACKWARD | (0 if need_weight else _lib.WS_NO_GRADW) | (0 if need_rows else _lib.WS_NO_GRADH)
                 | _gather_flag(rows2, idx))
     nbytes = _lib.workspace_bytes(n_max, d, V, w_code, ws_flags)

@@ -27,6 +27,15 @@ def test_library_exports_every_declared_symbol():
     assert lib.octo_version().startswith(b"octo_head")
 
 
+def test_ctypes_constants_match_the_header():
+    """Every numeric #define OCTO_<NAME> of the header (status codes, element types, flags) has the same value as
+    the binding's <NAME>, so no flag reaches the library with another meaning."""
+    defines = dict(re.findall(r"^#define\s+OCTO_(\w+)\s+(-?\d+)", open(HEADER).read(), flags=re.M))
+    assert len(defines) >= 19
+    for name, value in defines.items():
+        assert getattr(_lib, name) == int(value), name
+
+
 GIB = 1 << 30
 BUDGET = 2 * GIB  # the backward's default staging budget
 

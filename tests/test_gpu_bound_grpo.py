@@ -215,3 +215,44 @@ def test_bound_route_refuses_a_second_backward():
     loss.backward(retain_graph=True)
     with pytest.raises(RuntimeError, match="runs once"):
         loss.backward()
+
+
+def _fit_call(src, idx, h, count):
+    n = h.numel()
+    c = torch.full((1,), -7.0, device=DEV)
+    rest = torch.full((n,), -7.0, device=DEV)
+    cr = torch.full((1,), -7, dtype=torch.int32, device=DEV)
+    skip = torch.full((1,), -7, dtype=torch.int32, device=DEV)
+    P = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    _lib.call("octo_grpo_fit", P(src), src.stride(0), P(idx), P(h), n, P(count), head_op.SPEC_TOL, P(c), P(rest),
+              P(cr), P(skip), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    return c.item(), rest, cr.item(), skip.item()
+
+
+def test_grpo_fit_through_the_c_abi():
+    """octo_grpo_fit against the same arithmetic in torch: a gathered through idx up to the device count (0 past it),
+    c the least-squares multiple of h, rest = a - c h, and the rest's row count 0 (skip 1) exactly when it is
+    negligible; with h = 0, c = 0 and the whole of a is the rest; with no rows, nothing to fit."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    N, n = 5000, 3000
+    src = torch.randn(N, 2, device=DEV, generator=g)
+    idx = torch.randperm(N, device=DEV, generator=g)[:n].sort().values
+    h = torch.randn(n, device=DEV, generator=g)
+    count = torch.tensor([2500], dtype=torch.int32, device=DEV)
+    a = torch.where(torch.arange(n, device=DEV) < 2500, src[idx, 0], torch.zeros((), device=DEV))
+    h[2500:] = 0.0
+    c, rest, cr, skip = _fit_call(src, idx, h, count)  # unrelated a: the rest is everything but its h component
+    c_ref = (a @ h / (h @ h)).item()
+    assert abs(c - c_ref) <= 1e-5 * abs(c_ref) + 1e-7
+    assert torch.allclose(rest, a - c * h, atol=1e-6) and (cr, skip) == (2500, 0)
+    src2 = torch.zeros(N, 2, device=DEV)
+    src2[idx[:2500], 0] = h[:2500] / 3  # a = h / 3 (rounded): c = 1/3 and a negligible rest
+    c, rest, cr, skip = _fit_call(src2, idx, h, count)
+    assert abs(c - 1 / 3) <= 1e-6 and (cr, skip) == (0, 1)
+    assert rest.abs().max().item() <= 1e-6 * h.abs().max().item()
+    c, rest, cr, skip = _fit_call(src, None, torch.zeros(n, device=DEV), None)  # h = 0, no idx, no count
+    assert c == 0.0 and torch.equal(rest, src[:n, 0]) and (cr, skip) == (n, 0)
+    c, rest, cr, skip = _fit_call(src, None, torch.zeros(0, device=DEV), None)  # no rows
+    assert c == 0.0 and (cr, skip) == (0, 1)
+
