@@ -106,8 +106,8 @@ int octo_timing_read(const char *kernel, int *launches, double *total_ms);
  * Backward: the size of its plan at a 2 GiB staging budget (see octo_head_bwd); a smaller workspace is accepted
  * down to the plan at a 1 MiB budget, a larger one may run fewer chunks. OCTO_WS_STEP [| OCTO_WS_NO_GRADW |
  * OCTO_WS_NO_GRADH]: for octo_head_step_grpo and octo_head_step_grpo_pairs (n_max = the pair rows), whose plan has
- * row passes only: one pass of the n_max rows when n_max <= 32,768 and its [n_max, V] staging fits 12 GiB, else
- * passes within the 2 GiB staging budget; for fp32 operands the larger of the forward's and the backward's. */
+ * row passes only, each pass's [rows, V] exponentials within the 2 GiB staging budget (a larger workspace runs larger
+ * passes); for fp32 operands the larger of the forward's and the backward's. */
 int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flags, size_t *bytes);
 
 /* The chunking octo_head_bwd runs in ws_bytes of workspace (a planning aid; no counterpart in the reference):

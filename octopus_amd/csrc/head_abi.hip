@@ -795,7 +795,7 @@ int octo_head_workspace_bytes(int64_t n_max, int d, int V, int w_dtype, int flag
   const bool gather = flags & OCTO_WS_GATHER;
   if (flags & OCTO_WS_STEP) {
     StepLayout L;
-    if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, step_default_budget(n_max, V, w_dtype), L)) {
+    if (step_plan(n_max, d, V, w_dtype, need_gh, need_gw, gather, kStagingBudget, L)) {
       *bytes = L.total;
     } else {
       if (elem_bytes(staged_dtype(w_dtype)) == 2)

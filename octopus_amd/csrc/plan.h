@@ -26,11 +26,6 @@ constexpr int64_t kPassRowsMax = 32768;
 // Default budget of the chunk-sized staging (dz, grad_h partials, the chunk's W^T or widened fp8 rows): 2 GiB, against
 // 2 V bytes per row for the whole dz (7.5 GB at 24,576 rows and V = 151,936).
 constexpr size_t kStagingBudget = (size_t)2 << 30;
-// The fused step's default staging: one pass over all n_max rows when that pass's [rows, V_pad] staging is at most
-// kOnePassBudget, else passes within kStagingBudget. One pass leaves out the fp32 grad_W partials across passes
-// (1.56 GB added per pass at d 2560, V 151,936) and every pass's tail; at 32,768 rows of V 151,936 bf16 it holds
-// 9.96 GB of the part's 288 GB.
-constexpr size_t kOnePassBudget = (size_t)12 << 30;
 // The forward widens fp8 weights to bf16 one vocabulary chunk at a time, at most this many bytes of them.
 constexpr size_t kFwdWideBytes = (size_t)256 << 20;
 constexpr size_t kAlign = 256;
@@ -331,13 +326,6 @@ inline bool step_plan_for(int64_t n_max, int d, int V, int w_dtype, bool need_gh
         return true;
   }
   return false;
-}
-
-// The staging budget of the fused step's default plan (the workspace query): one pass of the n_max rows when its
-// staging fits kOnePassBudget, else kStagingBudget.
-inline size_t step_default_budget(int64_t n_max, int V, int w_dtype) {
-  const size_t one = (size_t)round_to(n_max, kTile) * (size_t)round_to(V, kTile) * elem_bytes(staged_dtype(w_dtype));
-  return (n_max <= kPassRowsMax && one > kStagingBudget && one <= kOnePassBudget) ? one : kStagingBudget;
 }
 
 // Workspace of the step for fp32 operands: the forward's, then the backward's (at the default budget), in turn.

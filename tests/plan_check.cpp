@@ -201,11 +201,6 @@ int main() {
                   }
                 }
               }
-              StepLayout SD;  // the query's default plan (one pass up to kOnePassBudget)
-              if (step_plan(n, d, V, dt, gh, gw, gather, step_default_budget(n, V, dt), SD)) {
-                check_step(SD, n, d, V, dt, gh, gw, gather);
-                CHECK(SD.passes <= 1 || step_default_budget(n, V, dt) == kStagingBudget, "default step plan");
-              }
               StepLayout S0;
               if (n <= 32768 && step_plan(n, d, V, dt, gh, gw, gather, kStagingBudget, S0)) {
                 for (size_t ws : {S0.total, S0.total / 3, (size_t)(64 << 20)}) {

@@ -143,22 +143,15 @@ def _gradh_rounds(n, d, p_tiles):
     return (passes - 1) * -(-(p_tiles * nd) // 256) + -(-(last * nd) // 256)
 
 
-def _step_budget(n, Vp, esz=2):
-    """The staging budget of the fused step's default plan: one pass of all n rows when its [rows, V_pad] staging
-    lies between 2 GiB and 12 GiB (and n within the 32,768-row pass cap), else 2 GiB."""
-    one = -(-n // 256) * 256 * Vp * esz
-    return one if n <= 32768 and BUDGET < one <= 12 * GIB else BUDGET
-
-
 @pytest.mark.parametrize("n,d,V,w,flags", [
-    (32768, 2560, 151936, _lib.BF16, 0),                     # 32,768 packed rows, grad_h + grad_W: one pass
+    (32768, 2560, 151936, _lib.BF16, 0),                     # 32,768 packed rows, grad_h + grad_W: six passes
     (65536, 4096, 128256, _lib.BF16, 0),                     # d 4096, V 128,256: eight passes of 8,192
     (131072, 2560, 151936, _lib.FP8E4M3, _lib.WS_NO_GRADW),  # fp8 weights, grad_h only
     (32768, 2560, 151937, _lib.F16, _lib.WS_NO_GRADW),       # V not a multiple of 64: W^T staged once
 ])
 def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     """The fused step's workspace at the default plan: one pass's [rows, V_pad] exponentials (then dz) within the
-    staging budget (one pass of all rows up to 12 GiB, else 2 GiB), plus that pass's statistics, h^T and label entries, each row's columns (for pair rows), the
+    2 GiB staging budget, plus that pass's statistics, h^T and label entries, each row's columns (for pair rows), the
     row offsets of the bf16 exponentials with their target dots, dz scales and flagged rows,
     fp32 grad_W partials over several passes (tile-blocked over V rounded up to 256 rows when d is a multiple of 256),
     and once per call the widened fp8 weights and W^T (where grad_h cannot
@@ -167,10 +160,9 @@ def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     ws = _lib.workspace_bytes(n, d, V, w, _lib.WS_STEP | flags)
     P, passes, Vp, one = _lib.bwd_plan(n, d, V, w, _lib.WS_STEP | flags, ws)
     assert Vp == (V + 255) // 256 * 256 and one == 1
-    budget = _step_budget(n, Vp)
-    assert P % 256 == 0 and P * Vp * 2 <= budget and passes == -(-n // P)
+    assert P % 256 == 0 and P * Vp * 2 <= BUDGET and passes == -(-n // P)
     need_gw = not flags & _lib.WS_NO_GRADW
-    pmax = min(32768, budget // (Vp * 2) // 256 * 256)
+    pmax = min(32768, BUDGET // (Vp * 2) // 256 * 256)
     top = min(pmax // 256, -(-n // 256))
     best = min(_gradh_rounds(n, d, p) for p in range(1, top + 1))
     assert _gradh_rounds(n, d, P // 256) == best
@@ -184,15 +176,14 @@ def test_step_workspace_stays_within_the_staging_budget(n, d, V, w, flags):
     if n == 131072:
         assert (P, passes) == (6400, 21)  # 21 grad_h rounds, against 38 for 27 x 256 rows
     if (n, d) == (32768, 2560):
-        assert (P, passes) == (32768, 1)  # one pass: 9.96 GB of staging, no fp32 grad_W partials
+        assert (P, passes) == (6400, 6)  # 250 grad_h tiles a pass: one round each
 
 
 @pytest.mark.parametrize("grads", ["both", "grad_h", "grad_W"])
 def test_queried_size_runs_the_default_plan_for_each_gradient_set(grads):
-    """The size the query returns for a set of gradients runs that set's plan at the default staging budget (not a
-    smaller budget's): the step and the backward, at 40,000 rows of d 2560, V 151,936 (2 GiB passes), and the step's
-    one pass at 32,768 rows."""
-    n, d, V = 40000, 2560, 151936
+    """The size the query returns for a set of gradients runs that set's plan at the 2 GiB staging budget (not a
+    smaller budget's): the step and the backward, at 32,768 rows of d 2560, V 151,936."""
+    n, d, V = 32768, 2560, 151936
     Vp = (V + 255) // 256 * 256
     flags = {"both": 0, "grad_h": _lib.WS_NO_GRADW, "grad_W": _lib.WS_NO_GRADH}[grads]
     ws = _lib.workspace_bytes(n, d, V, _lib.BF16, _lib.WS_STEP | flags)
@@ -200,14 +191,9 @@ def test_queried_size_runs_the_default_plan_for_each_gradient_set(grads):
     pmax = BUDGET // (Vp * 2) // 256 * 256
     if grads == "grad_W":  # rows balanced over the fewest passes that fit
         k = -(-n // pmax)
-        assert (P, passes) == (-(-(-(-n // k)) // 256) * 256, k) == (6912, 6)
+        assert (P, passes) == (-(-(-(-n // k)) // 256) * 256, k) == (6656, 5)
     else:  # the fewest grad_h rounds
-        assert (P, passes) == (max(p for p in range(256, pmax + 1, 256)
-                                   if _gradh_rounds(n, d, p // 256) == min(_gradh_rounds(n, d, q // 256)
-                                                                            for q in range(256, pmax + 1, 256))),
-                               -(-n // P))
-    one = _lib.workspace_bytes(32768, d, V, _lib.BF16, _lib.WS_STEP | flags)
-    assert _lib.bwd_plan(32768, d, V, _lib.BF16, _lib.WS_STEP | flags, one)[:2] == (32768, 1)
+        assert (P, passes) == (6400, 6)
     # the backward: the queried size is the least that runs its plan
     bw = _lib.workspace_bytes(n, d, V, _lib.BF16, _lib.WS_BACKWARD | flags)
     plan = _lib.bwd_plan(n, d, V, _lib.BF16, flags, bw)
