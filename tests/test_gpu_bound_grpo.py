@@ -256,3 +256,39 @@ def test_grpo_fit_through_the_c_abi():
     c, rest, cr, skip = _fit_call(src, None, torch.zeros(0, device=DEV), None)  # no rows
     assert c == 0.0 and (cr, skip) == (0, 1)
 
+
+
+@pytest.mark.parametrize("form", ["f16-softcap", "fp8-weights"])
+def test_bound_route_with_other_operand_forms(form):
+    """The bound route beyond bf16: f16 operands with the tanh soft-cap (post-head transform in the epilogue), and fp8
+    weights with row scales (grad_h only, as a frozen quantised head). The objective plus another term on the logprob
+    column, so both the held gradients and the rest's backward run; the gradients against the two-call route
+    (fused_head, the same loss, backward) to the 16-bit rounding of dz."""
+    N, d, V, T = 1800, 256, 4096, 0.9
+    dtype = torch.float16 if form == "f16-softcap" else torch.bfloat16
+    h, W, y, scored, mask, adv, noise = _batch(N, d, V, dtype, seed=13)
+    hd, yd = h.to(DEV), y.to(DEV)
+    post, sc = head_op.Post(), None
+    if form == "f16-softcap":
+        post, Wd = head_op.Post(0.5, 2.0, True), W.to(DEV)
+    else:
+        Wd, sc = head_op.quantise_fp8_rows(W.to(DEV))
+    idx, count = head_op.compact_rows(scored.to(DEV))
+    kw = dict(idx=idx, count=count, labels_via_idx=True, scatter=True, w_scale=sc)
+    with torch.no_grad():
+        old = head_op.fused_head(hd, Wd, yd, T, post, **kw)[:, 0] + noise.to(DEV)
+    grpo = head_op.GrpoInputs(adv=adv.to(DEV), old=old, prox=None, mask=mask.to(DEV))
+    need_w = form == "f16-softcap"
+    h1, W1 = hd.clone().requires_grad_(True), Wd.clone().requires_grad_(need_w)
+    out1 = head_op.grpo_bound_head(h1, W1, yd, T, grpo, post=post, idx=idx, count=count, w_scale=sc)
+    _objective(out1[:, 0], grpo, 1.0, 0.3).backward()
+    h2, W2 = hd.clone().requires_grad_(True), Wd.clone().requires_grad_(need_w)
+    out2 = head_op.fused_head(h2, W2, yd, T, post, **kw)
+    _objective(out2[:, 0], grpo, 1.0, 0.3).backward()
+    torch.cuda.synchronize()
+    assert torch.equal(out1.detach(), out2.detach())
+    assert (h1.grad[~scored.to(DEV)] == 0).all() and _rel(h1.grad, h2.grad) <= 4e-3
+    if need_w:
+        assert _rel(W1.grad, W2.grad) <= 4e-3
+    else:
+        assert W1.grad is None
