@@ -82,24 +82,28 @@ def _run(dev, dtype, tol_out, tol_grad):
     def rel(a, b):
         return ((a.double() - b.double()).norm() / b.double().norm()).item()
 
-    assert rel(head.weight.grad, gw_all) <= tol_grad
-    assert rel(h_cm.grad, gh_all) <= tol_grad
-
-    # against the fp64 oracle on the same inputs: the pair rows' columns expanded to the flat positions, and the
-    # gradients of the loss whose dL/dlogprob per pair is grad_pairs[:, 0] (the entropy column is detached), the hidden
-    # gradient folded back onto the tree rows the pairs read (chunk_major.py:339-363)
+    # each route against the fp64 oracle on the same inputs first, so that a failure names the route: the pair rows'
+    # columns expanded to the flat positions, and the gradients of the loss whose dL/dlogprob per pair is
+    # grad_pairs[:, 0] (the entropy column is detached), the hidden gradient folded back onto the tree rows the pairs
+    # read (chunk_major.py:339-363)
     rows = hidden[0].index_select(0, meta.pair_pos).cpu()
     W = old.detach().cpu()
     labels = meta.pair_label.cpu()
     lp, ent, _ = ohead.head_forward(rows, W, labels, 0.8)
     want_out = ohead.tree_output(torch.stack([lp, ent], 1), meta.flat_pair.cpu())
     tol_oracle = 1e-5 if dtype == torch.float32 else 2e-3
-    assert (out_cm[0].cpu().double() - want_out).abs().max().item() <= tol_oracle
+    assert (out_all[0].detach().cpu().double() - want_out).abs().max().item() <= tol_oracle, "whole-tree columns"
+    assert (out_cm[0].cpu().double() - want_out).abs().max().item() <= tol_oracle, "chunked columns"
     gh_pairs, gw_want = ohead.head_backward(rows, W, labels, 0.8, grad_pairs[:P, 0].cpu())
     gh_want = torch.zeros(hidden.shape[1], hidden.shape[2], dtype=torch.float64).index_add_(
         0, meta.pair_pos.cpu(), gh_pairs)
     bar = 1e-4 if dtype == torch.float32 else 1e-2
-    assert rel(h_cm.grad[0].cpu(), gh_want) <= bar and rel(head.weight.grad.cpu(), gw_want) <= bar
+    assert rel(gh_all[0].cpu(), gh_want) <= bar and rel(gw_all.cpu(), gw_want) <= bar, "whole-tree gradients"
+    assert rel(h_cm.grad[0].cpu(), gh_want) <= bar and rel(head.weight.grad.cpu(), gw_want) <= bar, \
+        "chunked gradients"
+    # then the two routes against each other, at the tighter bar of their shared arithmetic
+    assert rel(head.weight.grad, gw_all) <= tol_grad
+    assert rel(h_cm.grad, gh_all) <= tol_grad
 
 
 def test_chunk_major_head_cpu():
